@@ -1,0 +1,247 @@
+// Packed causal depthwise conv1d + SiLU with a head-split q/k/v store, gfx950.
+//
+// Replaces the reference's hand-edited Inductor pointwise kernel
+// (ref: src/decider/packed_conv_kernel.py:115-191), which reads x [B*T, C]
+// token-major and stores straight into q/k/v [B, T, H, D].
+//
+// HBM-bound, no MFMA.  A thread owns 8 contiguous channels (one 16-byte
+// vector) and a run of RUN consecutive tokens.  The causal window of the last
+// WIDTH-1 inputs stays in registers, so each input vector is loaded from HBM
+// once; only the WIDTH-1 halo rows in front of a run are read a second time
+// (from L2: the neighbouring run is mapped to the same XCD, see below).  A
+// wavefront covers 512 channels = 1 KiB contiguous per token row, for both the
+// loads and the stores.
+//
+// XCD-aware block order: the hardware deals workgroups round-robin over the 8
+// XCDs, so block b runs on XCD b % 8.  Token runs are renumbered so that each
+// XCD receives one contiguous range of runs; the halo rows a run re-reads
+// were loaded by its predecessor into the same XCD's L2.
+//
+// fp32 sequence per output (the CPU restatement reproduces it bit for bit):
+//   acc = w[W-1]*x[t]; acc = acc + w[0]*x[t-W+1]; ...; acc = acc + w[W-2]*x[t-1]
+//   (+ bias), then y = acc / (1 + exp(-acc)) for SiLU, one bf16 rounding.
+// Products of two bf16 values are exact in fp32, so this equals the
+// reference's fused multiply-add chain (ref: :139-177).
+#include "fd_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kNumXcd = 8;
+
+struct Vec8 {
+  float v[8];
+};
+
+__device__ __forceinline__ Vec8 unpack8(uint4 raw) {
+  uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  Vec8 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    r.v[2 * i] = fd_lo(w[i]);
+    r.v[2 * i + 1] = fd_hi(w[i]);
+  }
+  return r;
+}
+
+__device__ __forceinline__ uint4 load16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// Grid: 1-D, n_col * n_runs_padded blocks (a multiple of 8).  Linear block b
+// runs on XCD b % 8; logical block L = (b % 8) * (nblocks / 8) + b / 8, so the
+// logical blocks of one XCD are contiguous: all channel columns of a run, then
+// the next run.
+template <int WIDTH, int RUN, bool SILU>
+__global__ __launch_bounds__(kThreads) void packed_conv_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias,
+    uint16_t* __restrict__ q, uint16_t* __restrict__ k, uint16_t* __restrict__ v, int total_rows, int seq_len,
+    int key_dim, int value_dim, const int32_t* __restrict__ cu_seqlens, int n_seqs, int n_runs, int n_col) {
+  const int C = 2 * key_dim + value_dim;
+  const int nblocks = gridDim.x;
+  const int lin = blockIdx.x;
+  const int logical = (lin % kNumXcd) * (nblocks / kNumXcd) + lin / kNumXcd;
+  const int run = logical / n_col;
+  const int chunk = (logical % n_col) * kThreads + threadIdx.x;  // 8-channel chunk
+  if (run >= n_runs || chunk * 8 >= C) return;
+  const int c0 = chunk * 8;
+  const int r0 = run * RUN;
+
+  // Per-channel taps (tap WIDTH-1 multiplies the current token) and bias.
+  float wt[WIDTH][8];
+  if (WIDTH == 4) {
+    const uint4* wp = reinterpret_cast<const uint4*>(w + c0 * 4);  // 8 channels x 4 taps = 64 B
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      Vec8 t = unpack8(wp[i]);  // channels 2i, 2i+1, taps 0..3 each
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        wt[j][2 * i] = t.v[j];
+        wt[j][2 * i + 1] = t.v[4 + j];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+#pragma unroll
+      for (int j = 0; j < WIDTH; ++j) wt[j][e] = fd_bf16_to_f32(w[(c0 + e) * WIDTH + j]);
+    }
+  }
+  Vec8 bs;
+  const bool has_bias = bias != nullptr;
+  if (has_bias) bs = unpack8(load16(bias + c0));
+
+  // Sequence containing r0: [seg_start, seg_end).  For varlen, seg is the
+  // largest index in [0, n_seqs) with cu_seqlens[seg] <= r0.
+  int seg = 0, seg_start, seg_end;
+  if (cu_seqlens != nullptr) {
+    int lo = 0, hi = n_seqs;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (cu_seqlens[mid] <= r0) lo = mid; else hi = mid;
+    }
+    seg = lo;
+    seg_start = cu_seqlens[seg];
+    seg_end = cu_seqlens[seg + 1];
+  } else {
+    seg_start = (r0 / seq_len) * seq_len;
+    seg_end = seg_start + seq_len;
+  }
+
+  // Issue every load of the run up front: WIDTH-1 halo rows + RUN rows.
+  const int r_end = min(r0 + RUN, total_rows);
+  uint4 halo[WIDTH > 1 ? WIDTH - 1 : 1];
+  const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+  for (int j = 0; j < WIDTH - 1; ++j) {
+    const int r = r0 - (WIDTH - 1) + j;
+    halo[j] = (r >= seg_start && r >= 0) ? load16(x + static_cast<int64_t>(r) * C + c0) : zero;
+  }
+  uint4 cur[RUN];
+#pragma unroll
+  for (int i = 0; i < RUN; ++i) {
+    const int r = r0 + i;
+    cur[i] = (r < r_end) ? load16(x + static_cast<int64_t>(r) * C + c0) : zero;
+  }
+
+  uint16_t* dst;
+  int dst_stride, dst_c;
+  if (c0 < key_dim) {
+    dst = q; dst_stride = key_dim; dst_c = c0;
+  } else if (c0 < 2 * key_dim) {
+    dst = k; dst_stride = key_dim; dst_c = c0 - key_dim;
+  } else {
+    dst = v; dst_stride = value_dim; dst_c = c0 - 2 * key_dim;
+  }
+
+  Vec8 win[WIDTH > 1 ? WIDTH - 1 : 1];
+#pragma unroll
+  for (int j = 0; j < WIDTH - 1; ++j) win[j] = unpack8(halo[j]);
+
+#pragma unroll
+  for (int i = 0; i < RUN; ++i) {
+    const int r = r0 + i;
+    if (r >= r_end) break;
+    if (r >= seg_end) {  // first token of the next sequence: restart the window
+      if (cu_seqlens != nullptr) {
+        while (seg + 1 < n_seqs && cu_seqlens[seg + 1] <= r) ++seg;
+        seg_end = cu_seqlens[seg + 1];
+      } else {
+        seg_end = (r / seq_len) * seq_len + seq_len;
+      }
+#pragma unroll
+      for (int j = 0; j < WIDTH - 1; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) win[j].v[e] = 0.0f;
+    }
+    const Vec8 xc = unpack8(cur[i]);
+    uint32_t o[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      float y2[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int e = 2 * p + h;
+        float acc = wt[WIDTH - 1][e] * xc.v[e];
+#pragma unroll
+        for (int j = 0; j < WIDTH - 1; ++j) {
+          const float prod = wt[j][e] * win[j].v[e];
+          acc = acc + prod;
+        }
+        if (has_bias) acc = acc + bs.v[e];
+        y2[h] = SILU ? fd_silu(acc) : acc;
+      }
+      o[p] = fd_pack2(y2[0], y2[1]);
+    }
+    *reinterpret_cast<uint4*>(dst + static_cast<int64_t>(r) * dst_stride + dst_c) = make_uint4(o[0], o[1], o[2], o[3]);
+#pragma unroll
+    for (int j = 0; j + 1 < WIDTH - 1; ++j) win[j] = win[j + 1];
+    if (WIDTH > 1) win[WIDTH > 1 ? WIDTH - 2 : 0] = xc;
+  }
+}
+
+template <int WIDTH, int RUN>
+int launch_run(const void* x, const void* w, const void* bias, void* q, void* k, void* v, int total_rows,
+               int seq_len, int key_dim, int value_dim, const int32_t* cu, int n_seqs, int act,
+               hipStream_t stream) {
+  const int C = 2 * key_dim + value_dim;
+  const int chunks = C / 8;
+  const int n_runs = (total_rows + RUN - 1) / RUN;
+  const int n_col = (chunks + kThreads - 1) / kThreads;
+  int64_t nblocks = static_cast<int64_t>(n_col) * n_runs;
+  nblocks = (nblocks + kNumXcd - 1) / kNumXcd * kNumXcd;  // padded blocks exit at once
+  if (nblocks > 2147483647LL) return fd_set_error(FD_ERR_INVALID_ARGUMENT, "fd_packed_conv_fwd: grid too large");
+  dim3 grid(static_cast<unsigned>(nblocks)), block(kThreads);
+  auto xs = static_cast<const uint16_t*>(x);
+  auto ws = static_cast<const uint16_t*>(w);
+  auto bsp = static_cast<const uint16_t*>(bias);
+  auto qs = static_cast<uint16_t*>(q);
+  auto ks = static_cast<uint16_t*>(k);
+  auto vs = static_cast<uint16_t*>(v);
+  if (act == FD_ACT_SILU)
+    hipLaunchKernelGGL((packed_conv_kernel<WIDTH, RUN, true>), grid, block, 0, stream, xs, ws, bsp, qs, ks, vs,
+                       total_rows, seq_len, key_dim, value_dim, cu, n_seqs, n_runs, n_col);
+  else
+    hipLaunchKernelGGL((packed_conv_kernel<WIDTH, RUN, false>), grid, block, 0, stream, xs, ws, bsp, qs, ks, vs,
+                       total_rows, seq_len, key_dim, value_dim, cu, n_seqs, n_runs, n_col);
+  return fd_check_launch("fd_packed_conv_fwd");
+}
+
+constexpr int kRun = 16;
+
+}  // namespace
+
+extern "C" int fd_packed_conv_fwd(const void* x, const void* weight, const void* bias, void* q, void* k, void* v,
+                                  int batch, int seq_len, int key_dim, int value_dim, int width,
+                                  const int32_t* cu_seqlens, int n_seqs, int activation, void* stream) {
+  FD_REQUIRE(x != nullptr && weight != nullptr && q != nullptr && k != nullptr && v != nullptr,
+             FD_ERR_INVALID_ARGUMENT, "fd_packed_conv_fwd: x, weight, q, k and v must be non-null");
+  FD_REQUIRE(batch >= 0 && seq_len >= 0, FD_ERR_INVALID_ARGUMENT,
+             "fd_packed_conv_fwd: batch and seq_len must be >= 0 (got %d, %d)", batch, seq_len);
+  FD_REQUIRE(key_dim > 0 && value_dim > 0 && key_dim % 8 == 0 && value_dim % 8 == 0, FD_ERR_INVALID_ARGUMENT,
+             "fd_packed_conv_fwd: key_dim and value_dim must be positive multiples of 8 (got %d, %d)", key_dim,
+             value_dim);
+  FD_REQUIRE(width >= 1 && width <= 4, FD_ERR_UNSUPPORTED,
+             "fd_packed_conv_fwd: width must be in [1, 4] (got %d)", width);
+  FD_REQUIRE(activation == FD_ACT_NONE || activation == FD_ACT_SILU, FD_ERR_INVALID_ARGUMENT,
+             "fd_packed_conv_fwd: activation must be FD_ACT_NONE or FD_ACT_SILU (got %d)", activation);
+  const int64_t total = static_cast<int64_t>(batch) * seq_len;
+  const int64_t C = 2 * static_cast<int64_t>(key_dim) + value_dim;
+  FD_REQUIRE(total * C < (static_cast<int64_t>(1) << 40) && total < 2147483647LL && C <= 1048576,
+             FD_ERR_INVALID_ARGUMENT, "fd_packed_conv_fwd: problem too large");
+  if (cu_seqlens != nullptr) {
+    FD_REQUIRE(batch == 1, FD_ERR_INVALID_ARGUMENT,
+               "fd_packed_conv_fwd: cu_seqlens requires batch == 1 (got %d)", batch);
+    FD_REQUIRE(n_seqs >= 1, FD_ERR_INVALID_ARGUMENT, "fd_packed_conv_fwd: n_seqs must be >= 1 (got %d)", n_seqs);
+  }
+  FD_REQUIRE(fd_aligned16(x) && fd_aligned16(weight) && fd_aligned16(q) && fd_aligned16(k) && fd_aligned16(v) &&
+                 (bias == nullptr || fd_aligned16(bias)),
+             FD_ERR_ALIGNMENT, "fd_packed_conv_fwd: inputs must be aligned to 16 bytes");
+  if (total == 0) return FD_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int rows = static_cast<int>(total);
+  switch (width) {
+    case 1: return launch_run<1, kRun>(x, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, s);
+    case 2: return launch_run<2, kRun>(x, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, s);
+    case 3: return launch_run<3, kRun>(x, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, s);
+    default: return launch_run<4, kRun>(x, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, s);
+  }
+}

@@ -1,0 +1,90 @@
+"""Native GQA causal attention on the gfx950 HIP kernel ``fd_gqa_fwd``.
+
+Drop-in for the reference launcher ``native_gqa_attention(q, k, v)``
+(ref: src/decider/native_gqa_kernel.py:116-173): same logical shapes
+(Q ``[B, Hq, T, D]``, K/V ``[B, Hkv, T, D]``, any strides with a contiguous
+feature dimension), same validation messages, same output allocation (physical
+``[B, T, Hq, D]`` returned as the ``[B, Hq, T, D]`` view), launched on the
+current stream without synchronisation.
+
+Differences, all widenings: head_dim 64/128/256 (the reference accepts only
+256, ref: :132-133), an optional ``scale`` (default ``D**-0.5`` as ref: :168),
+and packed variable-length batches through ``cu_seqlens``/``max_seqlen``
+(B == 1, T = total tokens), with causal masking inside each request.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+SUPPORTED_HEAD_DIMS = (64, 128, 256)
+
+
+def native_gqa_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    scale: float | None = None,
+    cu_seqlens: torch.Tensor | None = None,
+    max_seqlen: int | None = None,
+) -> torch.Tensor:
+    # Logical shapes: Q [B, Hq, T, D], K/V [B, Hkv, T, D] (ref: :120).
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("Q, K and V must be four-dimensional")
+
+    batch, q_heads, seq_len, head_dim = q.shape
+    kv_heads = k.shape[1]
+
+    if min(batch, q_heads, kv_heads, seq_len) < 1:
+        raise ValueError("Batch, head counts and sequence length must be positive")
+    if q_heads % kv_heads:
+        raise ValueError("Query heads must be divisible by KV heads")
+    if head_dim not in SUPPORTED_HEAD_DIMS:
+        raise ValueError("This launcher supports head dimension 64, 128 or 256")
+    if k.shape != (batch, kv_heads, seq_len, head_dim) or v.shape != k.shape:
+        raise ValueError("Incompatible Q/K/V shapes")
+
+    for tensor in (q, k, v):
+        if not tensor.is_cuda or tensor.device != q.device:
+            raise ValueError("Q, K and V must share a CUDA device")
+        if tensor.dtype != torch.bfloat16:
+            raise ValueError("Q, K and V must be BF16")
+        if tensor.stride(-1) != 1:
+            raise ValueError("The feature dimension must be contiguous")
+        if tensor.data_ptr() % 16 or any(s % 8 for s in tensor.stride()[:3]):
+            raise ValueError("Q, K and V rows must be 16-byte aligned")
+
+    n_seqs = 0
+    cu_ptr = None
+    if cu_seqlens is not None:
+        if batch != 1:
+            raise ValueError("cu_seqlens requires batch size 1 (packed requests)")
+        if (cu_seqlens.ndim != 1 or cu_seqlens.dtype != torch.int32 or cu_seqlens.device != q.device
+                or cu_seqlens.numel() < 2 or not cu_seqlens.is_contiguous()):
+            raise ValueError("cu_seqlens must be a contiguous int32 vector [n_seqs + 1] on Q's device")
+        if max_seqlen is None:
+            raise ValueError("max_seqlen is required with cu_seqlens")
+        if not 0 <= int(max_seqlen) <= seq_len:
+            raise ValueError("max_seqlen must lie in [0, T]")
+        n_seqs = cu_seqlens.numel() - 1
+        cu_ptr = cu_seqlens.data_ptr()
+    else:
+        max_seqlen = seq_len
+
+    if scale is None:
+        scale = head_dim ** -0.5
+
+    with torch.cuda.device(q.device):
+        # Physical layout [B, T, Hq, D], logical layout [B, Hq, T, D] (ref: :145-151).
+        output = torch.empty(
+            (batch, seq_len, q_heads, head_dim), device=q.device, dtype=q.dtype
+        ).permute(0, 2, 1, 3)
+        lib = _lib.lib()
+        _lib.check("fd_gqa_fwd", lib.fd_gqa_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), output.data_ptr(),
+            _lib.strides4(q), _lib.strides4(k), _lib.strides4(v), _lib.strides4(output),
+            batch, q_heads, kv_heads, seq_len, head_dim, float(scale),
+            cu_ptr, n_seqs, int(max_seqlen), _lib.stream_handle(q.device)))
+    return output

@@ -1,0 +1,138 @@
+/*
+ * fd_kernels.h — C ABI of the FastDecisions MI355X (gfx950) hot-path kernels.
+ *
+ * Three forward kernels of the decider model, each a drop-in for one Python
+ * launcher of the reference:
+ *
+ *   fd_gqa_fwd          native GQA causal attention
+ *                       replaces native_gqa_attention(q, k, v)
+ *                       (ref: src/decider/native_gqa_kernel.py:116-173, kernel :6-113)
+ *   fd_packed_conv_fwd  packed causal depthwise conv1d + SiLU, head-split q/k/v store
+ *                       replaces prep_qkv(input_qkv, weight)
+ *                       (ref: src/decider/packed_conv_kernel.py:194-232, kernel :115-191)
+ *   fd_add_rmsnorm_fwd  fused residual add + RMSNorm returning both outputs
+ *                       replaces residual_rms(a, b, weight)
+ *                       (ref: src/decider/persistent_residual_rms_kernel.py:75-104, kernel :49-72;
+ *                        eps placement as ref: src/decider/residual_rms_baseline.py:75-78)
+ *
+ * Conventions shared by every entry point:
+ *   - every tensor pointer is a device pointer; bf16 tensors are passed as raw
+ *     16-bit storage (torch.bfloat16 bit layout);
+ *   - no entry point allocates, frees or synchronises: work is enqueued on
+ *     `stream` (a hipStream_t; NULL is the legacy default stream), so calls
+ *     can be captured into a HIP graph;
+ *   - the return value is FD_OK (0) or a negative FD_ERR_* code; the message
+ *     of the last failure on the calling thread is fd_last_error().
+ */
+#ifndef FD_KERNELS_H
+#define FD_KERNELS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define FD_API __attribute__((visibility("default")))
+#else
+#define FD_API
+#endif
+
+#define FD_ABI_VERSION 1
+
+#define FD_OK 0
+#define FD_ERR_INVALID_ARGUMENT (-1) /* shape, size, stride or flag out of range */
+#define FD_ERR_UNSUPPORTED (-2)      /* valid request this build does not implement */
+#define FD_ERR_ALIGNMENT (-3)        /* pointer or stride breaks the 16-byte vector contract */
+#define FD_ERR_LAUNCH (-4)           /* the HIP runtime rejected the launch */
+
+#define FD_DTYPE_BF16 0
+#define FD_DTYPE_F32 1
+
+#define FD_ACT_NONE 0
+#define FD_ACT_SILU 1
+
+/* Version of this ABI (FD_ABI_VERSION of the library that was built). */
+FD_API int fd_abi_version(void);
+
+/* Message describing the last failed call on this thread ("" if none). */
+FD_API const char* fd_last_error(void);
+
+/*
+ * Causal grouped-query attention forward, bf16 in/out, fp32 softmax.
+ *
+ * Logical layouts (strides in elements, innermost stride must be 1):
+ *   q   [batch, q_heads,  seq_len, head_dim]   q_strides   = {b, h, t, d}
+ *   k,v [batch, kv_heads, seq_len, head_dim]   k/v_strides = {b, h, t, d}
+ *   out [batch, q_heads,  seq_len, head_dim]   out_strides = {b, h, t, d}
+ * Query head h reads key/value head h / (q_heads / kv_heads), as the
+ * reference kernel does (ref: src/decider/native_gqa_kernel.py:39-41).
+ * Key j is visible to query i iff j <= i (same sequence).  P is rounded to
+ * bf16 before the P·V product (ref: src/decider/native_gqa_kernel.py:98-102).
+ *
+ * Varlen: with cu_seqlens != NULL (device int32[n_seqs + 1], non-decreasing,
+ * cu_seqlens[0] == 0, cu_seqlens[n_seqs] == seq_len), batch must be 1 and the
+ * T axis holds n_seqs packed requests; masking is causal within each request
+ * and no request sees another.  max_seqlen (host) bounds the longest request.
+ *
+ * Limits: head_dim in {64, 128, 256}; q_heads % kv_heads == 0; every base
+ * pointer and every non-unit stride keeps 16-byte alignment.
+ */
+FD_API int fd_gqa_fwd(const void* q, const void* k, const void* v, void* out,
+               const int64_t q_strides[4], const int64_t k_strides[4],
+               const int64_t v_strides[4], const int64_t out_strides[4],
+               int batch, int q_heads, int kv_heads, int seq_len, int head_dim,
+               float scale, const int32_t* cu_seqlens, int n_seqs, int max_seqlen,
+               void* stream);
+
+/*
+ * Packed causal depthwise conv1d + activation with a head-split store.
+ *
+ *   x      [batch, seq_len, C] bf16 contiguous, C = 2*key_dim + value_dim
+ *   weight [C, width] bf16 contiguous (tap `width-1` multiplies the current token)
+ *   bias   [C] bf16 or NULL
+ *   q, k   [batch, seq_len, key_dim] bf16 contiguous (any head split of key_dim)
+ *   v      [batch, seq_len, value_dim] bf16 contiguous
+ *
+ * y[t, c] = act(w[c, W-1]*x[t, c] + w[c, 0]*x[t-W+1, c] + ... + w[c, W-2]*x[t-1, c] + bias[c])
+ * evaluated in fp32 in exactly that order (the reference's order,
+ * ref: src/decider/packed_conv_kernel.py:139-177), taps before the start of
+ * the sequence read zero (ref: :128-176), SiLU = y / (1 + exp(-y)) (ref: :178-182),
+ * one bf16 rounding; channels [0, key_dim) go to q, the next key_dim to k,
+ * the rest to v (ref: :184-191).
+ *
+ * Varlen: cu_seqlens (device int32[n_seqs + 1]) with batch == 1 restarts the
+ * causal window at every request start.
+ *
+ * Limits: width in [1, 4]; key_dim, value_dim multiples of 8; all pointers
+ * 16-byte aligned (as ref: src/decider/packed_conv_kernel.py:211-212).
+ */
+FD_API int fd_packed_conv_fwd(const void* x, const void* weight, const void* bias, void* q,
+                       void* k, void* v, int batch, int seq_len, int key_dim,
+                       int value_dim, int width, const int32_t* cu_seqlens, int n_seqs,
+                       int activation, void* stream);
+
+/*
+ * Fused residual add + RMSNorm over rows of `width` features.
+ *
+ *   h            = bf16(x + residual)            (residual == NULL: h = x)
+ *   residual_out = h                             (skipped when NULL; may alias x or residual)
+ *   out          = bf16((f32(h) * rsqrt(mean(f32(h)^2) + eps)) * g),
+ *                  g = 1 + weight (gain_offset = 1, Qwen3.5 form) or weight (0)
+ *
+ * x, residual, out, residual_out: [rows, width] bf16 contiguous; weight:
+ * [width] of weight_dtype (FD_DTYPE_BF16 or FD_DTYPE_F32).  fp32 accumulation,
+ * fixed reduction order, correctly rounded sqrt and division.  out may alias x.
+ *
+ * Limits: width a multiple of 8 in [8, 8192]; pointers 16-byte aligned.
+ */
+FD_API int fd_add_rmsnorm_fwd(const void* x, const void* residual, const void* weight, void* out,
+                       void* residual_out, int64_t rows, int width, float eps,
+                       int weight_dtype, int gain_offset, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FD_KERNELS_H */

@@ -1,0 +1,174 @@
+/*
+ * TEST INFRASTRUCTURE — CPU oracle for the decider hot path.  Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this; the
+ * product never does.
+ *
+ * Plain-C restatement, in fp32 with every operation rounded where written
+ * (build with -ffp-contract=off), of:
+ *   - the packed causal depthwise conv1d + SiLU with head-split store
+ *     (ref: src/decider/packed_conv_kernel.py:128-191: tap order :139-177,
+ *      zero taps before the sequence start :128-176, SiLU :178-182,
+ *      q/k/v split :184-191);
+ *   - the fused residual add + RMSNorm (ref: src/decider/residual_rms_baseline.py:48-85
+ *     for eps placement, ref: src/decider/persistent_residual_rms_kernel.py:59-72 for
+ *     the (w + 1) gain; the residual is rounded to bf16 before it is normalised as in
+ *     transformers' Qwen3_5DecoderLayer + Qwen3_5RMSNorm).
+ * The summation order of the RMSNorm matches the GPU kernel's documented order
+ * (per-lane chunk order, then a 6-step xor butterfly over 64 lanes), so GPU
+ * output is compared bit for bit; the mathematics pins this restatement
+ * independently (tests/test_oracle.py: fp64 closed forms, torch's F.conv1d and
+ * eager RMSNorm, special cases).
+ */
+#include <math.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <string.h>
+
+static float bf16_to_f32(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+static uint32_t f32_bits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+
+static float bits_f32(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* Round-to-nearest-even fp32 -> bf16, NaN -> 0x7fc0 (torch's rule). */
+uint16_t fd_oracle_f32_to_bf16(float f) {
+  uint32_t u = f32_bits(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+/* exp(x): Cody–Waite reduction x = k ln2 + r with ln2 split into a head of 16
+ * significant bits and a tail, degree-7 Taylor polynomial of e^r in Horner
+ * form, exact scaling by 2^k (two steps into the subnormal range). */
+float fd_oracle_expf(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return bits_f32(0x7f800000u);
+  if (x < -103.972084045410156f) return 0.0f;
+  const float log2e = 1.44269502162933349609375f;
+  const float ln2_hi = 0.693145751953125f;
+  const float ln2_lo = 1.428606765330187045e-06f;
+  float k = rintf(x * log2e);
+  float r = fmaf(-k, ln2_hi, x);
+  r = fmaf(-k, ln2_lo, r);
+  float p = 1.0f / 5040.0f;
+  p = fmaf(p, r, 1.0f / 720.0f);
+  p = fmaf(p, r, 1.0f / 120.0f);
+  p = fmaf(p, r, 1.0f / 24.0f);
+  p = fmaf(p, r, 1.0f / 6.0f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  int ki = (int)k;
+  if (ki > 127) return (p * 1.7014118346046923e38f) * bits_f32((uint32_t)(ki) << 23);
+  if (ki < -126) return (p * bits_f32((uint32_t)(ki + 64 + 127) << 23)) * 5.421010862427522e-20f;
+  return p * bits_f32((uint32_t)(ki + 127) << 23);
+}
+
+float fd_oracle_silu(float y) { return y / (1.0f + fd_oracle_expf(-y)); }
+
+/* Packed causal depthwise conv1d + activation, token-major [B, T, C] input,
+ * C = 2*key_dim + value_dim, weight [C, width], optional bias [C].
+ * Returns 0, or -1 on invalid arguments. */
+int fd_oracle_packed_conv(const uint16_t* x, const uint16_t* w, const uint16_t* bias, uint16_t* q, uint16_t* k,
+                          uint16_t* v, int batch, int seq_len, int key_dim, int value_dim, int width,
+                          const int32_t* cu_seqlens, int n_seqs, int activation) {
+  if (batch < 0 || seq_len < 0 || key_dim <= 0 || value_dim <= 0 || width < 1 || width > 4) return -1;
+  const int C = 2 * key_dim + value_dim;
+  const int64_t total = (int64_t)batch * seq_len;
+  for (int64_t r = 0; r < total; ++r) {
+    /* start of the sequence that holds row r */
+    int64_t start;
+    if (cu_seqlens) {
+      int s = 0;
+      while (s + 1 < n_seqs && cu_seqlens[s + 1] <= r) ++s;
+      start = cu_seqlens[s];
+    } else {
+      start = (r / seq_len) * seq_len;
+    }
+    for (int c = 0; c < C; ++c) {
+      float wt[4];
+      for (int j = 0; j < width; ++j) wt[j] = bf16_to_f32(w[(size_t)c * width + j]);
+      float acc = wt[width - 1] * bf16_to_f32(x[(size_t)r * C + c]);
+      for (int j = 0; j < width - 1; ++j) {
+        const int64_t src = r - (width - 1) + j;
+        const float xv = src >= start ? bf16_to_f32(x[(size_t)src * C + c]) : 0.0f;
+        const float prod = wt[j] * xv;
+        acc = acc + prod;
+      }
+      if (bias) acc = acc + bf16_to_f32(bias[c]);
+      const float y = activation == 1 ? fd_oracle_silu(acc) : acc;
+      const uint16_t h = fd_oracle_f32_to_bf16(y);
+      if (c < key_dim)
+        q[(size_t)r * key_dim + c] = h;
+      else if (c < 2 * key_dim)
+        k[(size_t)r * key_dim + (c - key_dim)] = h;
+      else
+        v[(size_t)r * value_dim + (c - 2 * key_dim)] = h;
+    }
+  }
+  return 0;
+}
+
+/* Fused residual add + RMSNorm over rows of `width` (a multiple of 8, <= 8192).
+ * weight_dtype 0: bf16 weight, 1: fp32 weight.  residual / residual_out may be NULL. */
+int fd_oracle_add_rmsnorm(const uint16_t* x, const uint16_t* residual, const void* weight, uint16_t* out,
+                          uint16_t* residual_out, int64_t rows, int width, float eps, int weight_dtype,
+                          int gain_offset) {
+  if (width < 8 || width > 8192 || width % 8 || rows < 0) return -1;
+  const int nchunks = width / 8;
+  float h[8192];
+  for (int64_t row = 0; row < rows; ++row) {
+    const size_t base = (size_t)row * width;
+    for (int i = 0; i < width; ++i) {
+      if (residual) {
+        const float sum = bf16_to_f32(x[base + i]) + bf16_to_f32(residual[base + i]);
+        const uint16_t hb = fd_oracle_f32_to_bf16(sum);
+        h[i] = bf16_to_f32(hb);
+        if (residual_out) residual_out[base + i] = hb;
+      } else {
+        h[i] = bf16_to_f32(x[base + i]);
+      }
+    }
+    /* lane l owns chunks l, l+64, l+128, ... (8 features each) */
+    float lane_sum[64];
+    for (int l = 0; l < 64; ++l) {
+      float s = 0.0f;
+      for (int chunk = l; chunk < nchunks; chunk += 64) {
+        for (int e = 0; e < 8; ++e) {
+          const float hv = h[chunk * 8 + e];
+          const float sq = hv * hv;
+          s = s + sq;
+        }
+      }
+      lane_sum[l] = s;
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+      float next[64];
+      for (int l = 0; l < 64; ++l) next[l] = lane_sum[l] + lane_sum[l ^ off];
+      memcpy(lane_sum, next, sizeof(next));
+    }
+    const float mean = lane_sum[0] / (float)width;
+    const float inv = 1.0f / sqrtf(mean + eps);
+    for (int i = 0; i < width; ++i) {
+      float g = weight_dtype == 1 ? ((const float*)weight)[i] : bf16_to_f32(((const uint16_t*)weight)[i]);
+      if (gain_offset) g = 1.0f + g;
+      const float y = (h[i] * inv) * g;
+      out[base + i] = fd_oracle_f32_to_bf16(y);
+    }
+  }
+  return 0;
+}

@@ -1,0 +1,178 @@
+"""Write the golden fixtures of the decider hot path (run: python tests/golden/make_golden.py).
+
+The expected outputs come from the reference's PyTorch path on CPU — the
+operations the reference itself uses as ground truth — never from this
+repository's oracle or kernels:
+
+* conv: fp32 ``F.conv1d`` (depthwise, padding W-1, sliced to T) + SiLU, one cast
+  to bf16 (BASELINE config 2's recipe; the eager op is transformers'
+  ``causal_conv1d_fn``), and the reference test's fp64 tap loop
+  (ref: experiments/packed_conv/check_packed_output_conv.py:21-32);
+* RMSNorm: the eager decoder-layer arithmetic, ``h = residual + x`` in bf16
+  then transformers' ``Qwen3_5RMSNorm`` (its ``(1 + w)`` gain, eps inside rsqrt);
+* GQA: ``F.scaled_dot_product_attention`` (MATH backend, fp32) on K/V repeated
+  per group with a causal mask, the reference oracle
+  (ref: experiments/native_gqa/bench_native_gqa.py:46-48), per request for varlen;
+* readout: brute-force argmax over the allowed letters.
+
+bf16 arrays are stored as uint16 bit patterns.  Each fixture is small (< 1 MB).
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+HERE = Path(__file__).resolve().parent
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16).copy()
+
+
+def conv_ref_fp32(x: torch.Tensor, w: torch.Tensor, bias=None, segments=None) -> torch.Tensor:
+    """fp32 depthwise causal conv1d + SiLU, then one bf16 cast. x [B,T,C] bf16, w [C,W] bf16."""
+    B, T, C = x.shape
+    W = w.shape[1]
+
+    def one(xs):
+        y = F.conv1d(xs.float().transpose(1, 2), w.float()[:, None, :], None if bias is None else bias.float(),
+                     padding=W - 1, groups=C)[..., :xs.shape[1]]
+        return F.silu(y).transpose(1, 2).to(torch.bfloat16)
+
+    if segments is None:
+        return one(x)
+    return torch.cat([one(x[:, a:b]) for a, b in segments if b > a], dim=1)
+
+
+def conv_ref_fp64(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """The reference test's fp64 tap loop (ref: experiments/packed_conv/check_packed_output_conv.py:21-32)."""
+    T = x.shape[1]
+    W = w.shape[1]
+    wd = w.double()
+    xf = x.double()
+    acc = torch.zeros_like(xf)
+    for tap in range(W):
+        lag = W - 1 - tap
+        acc[:, lag:, :] += xf[:, :T - lag, :] * wd[:, tap]
+    return (acc * torch.sigmoid(acc)).to(torch.bfloat16)
+
+
+def rms_eager(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float):
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5RMSNorm
+    h = residual + x  # bf16 add, as Qwen3_5DecoderLayer
+    norm = Qwen3_5RMSNorm(x.shape[-1], eps=eps)
+    with torch.no_grad():
+        norm.weight.data = weight.clone()
+        return norm(h), h
+
+
+def sdpa_ref(q, k, v, cu=None):
+    """fp32 MATH SDPA with repeated KV and causal mask; q [B,Hq,T,D], k/v [B,Hkv,T,D]."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    group = q.shape[1] // k.shape[1]
+    kr = k.repeat_interleave(group, dim=1)
+    vr = v.repeat_interleave(group, dim=1)
+    with sdpa_kernel(SDPBackend.MATH):
+        if cu is None:
+            return F.scaled_dot_product_attention(q.float(), kr.float(), vr.float(), is_causal=True)
+        out = torch.zeros(q.shape, dtype=torch.float32)
+        for a, b in zip(cu[:-1], cu[1:]):
+            if b > a:
+                out[:, :, a:b] = F.scaled_dot_product_attention(q[:, :, a:b].float(), kr[:, :, a:b].float(),
+                                                                vr[:, :, a:b].float(), is_causal=True)
+        return out
+
+
+def make_conv(g: torch.Generator) -> dict:
+    out = {}
+    # padded batch: B=2, T=40, key_dim=value_dim=16 (C=48), W=4
+    x = (torch.randn((2, 40, 48), generator=g)).to(torch.bfloat16)
+    w = (torch.randn((48, 4), generator=g) * 0.25).to(torch.bfloat16)
+    out.update(batch_x=bits(x), batch_w=bits(w), batch_y_fp32=bits(conv_ref_fp32(x, w)),
+               batch_y_fp64=bits(conv_ref_fp64(x, w)))
+    # with bias
+    bias = (torch.randn((48,), generator=g) * 0.1).to(torch.bfloat16)
+    out.update(bias_b=bits(bias), bias_y_fp32=bits(conv_ref_fp32(x, w, bias)))
+    # varlen: one packed row of 50 tokens, requests [0,7), [7,7) (empty), [7,30), [30,50)
+    xv = torch.randn((1, 50, 48), generator=g).to(torch.bfloat16)
+    cu = [0, 7, 7, 30, 50]
+    out.update(var_x=bits(xv), var_cu=np.array(cu, np.int32),
+               var_y_fp32=bits(conv_ref_fp32(xv, w, segments=list(zip(cu[:-1], cu[1:])))))
+    # decider-shaped channel split on a short sequence: C = 6144, T = 8
+    xd = torch.randn((1, 8, 6144), generator=g).to(torch.bfloat16)
+    wd = (torch.randn((6144, 4), generator=g) * 0.25).to(torch.bfloat16)
+    out.update(dec_x=bits(xd), dec_w=bits(wd), dec_y_fp32=bits(conv_ref_fp32(xd, wd)))
+    return out
+
+
+def make_rms(g: torch.Generator) -> dict:
+    out = {}
+    x = torch.randn((3, 5, 256), generator=g).to(torch.bfloat16)
+    r = torch.randn((3, 5, 256), generator=g).to(torch.bfloat16)
+    w = (torch.randn((256,), generator=g) * 0.02).to(torch.bfloat16)
+    y, h = rms_eager(x, r, w, 1e-6)
+    out.update(small_x=bits(x), small_r=bits(r), small_w=bits(w), small_y=bits(y), small_h=bits(h))
+    # decider width 2048, fp32 weight
+    x2 = torch.randn((6, 2048), generator=g).to(torch.bfloat16)
+    r2 = (torch.randn((6, 2048), generator=g) * 4).to(torch.bfloat16)
+    w2 = torch.randn((2048,), generator=g) * 0.02
+    y2, h2 = rms_eager(x2, r2, w2.to(torch.bfloat16), 1e-6)
+    out.update(wide_x=bits(x2), wide_r=bits(r2), wide_w_bf16=bits(w2.to(torch.bfloat16)),
+               wide_y=bits(y2), wide_h=bits(h2))
+    # fp32 weight variant of the same rows (module weight kept in fp32)
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5RMSNorm
+    norm = Qwen3_5RMSNorm(2048, eps=1e-6)
+    with torch.no_grad():
+        norm.weight.data = w2.clone()
+        y3 = norm(h2)
+    out.update(wide_w_f32=w2.numpy().astype(np.float32), wide_y_f32w=bits(y3))
+    return out
+
+
+def make_gqa(g: torch.Generator) -> dict:
+    out = {}
+    # config-1 recipe at a small size: fp32, N(0,1)/sqrt(D), drawn in order q, k, v
+    D = 64
+    q = torch.randn((1, 4, 48, D), generator=g) / D ** 0.5
+    k = torch.randn((1, 2, 48, D), generator=g) / D ** 0.5
+    v = torch.randn((1, 2, 48, D), generator=g) / D ** 0.5
+    out.update(f32_q=q.numpy(), f32_k=k.numpy(), f32_v=v.numpy(), f32_o=sdpa_ref(q, k, v).numpy())
+    # bf16 inputs (unscaled N(0,1) as ref: experiments/native_gqa/bench_native_gqa.py:43-45), D = 128
+    D = 128
+    qb = torch.randn((2, 4, 70, D), generator=g).to(torch.bfloat16)
+    kb = torch.randn((2, 2, 70, D), generator=g).to(torch.bfloat16)
+    vb = torch.randn((2, 2, 70, D), generator=g).to(torch.bfloat16)
+    out.update(bf16_q=bits(qb), bf16_k=bits(kb), bf16_v=bits(vb), bf16_o=sdpa_ref(qb, kb, vb).numpy())
+    # varlen bf16: 4 requests packed on T = 90 (one empty), 4 q / 1 kv heads, D = 64
+    D = 64
+    cu = [0, 13, 13, 64, 90]
+    qv = torch.randn((1, 4, 90, D), generator=g).to(torch.bfloat16)
+    kv = torch.randn((1, 1, 90, D), generator=g).to(torch.bfloat16)
+    vv = torch.randn((1, 1, 90, D), generator=g).to(torch.bfloat16)
+    out.update(var_q=bits(qv), var_k=bits(kv), var_v=bits(vv), var_cu=np.array(cu, np.int32),
+               var_o=sdpa_ref(qv, kv, vv, cu).numpy())
+    return out
+
+
+def make_readout(g: torch.Generator) -> dict:
+    logits = torch.randn((64, 10), generator=g, dtype=torch.float64)
+    nopts = torch.randint(2, 11, (64,), generator=g)
+    choice = np.array([int(np.argmax(row[:n])) for row, n in zip(logits.numpy(), nopts.numpy())])
+    return dict(logits=logits.numpy(), nopts=nopts.numpy(), choice=choice)
+
+
+def main() -> None:
+    torch.manual_seed(0)
+    for name, fn in (("conv", make_conv), ("rmsnorm", make_rms), ("gqa", make_gqa), ("readout", make_readout)):
+        g = torch.Generator().manual_seed(20260101)
+        data = fn(g)
+        path = HERE / f"{name}.npz"
+        np.savez_compressed(path, **data)
+        print(f"wrote {path} ({path.stat().st_size} bytes)")
+
+
+if __name__ == "__main__":
+    main()

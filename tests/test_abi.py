@@ -1,0 +1,128 @@
+"""CPU tests of the C-ABI boundary: the library loads, exports exactly what
+include/fd_kernels.h declares, and rejects bad arguments before touching a GPU."""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "fd_kernels.h"
+
+
+def declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"FD_API\s+[\w\s\*]+?\b(fd_\w+)\s*\(", text))
+
+
+def test_header_declares_the_expected_entry_points():
+    assert declared_functions() == {"fd_abi_version", "fd_last_error", "fd_gqa_fwd", "fd_packed_conv_fwd",
+                                    "fd_add_rmsnorm_fwd"}
+
+
+def test_library_exports_every_declared_symbol_and_nothing_else():
+    from fastdecisions_amd import _lib
+    lib = _lib.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert exported == declared_functions()
+    assert set(_lib.SIGNATURES) == declared_functions()
+
+
+def test_abi_version_matches_header():
+    from fastdecisions_amd import _lib
+    version = int(re.search(r"#define FD_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    assert _lib.lib().fd_abi_version() == version
+
+
+def test_the_library_uses_torch_s_hip_runtime():
+    from fastdecisions_amd import _lib
+    _lib.lib()
+    maps = [line.split()[-1] for line in open("/proc/self/maps") if "libamdhip64" in line]
+    assert maps and all("torch" in path for path in maps), set(maps)
+
+
+def _err(lib):
+    return lib.fd_last_error().decode()
+
+
+def test_rmsnorm_argument_errors():
+    from fastdecisions_amd import _lib
+    lib = _lib.lib()
+    fake = 1 << 20  # 16-byte aligned, never dereferenced: validation fails first
+    assert lib.fd_add_rmsnorm_fwd(fake, fake, fake, fake, None, 4, 7, 1e-6, 0, 1, None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert "width" in _err(lib)
+    assert lib.fd_add_rmsnorm_fwd(fake, fake, fake, fake, None, 4, 2048, 1e-6, 5, 1, None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert lib.fd_add_rmsnorm_fwd(fake + 2, fake, fake, fake, None, 4, 2048, 1e-6, 0, 1, None) == _lib.FD_ERR_ALIGNMENT
+    assert lib.fd_add_rmsnorm_fwd(None, fake, fake, fake, None, 4, 2048, 1e-6, 0, 1, None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert lib.fd_add_rmsnorm_fwd(fake, fake, fake, fake, fake, 4, 2048, -1.0, 0, 1, None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert lib.fd_add_rmsnorm_fwd(fake, fake, fake, fake, fake, 4, 2048, 1e-6, 0, 1, None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert "distinct" in _err(lib)
+    # zero rows is a valid no-op that never launches
+    assert lib.fd_add_rmsnorm_fwd(fake, fake, fake, fake, None, 0, 2048, 1e-6, 0, 1, None) == _lib.FD_OK
+
+
+def test_conv_argument_errors():
+    from fastdecisions_amd import _lib
+    lib = _lib.lib()
+    f = 1 << 20
+    call = lambda **kw: lib.fd_packed_conv_fwd(
+        kw.get("x", f), f, None, f, f, f, kw.get("B", 1), kw.get("T", 16), kw.get("kd", 2048), kw.get("vd", 2048),
+        kw.get("W", 4), kw.get("cu"), kw.get("n", 0), kw.get("act", 1), None)
+    assert call(W=5) == _lib.FD_ERR_UNSUPPORTED
+    assert call(kd=12) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert call(act=7) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert call(x=f + 8) == _lib.FD_ERR_ALIGNMENT
+    assert call(B=2, cu=f, n=1) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert "batch == 1" in _err(lib)
+    assert call(B=0) == _lib.FD_OK  # empty batch: nothing to launch
+
+
+def test_gqa_argument_errors():
+    from fastdecisions_amd import _lib
+    lib = _lib.lib()
+    f = 1 << 20
+    good = (ctypes.c_int64 * 4)(16 * 2048 * 128, 2048 * 128, 128, 1)
+    bad_inner = (ctypes.c_int64 * 4)(16 * 2048 * 128, 2048 * 128, 128, 2)
+    bad_row = (ctypes.c_int64 * 4)(16 * 2048 * 128, 2048 * 128, 100, 1)
+
+    def call(qs=good, Hq=16, Hkv=4, D=128, q=f, cu=None, n=0, mx=0, B=1, T=2048):
+        return lib.fd_gqa_fwd(q, f, f, f, qs, good, good, good, B, Hq, Hkv, T, D, 0.088, cu, n, mx, None)
+
+    assert call(D=96) == _lib.FD_ERR_UNSUPPORTED
+    assert call(Hq=15) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert call(qs=bad_inner) == _lib.FD_ERR_ALIGNMENT
+    assert call(qs=bad_row) == _lib.FD_ERR_ALIGNMENT
+    assert call(q=f + 4) == _lib.FD_ERR_ALIGNMENT
+    assert call(cu=f, n=2, mx=4096, T=2048) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert call(B=2, cu=f, n=2, mx=10) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert call(T=0) == _lib.FD_OK
+
+
+def test_python_wrappers_keep_the_reference_errors_on_cpu_tensors():
+    from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
+    from fastdecisions_amd.packed_conv_kernel import prep_qkv
+    from fastdecisions_amd.persistent_residual_rms_kernel import residual_rms
+    with pytest.raises(ValueError, match="input_qkv must be on CUDA"):
+        prep_qkv(torch.zeros((1, 2048, 6144), dtype=torch.bfloat16), torch.zeros((6144, 4), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="Q, K and V must share a CUDA device"):
+        native_gqa_attention(*(torch.zeros((1, 4, 8, 128), dtype=torch.bfloat16),) * 3)
+    with pytest.raises(ValueError, match="All tensors must share a CUDA device"):
+        residual_rms(*(torch.zeros((2, 2048), dtype=torch.bfloat16),) * 2, torch.zeros(2048))
+    with pytest.raises(ValueError, match="Incompatible Q/K/V shapes"):
+        native_gqa_attention(torch.zeros((1, 4, 8, 128)), torch.zeros((1, 2, 9, 128)), torch.zeros((1, 2, 9, 128)))
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    from fastdecisions_amd import _lib
+    monkeypatch.setattr(_lib, "_LIB", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
+    with pytest.raises(RuntimeError, match="HIP kernel library not found"):
+        _lib.lib()

@@ -1,0 +1,183 @@
+"""GPU parity of the native GQA causal attention kernel (fd_gqa_fwd).
+
+Bar (north_star): max abs error <= 2e-2 vs fp32 SDPA on the same bf16 inputs
+(the reference's oracle, ref: experiments/native_gqa/bench_native_gqa.py:46-61);
+exact identities where the mathematics fixes the answer (row 0 = V[0],
+constant V); varlen equal to per-request attention.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
+
+from helpers import announce, from_bits, seeded
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-2
+
+
+def sdpa_fp32(q, k, v):
+    """fp32 MATH SDPA with repeated KV heads and a causal mask (q [B,Hq,T,D])."""
+    group = q.shape[1] // k.shape[1]
+    with sdpa_kernel(SDPBackend.MATH):
+        return F.scaled_dot_product_attention(q.float(), k.float().repeat_interleave(group, 1),
+                                              v.float().repeat_interleave(group, 1), is_causal=True)
+
+
+def model_layout(B, Hq, Hkv, T, D, seed, scale=1.0):
+    """Q and V as permuted views of token-major [B, T, H, D] (as the decider feeds them), K head-major."""
+    q = seeded((B, T, Hq, D), seed, scale).cuda().permute(0, 2, 1, 3)
+    k = seeded((B, Hkv, T, D), seed + 1, scale).cuda()
+    v = seeded((B, T, Hkv, D), seed + 2, scale).cuda().permute(0, 2, 1, 3)
+    return q, k, v
+
+
+def test_golden_fixtures(golden, oracle):
+    from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
+    d = golden("gqa")
+    announce("gqa golden bf16 B=2 Hq=4 Hkv=2 T=70 D=128")
+    o = native_gqa_attention(from_bits(d["bf16_q"]), from_bits(d["bf16_k"]), from_bits(d["bf16_v"]))
+    torch.cuda.synchronize()
+    assert (o.float().cpu().numpy() - d["bf16_o"]).__abs__().max() <= ATOL
+    announce("gqa golden varlen")
+    cu = torch.from_numpy(d["var_cu"]).cuda()
+    o = native_gqa_attention(from_bits(d["var_q"]), from_bits(d["var_k"]), from_bits(d["var_v"]),
+                             cu_seqlens=cu, max_seqlen=int(np.diff(d["var_cu"]).max()))
+    torch.cuda.synchronize()
+    assert np.abs(o.float().cpu().numpy() - d["var_o"]).max() <= ATOL
+    announce("gqa golden fp32 recipe (inputs cast to bf16)")
+    f = lambda a: torch.from_numpy(a).to(torch.bfloat16).cuda()
+    qb, kb, vb = f(d["f32_q"]), f(d["f32_k"]), f(d["f32_v"])
+    o = native_gqa_attention(qb, kb, vb)
+    want = oracle.gqa_attention(qb.float().cpu().numpy(), kb.float().cpu().numpy(), vb.float().cpu().numpy())
+    assert np.abs(o.float().cpu().numpy() - want).max() <= ATOL
+
+
+@pytest.mark.parametrize("recipe", ["config1_scaled", "reference_bench_unscaled"])
+def test_decider_shape_T2048(recipe, oracle):
+    """B=1, T=2048, 16 q / 4 kv heads, D=128 bf16 (the BASELINE GQA kernel config)."""
+    from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
+    scale = 128 ** -0.5 if recipe == "config1_scaled" else 1.0
+    announce(f"gqa decider shape {recipe}")
+    q, k, v = model_layout(1, 16, 4, 2048, 128, 700, scale)
+    o = native_gqa_attention(q, k, v)
+    ref = sdpa_fp32(q, k, v)
+    torch.cuda.synchronize()
+    assert o.shape == (1, 16, 2048, 128) and o.stride() == (2048 * 16 * 128, 128, 16 * 128, 1)
+    err = (o.float() - ref).abs().max().item()
+    print(f"gqa {recipe}: max abs err vs fp32 SDPA = {err:.3e}")
+    assert err <= ATOL
+    # fp64 oracle on two heads (first and last of different KV groups)
+    for h in (0, 15):
+        want = oracle.gqa_attention(q[:, h:h + 1].float().cpu().numpy(), k[:, h // 4:h // 4 + 1].float().cpu().numpy(),
+                                    v[:, h // 4:h // 4 + 1].float().cpu().numpy())
+        assert np.abs(o[:, h:h + 1].float().cpu().numpy() - want).max() <= ATOL
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,T,D", [
+    (1, 8, 2, 2048, 256),   # real decider-2b attention shape
+    (2, 8, 2, 333, 256),
+    (2, 16, 4, 1000, 128),
+    (1, 4, 4, 257, 128),    # MHA (group 1)
+    (3, 6, 3, 129, 64),     # group 2
+    (1, 16, 2, 190, 64),    # group 8
+    (1, 4, 1, 1, 128),      # single token
+    (2, 12, 4, 95, 128),    # group 3
+])
+def test_shapes_groups_and_head_dims(B, Hq, Hkv, T, D):
+    from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
+    announce(f"gqa B={B} Hq={Hq} Hkv={Hkv} T={T} D={D}")
+    q, k, v = model_layout(B, Hq, Hkv, T, D, 800 + T + D)
+    o = native_gqa_attention(q, k, v)
+    ref = sdpa_fp32(q, k, v)
+    torch.cuda.synchronize()
+    err = (o.float() - ref).abs().max().item()
+    assert err <= ATOL, err
+
+
+def test_exact_identities():
+    from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
+    announce("gqa identities")
+    q, k, v = model_layout(1, 16, 4, 300, 128, 900)
+    o = native_gqa_attention(q, k, v)
+    torch.cuda.synchronize()
+    # query 0 sees key 0 only: output row 0 is V[0] exactly
+    assert torch.equal(o[:, :, 0], v[:, torch.arange(16, device="cuda") // 4, 0])
+    # constant V gives that constant, up to the bf16 rounding of P in the P·V product
+    # (the denominator sums the unrounded P, as ref: src/decider/native_gqa_kernel.py:98-103)
+    vc = torch.full_like(v, 0.6875)
+    oc = native_gqa_attention(q, k, vc)
+    torch.cuda.synchronize()
+    assert (oc.float() - 0.6875).abs().max().item() <= 0.6875 * 2.0 ** -7
+    # permuting query heads within KV groups permutes the output heads
+    perm = torch.tensor([3, 1, 2, 0, 4, 5, 6, 7, 11, 10, 9, 8, 12, 14, 13, 15], device="cuda")
+    op = native_gqa_attention(q[:, perm], k, v)
+    torch.cuda.synchronize()
+    assert torch.equal(op, o[:, perm])
+
+
+def test_varlen_equals_per_request():
+    """BASELINE config 5 style: 4 requests, lengths log-uniform in [256, 8192], packed with cu_seqlens."""
+    from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
+    rng = np.random.default_rng(11)
+    lengths = [int(round(np.exp(rng.uniform(np.log(256), np.log(8192))))) for _ in range(4)]
+    lengths = lengths[:2] + [0, 5] + lengths[2:]
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    T = int(cu[-1])
+    announce(f"gqa varlen lengths={lengths} T={T}")
+    q, k, v = model_layout(1, 16, 4, T, 128, 1000)
+    o = native_gqa_attention(q, k, v, cu_seqlens=torch.from_numpy(cu).cuda(), max_seqlen=max(lengths))
+    torch.cuda.synchronize()
+    for a, b in zip(cu[:-1], cu[1:]):
+        if b == a:
+            continue
+        alone = native_gqa_attention(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b])
+        ref = sdpa_fp32(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b])
+        torch.cuda.synchronize()
+        assert torch.equal(o[:, :, a:b], alone)  # same tiles relative to the request start
+        assert (o[:, :, a:b].float() - ref).abs().max().item() <= ATOL
+
+
+def test_graph_replay_with_changed_input():
+    from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
+    announce("gqa graph replay")
+    q, k, v = model_layout(1, 16, 4, 512, 128, 1100)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            native_gqa_attention(q, k, v)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = native_gqa_attention(q, k, v)
+    for seed in (1101, 1102):
+        k.copy_(seeded(tuple(k.shape), seed).cuda())
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = native_gqa_attention(q, k, v)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
+def test_wrapper_rejects_bad_inputs():
+    from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
+    q = torch.zeros((1, 4, 16, 128), dtype=torch.bfloat16, device="cuda")
+    k = torch.zeros((1, 2, 16, 128), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="four-dimensional"):
+        native_gqa_attention(q[0], k, k)
+    with pytest.raises(ValueError, match="divisible"):
+        native_gqa_attention(q[:, :3], k, k)
+    with pytest.raises(ValueError, match="head dimension"):
+        native_gqa_attention(q[..., :96], k[..., :96], k[..., :96])
+    with pytest.raises(ValueError, match="BF16"):
+        native_gqa_attention(q.float(), k.float(), k.float())
+    qt = torch.zeros((1, 4, 128, 16), dtype=torch.bfloat16, device="cuda").transpose(2, 3)
+    kt = torch.zeros((1, 2, 128, 16), dtype=torch.bfloat16, device="cuda").transpose(2, 3)
+    with pytest.raises(ValueError, match="contiguous"):
+        native_gqa_attention(qt, kt, kt)

@@ -1,0 +1,266 @@
+"""CPU tests that pin the oracle before it is trusted as the checker of the HIP kernels.
+
+Each oracle function is checked against (a) the golden fixtures produced by the
+reference's PyTorch path (tests/golden/make_golden.py), (b) closed forms and
+brute force in fp64, and (c) special cases — chosen so that a plausible slip
+(a dropped or reordered tap, a wrong sign, eps outside the rsqrt, an unrounded
+residual, a wrong KV-head mapping, a leak across requests) fails at least one
+of them; the ``planted`` tests show that it does.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+
+def concat_qkv(q, k, v):
+    return np.concatenate([q, k, v], axis=-1)
+
+
+# ------------------------------------------------------------------ exp / SiLU
+
+def test_expf_accuracy_over_full_range(oracle):
+    xs = np.concatenate([np.linspace(-103.9, 88.7, 40001), np.linspace(-1, 1, 2001)]).astype(np.float32)
+    got = np.array([oracle.expf(float(x)) for x in xs], np.float64)
+    ref = np.exp(xs.astype(np.float64))
+    normal = (ref > 1.2e-38) & (ref < 3.4e38)
+    ulp = np.abs(got[normal] - ref[normal]) / (np.spacing(ref[normal].astype(np.float32)).astype(np.float64))
+    assert ulp.max() < 2.0, ulp.max()
+
+
+def test_expf_special_values(oracle):
+    assert oracle.expf(0.0) == 1.0
+    assert oracle.expf(float("inf")) == float("inf")
+    assert oracle.expf(float("-inf")) == 0.0
+    assert np.isnan(oracle.expf(float("nan")))
+    assert oracle.expf(89.0) == float("inf")
+    assert oracle.expf(-110.0) == 0.0
+    # subnormal results are rounded once: within 1 subnormal ulp of the truth
+    for x in (-90.0, -100.0, -103.0):
+        assert abs(oracle.expf(x) - np.exp(x)) <= 2.0 ** -149
+
+
+# ------------------------------------------------------------------ packed conv
+
+@pytest.mark.parametrize("case,expected", [("batch", "batch_y_fp32"), ("batch", "batch_y_fp64")])
+def test_conv_matches_golden(oracle, golden, case, expected):
+    d = golden("conv")
+    got = concat_qkv(*oracle.packed_conv(d[f"{case}_x"], d[f"{case}_w"]))
+    assert np.array_equal(got, d[expected])
+
+
+def test_conv_bias_and_decider_split_match_golden(oracle, golden):
+    d = golden("conv")
+    got = concat_qkv(*oracle.packed_conv(d["batch_x"], d["batch_w"], d["bias_b"]))
+    assert np.array_equal(got, d["bias_y_fp32"])
+    q, k, v = oracle.packed_conv(d["dec_x"], d["dec_w"])
+    assert q.shape == (1, 8, 2048) and v.shape == (1, 8, 2048)
+    assert np.array_equal(concat_qkv(q, k, v), d["dec_y_fp32"])
+
+
+def test_conv_varlen_matches_golden(oracle, golden):
+    d = golden("conv")
+    got = concat_qkv(*oracle.packed_conv(d["var_x"], d["batch_w"], cu_seqlens=d["var_cu"]))
+    assert np.array_equal(got, d["var_y_fp32"])
+
+
+def test_conv_vs_fp64_and_torch_at_decider_size(oracle):
+    """Config-2 recipe (x ~ N(0,1), w ~ 0.25 N(0,1), bf16) on a T=256 slice."""
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn((1, 256, 6144), generator=g).to(torch.bfloat16)
+    w = (torch.randn((6144, 4), generator=g) * 0.25).to(torch.bfloat16)
+    xb = x.view(torch.int16).numpy().view(np.uint16)
+    wb = w.view(torch.int16).numpy().view(np.uint16)
+    got = concat_qkv(*oracle.packed_conv(xb, wb))
+    exact = oracle.packed_conv_f64(xb, wb)
+    ref = F.silu(F.conv1d(x.float().transpose(1, 2), w.float()[:, None], padding=3, groups=6144)[..., :256])
+    ref = ref.transpose(1, 2).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    for other in (exact, ref):
+        # <= 1 bf16 ulp, except where the conv cancels to ~0 and a 1-ulp fp32 difference of
+        # the tap sum is many ulps of a tiny result (then the absolute error is < 2^-20)
+        diff = np.abs(got.astype(np.int32) - other.astype(np.int32))
+        tiny = np.abs(oracle.bf16_to_f32(got) - oracle.bf16_to_f32(other)) < 2.0 ** -20
+        assert ((diff <= 1) | tiny).all()
+        assert (diff != 0).mean() < 1e-4
+
+
+def test_conv_reference_unit_cases(oracle):
+    """The reference's own conv unit cases (ref: experiments/packed_conv/check_packed_output_conv.py:59-77),
+    at the decider channel count with T shortened to 16."""
+    T = 16
+    x = np.zeros((2, T, 6144), np.float32)
+    for b in range(2):
+        for region in range(3):
+            x[b, :, region * 2048:(region + 1) * 2048] = (b * 3 + region + 1) / 8
+    x[0, -3:, :] = 3  # must never reach batch 1
+    xb = oracle.f32_to_bf16(x)
+    for tap in range(4):
+        w = np.zeros((6144, 4), np.float32)
+        w[:, tap] = 1
+        wb = oracle.f32_to_bf16(w)
+        got = concat_qkv(*oracle.packed_conv(xb, wb))
+        # one-hot tap `tap` copies x[t - (3 - tap)] (zero before the start), then SiLU
+        lag = 3 - tap
+        src = np.zeros_like(x)
+        src[:, lag:] = x[:, :T - lag] if lag else x
+        want = oracle._f64_to_bf16(src / (1 + np.exp(-src.astype(np.float64))))
+        assert np.array_equal(got, want), tap
+        assert not np.any(oracle.bf16_to_f32(got[1]) > 1.0)  # the 3s of batch 0 never leak
+    zero = oracle.packed_conv(np.zeros((1, 8, 6144), np.uint16), oracle.f32_to_bf16(np.random.randn(6144, 4)))
+    assert all((oracle.bf16_to_f32(t) == 0).all() for t in zero)  # +0 or -0, as count_nonzero
+
+
+def test_conv_varlen_equals_per_request(oracle):
+    rng = np.random.default_rng(3)
+    x = oracle.f32_to_bf16(rng.standard_normal((1, 61, 24)).astype(np.float32))
+    w = oracle.f32_to_bf16((0.25 * rng.standard_normal((24, 4))).astype(np.float32))
+    cu = np.array([0, 1, 20, 20, 61], np.int32)
+    got = concat_qkv(*oracle.packed_conv(x, w, cu_seqlens=cu))
+    for a, b in zip(cu[:-1], cu[1:]):
+        if b > a:
+            alone = concat_qkv(*oracle.packed_conv(x[:, a:b], w))
+            assert np.array_equal(got[:, a:b], alone)
+
+
+def test_planted_conv_slips_fail_the_golden(oracle, golden):
+    d = golden("conv")
+    x, w, want = d["batch_x"], d["batch_w"], d["batch_y_fp32"]
+    # reversed taps
+    assert not np.array_equal(concat_qkv(*oracle.packed_conv(x, w[:, ::-1].copy())), want)
+    # dropped term (tap 0 zeroed)
+    w0 = w.copy()
+    w0[:, 0] = 0
+    assert not np.array_equal(concat_qkv(*oracle.packed_conv(x, w0)), want)
+    # wrong sign inside SiLU: silu(-y) != silu(y)
+    neg = oracle.f32_to_bf16(-oracle.bf16_to_f32(w))
+    assert not np.array_equal(concat_qkv(*oracle.packed_conv(x, neg)), want)
+    # batch boundary ignored: treat the two batches as one sequence
+    joined = concat_qkv(*oracle.packed_conv(x.reshape(1, -1, x.shape[-1]), w)).reshape(want.shape)
+    assert not np.array_equal(joined, want)
+
+
+# ------------------------------------------------------------------ RMSNorm
+
+@pytest.mark.parametrize("case,wkey,ykey", [("small", "small_w", "small_y"), ("wide", "wide_w_bf16", "wide_y"),
+                                            ("wide", "wide_w_f32", "wide_y_f32w")])
+def test_rmsnorm_matches_eager_golden(oracle, golden, case, wkey, ykey):
+    d = golden("rmsnorm")
+    out, res = oracle.add_rmsnorm(d[f"{case}_x"], d[f"{case}_r"], d[wkey])
+    assert np.array_equal(res, d[f"{case}_h"])  # updated residual: bit-exact
+    diff = np.abs(out.astype(np.int32) - d[ykey].astype(np.int32))
+    assert diff.max() <= 1  # normed: <= 1 bf16 ulp of eager (observed: equal)
+
+
+def test_rmsnorm_vs_fp64_closed_form(oracle):
+    rng = np.random.default_rng(0)
+    x = oracle.f32_to_bf16(rng.standard_normal((64, 2048)).astype(np.float32))
+    r = oracle.f32_to_bf16(rng.standard_normal((64, 2048)).astype(np.float32))
+    w = oracle.f32_to_bf16((0.02 * rng.standard_normal(2048)).astype(np.float32))
+    out, _ = oracle.add_rmsnorm(x, r, w)
+    exact = oracle.add_rmsnorm_f64(x, r, w)
+    diff = np.abs(out.astype(np.int32) - exact.astype(np.int32))
+    assert diff.max() <= 1 and (diff != 0).mean() < 5e-3
+
+
+def test_rmsnorm_special_cases(oracle):
+    rng = np.random.default_rng(1)
+    x = oracle.f32_to_bf16(rng.standard_normal((8, 512)).astype(np.float32))
+    zero_w = np.zeros(512, np.uint16)
+    out, _ = oracle.add_rmsnorm(x, None, zero_w)  # gain 1 + 0: unit-rms rows
+    y = oracle.bf16_to_f32(out).astype(np.float64)
+    assert np.allclose(np.sqrt((y * y).mean(axis=1)), 1.0, atol=4e-3)
+    # scale invariance: norm(4x) == norm(x) bit for bit (power-of-two scale is exact)
+    x4 = oracle.f32_to_bf16(4 * oracle.bf16_to_f32(x))
+    assert np.array_equal(oracle.add_rmsnorm(x4, None, zero_w, eps=0.0)[0], oracle.add_rmsnorm(x, None, zero_w, eps=0.0)[0])
+    # plain-gain form (gain_offset=False) with w = 1 equals the offset form with w = 0
+    one_w = oracle.f32_to_bf16(np.ones(512, np.float32))
+    assert np.array_equal(oracle.add_rmsnorm(x, None, one_w, gain_offset=False)[0], out)
+
+
+def test_planted_rmsnorm_slips_fail_the_golden(oracle, golden):
+    d = golden("rmsnorm")
+    x, r, w, want = d["wide_x"], d["wide_r"], d["wide_w_bf16"], d["wide_y"]
+    # eps outside / much larger than eager's
+    assert not np.array_equal(oracle.add_rmsnorm(x, r, w, eps=1.0)[0], want)
+    # gain without the +1 offset
+    assert not np.array_equal(oracle.add_rmsnorm(x, r, w, gain_offset=False)[0], want)
+    # residual dropped
+    assert not np.array_equal(oracle.add_rmsnorm(x, None, w)[0], want)
+
+
+# ------------------------------------------------------------------ GQA
+
+def test_gqa_matches_golden(oracle, golden):
+    d = golden("gqa")
+    o = oracle.gqa_attention(d["f32_q"], d["f32_k"], d["f32_v"])
+    assert np.abs(o - d["f32_o"]).max() < 1e-6
+    f = oracle.bf16_to_f32
+    o = oracle.gqa_attention(f(d["bf16_q"]), f(d["bf16_k"]), f(d["bf16_v"]))
+    assert np.abs(o - d["bf16_o"]).max() < 1e-5
+    o = oracle.gqa_attention(f(d["var_q"]), f(d["var_k"]), f(d["var_v"]), cu_seqlens=d["var_cu"])
+    assert np.abs(o - d["var_o"]).max() < 1e-5
+
+
+def test_gqa_config1_vs_torch_sdpa(oracle):
+    """B=1, T=1024, 16 q / 4 kv heads, D=128, fp32, N(0,1)/sqrt(128), seed 0, order q, k, v."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn((1, 16, 1024, 128), generator=g) / 128 ** 0.5
+    k = torch.randn((1, 4, 1024, 128), generator=g) / 128 ** 0.5
+    v = torch.randn((1, 4, 1024, 128), generator=g) / 128 ** 0.5
+    with sdpa_kernel(SDPBackend.MATH):
+        ref = F.scaled_dot_product_attention(q, k.repeat_interleave(4, 1), v.repeat_interleave(4, 1), is_causal=True)
+    o = oracle.gqa_attention(q.numpy(), k.numpy(), v.numpy())
+    assert np.abs(o - ref.numpy()).max() < 1e-5
+
+
+def test_gqa_invariants(oracle):
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((1, 8, 33, 16))
+    k = rng.standard_normal((1, 2, 33, 16))
+    v = rng.standard_normal((1, 2, 33, 16))
+    o = oracle.gqa_attention(q, k, v)
+    # row 0 attends only to key 0
+    assert np.allclose(o[:, :, 0], v[:, np.arange(8) // 4, 0])
+    # Hkv == Hq reduces to MHA on the repeated heads
+    mha = oracle.gqa_attention(q, np.repeat(k, 4, axis=1), np.repeat(v, 4, axis=1))
+    assert np.allclose(o, mha)
+    # constant V gives constant output
+    oc = oracle.gqa_attention(q, k, np.full_like(v, 0.75))
+    assert np.allclose(oc, 0.75)
+    # permuting query heads inside a group permutes the output
+    perm = np.array([3, 2, 1, 0, 4, 5, 7, 6])
+    assert np.allclose(oracle.gqa_attention(q[:, perm], k, v), o[:, perm])
+    # brute force on a tiny case: explicit softmax per query
+    s = 1 / np.sqrt(16)
+    for h in (0, 5):
+        for i in (0, 7, 32):
+            logits = np.array([q[0, h, i] @ k[0, h // 4, j] * s for j in range(i + 1)])
+            p = np.exp(logits - logits.max())
+            p /= p.sum()
+            assert np.allclose(o[0, h, i], p @ v[0, h // 4, :i + 1])
+
+
+def test_planted_gqa_slips_fail_the_golden(oracle, golden):
+    d = golden("gqa")
+    q, k, v, want = d["f32_q"], d["f32_k"], d["f32_v"], d["f32_o"]
+    # wrong KV-head mapping (h % Hkv instead of h // group)
+    wrong = np.stack([oracle.gqa_attention(q[:, h:h + 1], k[:, h % 2:h % 2 + 1], v[:, h % 2:h % 2 + 1])[:, 0]
+                      for h in range(4)], axis=1)
+    assert np.abs(wrong - want).max() > 1e-2
+    # missing scale
+    assert np.abs(oracle.gqa_attention(q, k, v, scale=1.0) - want).max() > 1e-2
+    # transposed operand (V used as K)
+    assert np.abs(oracle.gqa_attention(q, v, k) - want).max() > 1e-2
+
+
+# ------------------------------------------------------------------ readout
+
+def test_readout_matches_golden(oracle, golden):
+    d = golden("readout")
+    choice, p = oracle.decide(d["logits"], d["nopts"])
+    assert np.array_equal(choice, d["choice"])
+    assert np.allclose(p.sum(axis=1), 1.0)
+    assert all((p[i, n:] == 0).all() for i, n in enumerate(d["nopts"]))

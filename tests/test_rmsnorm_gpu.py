@@ -1,0 +1,170 @@
+"""GPU parity of the fused residual add + RMSNorm kernel (fd_add_rmsnorm_fwd).
+
+Bar: updated residual bit-exact vs eager ``residual + x``; normed bit-exact vs
+the oracle's fp32 sequence and <= 1 bf16 ulp vs eager ``Qwen3_5RMSNorm``
+(BASELINE config 3).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import announce, from_bits, seeded, to_bits, ulp_diff
+
+pytestmark = pytest.mark.gpu
+
+
+def eager(x, residual, weight, eps=1e-6):
+    """The eager decoder layer: h = residual + x (bf16), then transformers' Qwen3_5RMSNorm."""
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5RMSNorm
+    h = residual + x
+    norm = Qwen3_5RMSNorm(x.shape[-1], eps=eps).to(x.device)
+    with torch.no_grad():
+        norm.weight.data = weight.clone()
+        return norm(h), h
+
+
+def test_golden_fixtures(golden, oracle):
+    from fastdecisions_amd.persistent_residual_rms_kernel import fused_add_rms_norm
+    d = golden("rmsnorm")
+    for case, wkey, ykey in (("small", "small_w", "small_y"), ("wide", "wide_w_bf16", "wide_y")):
+        announce(f"rmsnorm golden {case}")
+        x, r = from_bits(d[f"{case}_x"]), from_bits(d[f"{case}_r"])
+        w = from_bits(d[wkey])
+        out, res = fused_add_rms_norm(x, r, w, 1e-6)
+        torch.cuda.synchronize()
+        assert np.array_equal(to_bits(res), d[f"{case}_h"])
+        want, _ = oracle.add_rmsnorm(d[f"{case}_x"], d[f"{case}_r"], d[wkey])
+        assert np.array_equal(to_bits(out), want)
+        assert ulp_diff(to_bits(out), d[ykey]).max() <= 1
+    announce("rmsnorm golden fp32 weight")
+    w32 = torch.from_numpy(d["wide_w_f32"]).cuda()
+    out, _ = fused_add_rms_norm(from_bits(d["wide_x"]), from_bits(d["wide_r"]), w32)
+    want, _ = oracle.add_rmsnorm(d["wide_x"], d["wide_r"], d["wide_w_f32"])
+    assert np.array_equal(to_bits(out), want)
+    assert ulp_diff(to_bits(out), d["wide_y_f32w"]).max() <= 1
+
+
+def test_config3_full_size():
+    """x, residual [4, 2048, 2048] ~ N(0,1), gain 1 + 0.02 N(0,1), eps 1e-6."""
+    from fastdecisions_amd.persistent_residual_rms_kernel import fused_add_rms_norm
+    from oracle import cpu as oracle
+    announce("rmsnorm config3 [4,2048,2048]")
+    x = seeded((4, 2048, 2048), 1).cuda()
+    r = seeded((4, 2048, 2048), 2).cuda()
+    w = seeded((2048,), 3, 0.02).cuda()
+    out, res = fused_add_rms_norm(x, r, w, 1e-6)
+    ref_out, ref_res = eager(x, r, w)
+    torch.cuda.synchronize()
+    assert torch.equal(res.view(torch.int16), ref_res.view(torch.int16))
+    d = ulp_diff(to_bits(out), to_bits(ref_out))
+    print(f"config3: normed vs eager: {int((d != 0).sum())} of {d.size} differ by 1 ulp, max {int(d.max())}")
+    assert d.max() <= 1
+    want, want_res = oracle.add_rmsnorm(to_bits(x), to_bits(r), to_bits(w))
+    assert np.array_equal(to_bits(out), want)
+    assert np.array_equal(to_bits(res), want_res)
+
+
+@pytest.mark.parametrize("rows,width", [(1, 8), (3, 64), (5, 520), (7, 1000), (1025, 2048), (9, 4096),
+                                        (2, 8192), (4, 6144)])
+def test_widths_and_ragged_rows_bitexact(oracle, rows, width):
+    from fastdecisions_amd.persistent_residual_rms_kernel import fused_add_rms_norm, rms_norm
+    announce(f"rmsnorm rows={rows} width={width}")
+    x = seeded((rows, width), 10 + width, 3.0).cuda()
+    r = seeded((rows, width), 20 + width).cuda()
+    w = seeded((width,), 30 + width, 0.5).cuda()
+    out, res = fused_add_rms_norm(x, r, w, 1e-5)
+    plain = rms_norm(x, w, 1e-5)
+    torch.cuda.synchronize()
+    want, want_res = oracle.add_rmsnorm(to_bits(x), to_bits(r), to_bits(w), eps=1e-5)
+    assert np.array_equal(to_bits(res), want_res)
+    assert np.array_equal(to_bits(out), want)
+    want_plain, _ = oracle.add_rmsnorm(to_bits(x), None, to_bits(w), eps=1e-5)
+    assert np.array_equal(to_bits(plain), want_plain)
+
+
+def test_plain_gain_and_fp32_weight(oracle):
+    from fastdecisions_amd.persistent_residual_rms_kernel import fused_add_rms_norm
+    announce("rmsnorm gain_offset=False fp32 weight")
+    x = seeded((33, 2048), 41).cuda()
+    r = seeded((33, 2048), 42).cuda()
+    w = (1 + 0.1 * torch.randn(2048, generator=torch.Generator().manual_seed(43))).cuda()
+    out, _ = fused_add_rms_norm(x, r, w, 1e-6, gain_offset=False)
+    torch.cuda.synchronize()
+    want, _ = oracle.add_rmsnorm(to_bits(x), to_bits(r), w.cpu().numpy(), gain_offset=False)
+    assert np.array_equal(to_bits(out), want)
+
+
+def test_in_place_residual_update_through_abi(oracle):
+    """residual_out may alias residual: the C ABI contract of fd_add_rmsnorm_fwd."""
+    from fastdecisions_amd import _lib
+    announce("rmsnorm in-place residual")
+    x = seeded((64, 2048), 51).cuda()
+    r = seeded((64, 2048), 52).cuda()
+    w = seeded((2048,), 53, 0.02).cuda()
+    want, want_res = oracle.add_rmsnorm(to_bits(x), to_bits(r), to_bits(w))
+    out = torch.empty_like(x)
+    lib = _lib.lib()
+    rc = lib.fd_add_rmsnorm_fwd(x.data_ptr(), r.data_ptr(), w.data_ptr(), out.data_ptr(), r.data_ptr(),
+                                64, 2048, ctypes.c_float(1e-6), _lib.FD_DTYPE_BF16, 1,
+                                _lib.stream_handle(x.device))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(to_bits(r), want_res)
+    assert np.array_equal(to_bits(out), want)
+
+
+def test_reference_signature_residual_rms(oracle):
+    from fastdecisions_amd.persistent_residual_rms_kernel import residual_rms
+    announce("rmsnorm residual_rms(a, b, weight)")
+    a = seeded((2, 100, 2048), 61).cuda()
+    b = seeded((2, 100, 2048), 62).cuda()
+    w = seeded((2048,), 63, 0.02).cuda()
+    out = residual_rms(a, b, w)
+    torch.cuda.synchronize()
+    want, _ = oracle.add_rmsnorm(to_bits(b), to_bits(a), to_bits(w))
+    assert out.shape == a.shape and out.dtype == torch.bfloat16
+    assert np.array_equal(to_bits(out), want)
+
+
+def test_graph_replay_with_changed_input(oracle):
+    from fastdecisions_amd.persistent_residual_rms_kernel import fused_add_rms_norm
+    announce("rmsnorm graph replay")
+    x = seeded((256, 2048), 71).cuda()
+    r = seeded((256, 2048), 72).cuda()
+    w = seeded((2048,), 73, 0.02).cuda()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fused_add_rms_norm(x, r, w)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out, res = fused_add_rms_norm(x, r, w)
+    for seed in (74, 75, 76):
+        x.copy_(seeded((256, 2048), seed).cuda())
+        graph.replay()
+        torch.cuda.synchronize()
+        want, want_res = oracle.add_rmsnorm(to_bits(x), to_bits(r), to_bits(w))
+        assert np.array_equal(to_bits(out), want)
+        assert np.array_equal(to_bits(res), want_res)
+
+
+def test_wrapper_rejects_bad_inputs():
+    from fastdecisions_amd.persistent_residual_rms_kernel import fused_add_rms_norm, residual_rms
+    x = torch.zeros((4, 2048), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(2048, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="identical shapes"):
+        fused_add_rms_norm(x, x[:2], w)
+    with pytest.raises(ValueError, match="BF16"):
+        fused_add_rms_norm(x.float(), x.float(), w)
+    strided = torch.zeros((4, 4096), dtype=torch.bfloat16, device="cuda")[:, ::2]
+    with pytest.raises(ValueError, match="contiguous"):
+        fused_add_rms_norm(strided, strided, w)
+    with pytest.raises(ValueError, match="2048"):
+        residual_rms(x[:, :1024], x[:, :1024], w[:1024])
