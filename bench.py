@@ -1,0 +1,382 @@
+#!/usr/bin/env python
+"""Benchmark of the decider forward hot path on one MI355X (gfx950).
+
+Step = one forward of the decider-2b-shaped model (B=1,
+T=2048, 28 layers 3:1 Gated-DeltaNet/GQA, bf16, seeded random weights,
+synthetic token ids) with the three HIP kernels installed, replayed from a
+captured HIP graph; the metric is the median GPU forward time (ms).  The same
+model on the reference PyTorch path (SDPA / F.conv1d / eager RMSNorm, also
+graph-replayed) is timed interleaved with it, and the argmax decisions of the
+4 tail slots are compared.
+
+Per kernel, at its BASELINE configuration, the HIP kernel and the PyTorch-ROCm
+eager op it replaces are timed from HIP events on the launch stream (graph
+replays of back-to-back launches; HBM-bound kernels rotate > 512 MB of inputs
+so the 256 MB MALL cannot serve them), and the kernel's roofline fraction is
+computed from its algorithmic work:
+  GQA   4*B*Hq*D*T^2/2 flop (causal) vs dense bf16 MFMA 2.5 PFLOP/s
+  conv  x + w + q/k/v bytes vs HBM 8 TB/s
+  norm  x + residual + out + residual_out + gain bytes vs HBM 8 TB/s
+
+The reference CPU PyTorch path (oracle/reference_cpu.py) is timed on the host
+cores as a reported baseline.  Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import random
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20, help="timed forward steps (graph replays)")
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--kernel-samples", type=int, default=30, help="timing samples per kernel")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-kernels", action="store_true", help="skip the per-kernel micro-benchmarks")
+    p.add_argument("--no-forward", action="store_true", help="skip the full-forward benchmark")
+    p.add_argument("--only-kernel", choices=["gqa", "conv", "rmsnorm"], default=None,
+                   help="profiling aid: run just this kernel's HIP timing loop")
+    return p.parse_args()
+
+
+# --------------------------------------------------------------------------- timing helpers
+
+def graph_of(fns):
+    """Capture one HIP graph that calls every fn once, after warm-up on a side stream."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            for fn in fns:
+                fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for fn in fns:
+            fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graphs(graphs: dict, launches_per_replay: dict, samples: int, replays: int) -> dict:
+    """Interleaved (random order) event timing of graph replays; returns per-launch µs lists."""
+    import torch
+    rng = random.Random(17)
+    out = {k: [] for k in graphs}
+    for g in graphs.values():
+        for _ in range(3):
+            g.replay()
+    torch.cuda.synchronize()
+    for _ in range(samples):
+        order = list(graphs)
+        rng.shuffle(order)
+        for name in order:
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(replays):
+                graphs[name].replay()
+            end.record()
+            end.synchronize()
+            out[name].append(start.elapsed_time(end) * 1e3 / (replays * launches_per_replay[name]))
+    return out
+
+
+def summary(us: list[float]) -> dict:
+    s = sorted(us)
+    return dict(median_us=statistics.median(s), min_us=s[0], p95_us=s[min(len(s) - 1, int(0.95 * len(s)))])
+
+
+# --------------------------------------------------------------------------- kernels
+
+def bench_gqa(samples: int, only: bool = False) -> dict:
+    import torch
+    import torch.nn.functional as F
+    from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
+    B, Hq, Hkv, T, D = 1, 16, 4, 2048, 128
+    g = torch.Generator().manual_seed(0)
+    # decider layout: q and v are token-major [B, T, H, D] viewed head-major, k head-major
+    q = (torch.randn((B, T, Hq, D), generator=g) / D ** 0.5).to(torch.bfloat16).cuda().permute(0, 2, 1, 3)
+    k = (torch.randn((B, Hkv, T, D), generator=g) / D ** 0.5).to(torch.bfloat16).cuda()
+    v = (torch.randn((B, T, Hkv, D), generator=g) / D ** 0.5).to(torch.bfloat16).cuda().permute(0, 2, 1, 3)
+    flops = 4 * B * Hq * D * T * T / 2
+    bytes_ = 2 * (q.numel() + k.numel() + v.numel() + q.numel())
+    graphs = {"hip": graph_of([lambda: native_gqa_attention(q, k, v)])}
+    backend = None
+    if not only:
+        def sdpa_gqa():
+            return F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
+
+        def sdpa_repeat():
+            kr = k[:, :, None].expand(B, Hkv, Hq // Hkv, T, D).reshape(B, Hq, T, D)
+            vr = v[:, :, None].expand(B, Hkv, Hq // Hkv, T, D).reshape(B, Hq, T, D)
+            return F.scaled_dot_product_attention(q, kr, vr, is_causal=True)
+        graphs["eager_sdpa_enable_gqa"] = graph_of([sdpa_gqa])
+        graphs["eager_sdpa_repeat_kv"] = graph_of([sdpa_repeat])
+        backend = _sdpa_backend(q, k, v)
+    times = time_graphs(graphs, {k_: 1 for k_ in graphs}, samples, 20)
+    res = {name: summary(t) for name, t in times.items()}
+    us = res["hip"]["median_us"]
+    out = dict(config="B=1 T=2048 Hq=16 Hkv=4 D=128 bf16", bound="mfma", flops=flops, bytes=bytes_,
+               hip=res["hip"], tflops=flops / us / 1e6, peak_tflops=MFMA_BF16_PEAK_TFLOPS,
+               frac=flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS)
+    if not only:
+        base = min(res["eager_sdpa_enable_gqa"]["median_us"], res["eager_sdpa_repeat_kv"]["median_us"])
+        out.update(eager_sdpa_enable_gqa=res["eager_sdpa_enable_gqa"], eager_sdpa_repeat_kv=res["eager_sdpa_repeat_kv"],
+                   sdpa_backend=backend, speedup_vs_best_eager=base / us)
+    return out
+
+
+def _sdpa_backend(q, k, v) -> str:
+    """Which SDPA backend PyTorch picks for the enable_gqa call (first that accepts it)."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    for name, be in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION),
+                     ("math", SDPBackend.MATH)):
+        try:
+            with sdpa_kernel(be):
+                F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
+            torch.cuda.synchronize()
+            return name
+        except RuntimeError:
+            continue
+    return "unknown"
+
+
+def bench_conv(samples: int, only: bool = False) -> dict:
+    import torch
+    import torch.nn.functional as F
+    from fastdecisions_amd.packed_conv_kernel import prep_qkv
+    B, T, C = 1, 2048, 6144
+    sets = 12  # 12 x (24 MiB in + 24 MiB out) > 512 MB: defeats the 256 MB MALL
+    g = torch.Generator().manual_seed(0)
+    xs = [torch.randn((B, T, C), generator=g).to(torch.bfloat16).cuda() for _ in range(sets)]
+    w = (torch.randn((C, 4), generator=g) * 0.25).to(torch.bfloat16).cuda()
+    bytes_ = 2 * (B * T * C + C * 4 + B * T * C)
+    graphs = {"hip": graph_of([lambda x=x: prep_qkv(x, w) for x in xs])}
+    if not only:
+        from transformers.models.qwen3_5.modeling_qwen3_5 import causal_conv1d_fn
+
+        def eager(x):
+            # transformers' eager path: channel-major conv + SiLU, then split into the consumer layout
+            y = causal_conv1d_fn(x.transpose(1, 2), w, None, activation="silu").transpose(1, 2)
+            return [t.reshape(B, T, 16, 128).contiguous() for t in torch.split(y, [2048, 2048, 2048], dim=-1)]
+
+        def fp32_conv(x):
+            y = F.silu(F.conv1d(x.float().transpose(1, 2), w.float()[:, None], padding=3, groups=C)[..., :T])
+            return [t.contiguous() for t in y.transpose(1, 2).to(torch.bfloat16).split(2048, dim=-1)]
+        graphs["eager_hf_causal_conv1d"] = graph_of([lambda x=x: eager(x) for x in xs])
+        graphs["eager_fp32_conv1d"] = graph_of([lambda x=x: fp32_conv(x) for x in xs])
+    times = time_graphs(graphs, {k_: sets for k_ in graphs}, samples, 5)
+    res = {name: summary(t) for name, t in times.items()}
+    us = res["hip"]["median_us"]
+    out = dict(config="B=1 T=2048 C=6144 W=4 SiLU bf16", bound="hbm", bytes=bytes_, hip=res["hip"],
+               gbs=bytes_ / us / 1e3, peak_gbs=HBM_PEAK_GBS, frac=bytes_ / us / 1e3 / HBM_PEAK_GBS,
+               rotated_sets=sets)
+    if not only:
+        out.update(eager_hf_causal_conv1d=res["eager_hf_causal_conv1d"], eager_fp32_conv1d=res["eager_fp32_conv1d"],
+                   speedup_vs_eager=res["eager_hf_causal_conv1d"]["median_us"] / us)
+    return out
+
+
+def bench_rmsnorm(samples: int, only: bool = False) -> dict:
+    import torch
+    from fastdecisions_amd.persistent_residual_rms_kernel import fused_add_rms_norm
+    shape = (4, 2048, 2048)
+    sets = 5  # 5 x (64 MiB in + 64 MiB out) > 512 MB
+    g = torch.Generator().manual_seed(0)
+    xs = [torch.randn(shape, generator=g).to(torch.bfloat16).cuda() for _ in range(sets)]
+    rs = [torch.randn(shape, generator=g).to(torch.bfloat16).cuda() for _ in range(sets)]
+    w = (torch.randn((2048,), generator=g) * 0.02).to(torch.bfloat16).cuda()
+    n = 4 * 2048 * 2048
+    bytes_ = 2 * 4 * n + 2 * 2048
+    graphs = {"hip": graph_of([lambda x=x, r=r: fused_add_rms_norm(x, r, w) for x, r in zip(xs, rs)])}
+    if not only:
+        from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5RMSNorm
+        norm = Qwen3_5RMSNorm(2048, eps=1e-6).cuda().to(torch.bfloat16)
+        norm.weight.data.copy_(w)
+
+        def eager(x, r):
+            h = r + x
+            return norm(h), h
+        graphs["eager_add_qwen3_5_rmsnorm"] = graph_of([lambda x=x, r=r: eager(x, r) for x, r in zip(xs, rs)])
+    times = time_graphs(graphs, {k_: sets for k_ in graphs}, samples, 5)
+    res = {name: summary(t) for name, t in times.items()}
+    us = res["hip"]["median_us"]
+    out = dict(config="[4,2048,2048] bf16 eps=1e-6", bound="hbm", bytes=bytes_, hip=res["hip"],
+               gbs=bytes_ / us / 1e3, peak_gbs=HBM_PEAK_GBS, frac=bytes_ / us / 1e3 / HBM_PEAK_GBS,
+               rotated_sets=sets)
+    if not only:
+        out.update(eager_add_qwen3_5_rmsnorm=res["eager_add_qwen3_5_rmsnorm"],
+                   speedup_vs_eager=res["eager_add_qwen3_5_rmsnorm"]["median_us"] / us)
+    return out
+
+
+# --------------------------------------------------------------------------- full forward
+
+def bench_forward(args) -> dict:
+    import torch
+    from fastdecisions_amd.engine import Engine, margins, read_slots
+    from fastdecisions_amd.model import DECIDER_2B_SHAPED, build_decider, install_hip_kernels
+    from fastdecisions_amd.workloads import config4_request
+    t0 = time.time()
+    model = build_decider(DECIDER_2B_SHAPED, seed=args.seed, device="cuda")
+    req = config4_request(DECIDER_2B_SHAPED.vocab_size)
+    ids = req.ids[None].cuda()
+    log(f"model built in {time.time() - t0:.1f}s; capturing the eager (reference PyTorch path) graph")
+    eager_engine = Engine(model)
+    ref = eager_engine.logits_all(ids).clone()
+    counts = install_hip_kernels(model)
+    log(f"installed HIP kernels {counts}; capturing the HIP graph")
+    hip_engine = Engine(model)
+    got = hip_engine.logits_all(ids).clone()
+    torch.cuda.synchronize()
+    rows = [0] * len(req.slots)
+    d_ref = read_slots(ref, rows, req.slots, req.nopts).argmax(-1).tolist()
+    d_got = read_slots(got, rows, req.slots, req.nopts).argmax(-1).tolist()
+    key = tuple(ids.shape)
+
+    # warm-up, then exactly `steps` timed HIP steps, bracketed by synchronize on both sides
+    for _ in range(args.warmup):
+        hip_engine.replay(key)
+        eager_engine.replay(key)
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t_start = time.perf_counter()
+    for s, e in events:
+        s.record()
+        hip_engine.replay(key)
+        e.record()
+    torch.cuda.synchronize()
+    total_hip = (time.perf_counter() - t_start) * 1e3
+    hip_ms = [s.elapsed_time(e) for s, e in events]
+    # the reference PyTorch path, same number of steps, outside the timed region
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for s, e in events:
+        s.record()
+        eager_engine.replay(key)
+        e.record()
+    torch.cuda.synchronize()
+    eager_ms = [s.elapsed_time(e) for s, e in events]
+    return dict(
+        median_ms=statistics.median(hip_ms), min_ms=min(hip_ms), wall_ms_per_step=total_hip / args.steps,
+        eager_median_ms=statistics.median(eager_ms), speedup_vs_eager=statistics.median(eager_ms) / statistics.median(hip_ms),
+        decisions_eager=d_ref, decisions_hip=d_got, decisions_identical=d_ref == d_got,
+        slot_margins=[round(m, 4) for m in margins(ref, rows, req.slots, req.nopts)],
+        max_abs_logit_diff=float((got - ref).abs().max()), patched=counts)
+
+
+# --------------------------------------------------------------------------- CPU baseline
+
+def cpu_baseline() -> dict:
+    import torch
+    from oracle import reference_cpu
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    info = reference_cpu.cpu_info()
+    t0 = time.time()
+    fwd = reference_cpu.decider_forward_sample(layers=4, seq_len=2048, warmup=1, runs=3)
+    gqa = reference_cpu.gqa_config1()
+    conv = reference_cpu.conv_config2()
+    norm = reference_cpu.rmsnorm_config3()
+    log(f"cpu baseline took {time.time() - t0:.1f}s")
+    return dict(value=fwd["scaled_forward_ms"], unit="ms", cores=torch.get_num_threads(), kind="port",
+                sample=("eager fp32 PyTorch forward of the decider-2b-shaped model (transformers Qwen3.5 layers: "
+                        "SDPA, F.conv1d, eager RMSNorm, torch gated-delta rule) at B=1 T=2048 over layers 0-3 "
+                        f"(3 DeltaNet + 1 GQA), median of 3 runs = {fwd['sample_ms']:.1f} ms, scaled x7 to 28 layers"),
+                cpu_model=info["cpu_model"], cores_visible=info["cores_visible"],
+                gqa_config1_ms=gqa, conv_config2_ms=conv, rmsnorm_config3_ms=norm)
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build runs the decider forward on a "
+              "single MI355X; see DESIGN.md for how the path would shard across GPUs.", file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (torch.cuda.is_available() is False)", file=sys.stderr)
+        return 2
+    torch.backends.cuda.matmul.allow_tf32 = False
+    log(f"device: {torch.cuda.get_device_name(0)}")
+
+    if args.only_kernel:
+        fn = dict(gqa=bench_gqa, conv=bench_conv, rmsnorm=bench_rmsnorm)[args.only_kernel]
+        print(json.dumps({args.only_kernel: fn(args.kernel_samples, only=True)}), flush=True)
+        return 0
+
+    kernels = {}
+    if not args.no_kernels:
+        log("kernel micro-benchmarks")
+        kernels["gqa"] = bench_gqa(args.kernel_samples)
+        log(f"gqa: {kernels['gqa']['hip']['median_us']:.1f} us, {kernels['gqa']['tflops']:.0f} TFLOP/s")
+        kernels["packed_conv"] = bench_conv(args.kernel_samples)
+        log(f"conv: {kernels['packed_conv']['hip']['median_us']:.1f} us, {kernels['packed_conv']['gbs']:.0f} GB/s")
+        kernels["add_rmsnorm"] = bench_rmsnorm(args.kernel_samples)
+        log(f"rmsnorm: {kernels['add_rmsnorm']['hip']['median_us']:.1f} us, {kernels['add_rmsnorm']['gbs']:.0f} GB/s")
+        torch.cuda.empty_cache()
+
+    fwd = None
+    if not args.no_forward:
+        log("full forward")
+        fwd = bench_forward(args)
+        log(f"forward: hip {fwd['median_ms']:.3f} ms, eager {fwd['eager_median_ms']:.3f} ms, "
+            f"decisions identical: {fwd['decisions_identical']}")
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline()
+
+    roofline = None
+    if "gqa" in kernels:
+        gq = kernels["gqa"]
+        roofline = dict(bound="mfma", kernel="gqa_fwd_kernel<128> (B=1 T=2048 16/4 heads D=128)",
+                        achieved=gq["tflops"], peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s", frac=gq["frac"],
+                        traffic=None)
+    line = {
+        "metric": "median GPU forward ms, B=1 T=2048 decider-2b-shaped; per-kernel % roofline",
+        "value": fwd["median_ms"] if fwd else None,
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": fwd["wall_ms_per_step"] if fwd else None,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded random-init weights, uniform token ids)",
+        "config": {"workload": "decider-2b-shaped forward, B=1 T=2048, 28 layers (21 Gated-DeltaNet + 7 GQA 16/4x128), "
+                               "HIP graph replay", "global_batch": 1, "seq_len": 2048},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "forward": fwd,
+        "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

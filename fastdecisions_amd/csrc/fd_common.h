@@ -45,21 +45,21 @@ __device__ __forceinline__ uint32_t fd_pack2(float lo, float hi) {
   return fd_f32_to_bf16(lo) | (fd_f32_to_bf16(hi) << 16);
 }
 
-// exp(x) in fp32: Cody–Waite reduction x = k*ln2 + r (ln2 split into a
-// 16-significant-bit head and a tail so k*head is exact), degree-7 Taylor
-// polynomial of e^r on |r| <= ln2/2 in Horner form, then an exact scaling by
-// 2^k (two steps when the result is subnormal, so it rounds only once).
-// Error < 2 ulp over the whole range; identical bits on CPU and GPU because
-// every step is a single IEEE operation.
-__device__ __forceinline__ float fd_expf(float x) {
-  if (x != x) return x;
-  if (x > 88.72283935546875f) return __uint_as_float(0x7f800000u);
-  if (x < -103.972084045410156f) return 0.0f;
+// e^t for the SiLU, branch-free: t is first clamped to [-20, 89] (v_med3);
+// Cody–Waite reduction t = k*ln2 + r with ln2 split into a head of 16
+// significant bits (so k*head is exact) and a tail; degree-7 Taylor polynomial
+// of e^r on |r| <= ln2/2 in Horner form; exact scaling by 2^k (v_ldexp, k in
+// [-29, 129]: no subnormal result, overflow to +inf).  Error < 2 ulp on
+// [-20, 88.7]; identical bits on CPU and GPU since every step is one IEEE op.
+// The clamp changes nothing the SiLU can see: below -17.4, 1 + e^t == 1 in
+// fp32, and above 88.73 e^t is +inf either way.
+__device__ __forceinline__ float fd_exp_silu(float t) {
   const float kLog2e = 1.44269502162933349609375f;
   const float kLn2Hi = 0.693145751953125f;         // 0x3f317200
   const float kLn2Lo = 1.428606765330187045e-06f;  // ln2 - kLn2Hi
-  float k = rintf(x * kLog2e);
-  float r = __builtin_fmaf(-k, kLn2Hi, x);
+  t = __builtin_amdgcn_fmed3f(t, -20.0f, 89.0f);
+  const float k = __builtin_rintf(t * kLog2e);
+  float r = __builtin_fmaf(-k, kLn2Hi, t);
   r = __builtin_fmaf(-k, kLn2Lo, r);
   float p = 1.0f / 5040.0f;
   p = __builtin_fmaf(p, r, 1.0f / 720.0f);
@@ -69,11 +69,9 @@ __device__ __forceinline__ float fd_expf(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  int ki = static_cast<int>(k);
-  if (ki > 127) return (p * 1.7014118346046923e38f) * __uint_as_float(static_cast<uint32_t>(ki - 127 + 127) << 23);
-  if (ki < -126) return (p * __uint_as_float(static_cast<uint32_t>(ki + 64 + 127) << 23)) * 5.421010862427522e-20f;
-  return p * __uint_as_float(static_cast<uint32_t>(ki + 127) << 23);
+  return __builtin_ldexpf(p, static_cast<int>(k));
 }
 
 // SiLU as the reference writes it: y / (1 + exp(-y)), correctly rounded division.
-__device__ __forceinline__ float fd_silu(float y) { return y / (1.0f + fd_expf(-y)); }
+// A NaN y gives NaN whatever the clamped exponential returns.
+__device__ __forceinline__ float fd_silu(float y) { return y / (1.0f + fd_exp_silu(-y)); }

@@ -7,23 +7,31 @@
 // exp(m_old - m_new) (:84-104); P rounded to bf16 before P·V (:98-102);
 // out = acc / denominator (:106-113).  The design is CDNA4's own:
 //
-// * One workgroup = 4 wavefronts = the query heads of one KV group (or, for
-//   groups smaller than 4, several 32-query blocks of fewer heads).  A 64-key
-//   K tile and the transposed V tile are staged once in LDS and read by all 4
-//   wavefronts: K/V leave L2 once per group instead of once per query head.
+// * One workgroup = the query heads of one KV group x 32 queries; for
+//   head_dim <= 128 it has 8 wavefronts, two per SIMD: the two wavefronts of a
+//   head split every 64-key tile into its two 32-key halves (each keeps its
+//   own running max / denominator / accumulator; they are merged through LDS
+//   at the end).  Two wavefronts per SIMD let one run softmax VALU work while
+//   the other issues MFMAs.  head_dim 256 runs 4 wavefronts (register budget).
+// * K and V tiles (64 keys) are copied global -> LDS with global_load_lds
+//   (no staging registers, no VALU), double buffered, one barrier per tile.
+//   16-byte chunks are XOR-swizzled per row so that the MFMA operand reads
+//   below are bank-conflict free.
 // * The score tile is computed transposed, S^T = K · Q^T, with
 //   v_mfma_f32_32x32x16_bf16.  In the 32x32 accumulator a lane owns one
 //   column (= one query) and 16 rows (= keys), so the softmax row max and sum
-//   are lane-local except for one xor-32 exchange between the two lane halves.
+//   are lane-local except for one exchange between the two lane halves
+//   (v_permlane32_swap).
 // * The K rows fed to the MFMA are permuted (sigma below) so that the 8 keys a
 //   lane holds for each 16-key slice of P are exactly the 8 consecutive keys
 //   it must supply as the B operand of O^T += V^T · P^T: P never leaves
-//   registers.  V is transposed while it is staged (4 keys x 8 dims per
-//   thread, 8-byte LDS stores) so the A operand is one 16-byte LDS read.
-// * The output is accumulated transposed (O^T), so the per-query rescale by
-//   exp(m_old - m_new) and the final 1/denominator are lane-local too.
-// * Register double buffering: the next K/V tile is loaded from global memory
-//   while the current one is consumed from LDS; one barrier per tile.
+//   registers.  The V^T A operand comes straight from the row-major V tile
+//   with two ds_read_b64_tr_b16 (transposing LDS reads) per MFMA.
+// * The output is accumulated transposed (O^T), so the per-query rescale and
+//   the final 1/denominator are lane-local.  The scale is folded into the exp2
+//   argument (one fma per score), masks run only on diagonal / tail tiles, and
+//   the running max is raised lazily (only when a tile exceeds it by more than
+//   2^8), so the O rescale is skipped on most tiles.
 // * Work items are ordered longest-first (causal tiles near the end of the
 //   sequence have the most keys) and mapped so that each XCD receives a
 //   contiguous range of (head group, query tile) items, keeping a KV head's
@@ -33,14 +41,18 @@
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
 constexpr int kBlockM = 32;  // queries per wavefront
 constexpr int kBlockN = 64;  // keys per LDS tile
 constexpr int kNumXcd = 8;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 
 struct GqaArgs {
   const uint16_t* q;
@@ -59,16 +71,19 @@ struct GqaArgs {
   int n_items;    // n_qtiles * n_hgroups * sequences
 };
 
-template <int D>
-struct Tile {
-  static constexpr int kRow = D + 8;         // K tile row stride (bf16), 16-byte pad
-  static constexpr int kVtRow = kBlockN + 8;  // V^T row stride (bf16), 16-byte pad
-  static constexpr int kKElems = kBlockN * kRow;
-  static constexpr int kVElems = D * kVtRow;
-  static constexpr int kStage = kKElems + kVElems;
-  static constexpr int kKChunks = kBlockN * D / 8 / kThreads;          // 16-B K chunks per thread
-  static constexpr int kVTasks = (kBlockN / 4) * (D / 8);             // (4 keys x 8 dims) tasks
-  static constexpr int kVPerThread = (kVTasks + kThreads - 1) / kThreads;
+// KSPLIT = wavefronts per (head, query block): each takes 64/KSPLIT keys of a tile.
+template <int D, int KSPLIT>
+struct Cfg {
+  static constexpr int kWaves = 4 * KSPLIT;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kBlocks = 2 / KSPLIT;                 // 32-key blocks per wavefront per tile
+  static constexpr int kChunksRow = D / 8;                   // 16-byte chunks per K / V row
+  static constexpr int kTileBytes = kBlockN * kChunksRow * 16;
+  static constexpr int kLoads = kBlockN * kChunksRow / kThreads;  // global_load_lds per thread per K (or V) tile
+  static constexpr int kStageBytes = 2 * kTileBytes;         // K tile + V tile
+  static constexpr int kCombineBytes = KSPLIT > 1 ? 4 * 64 * (D / 2 + 2) * 4 : 0;
+  static constexpr int kSmemBytes = (2 * kStageBytes > kCombineBytes) ? 2 * kStageBytes : kCombineBytes;
+  static_assert(kLoads * kThreads == kBlockN * kChunksRow, "tile must split evenly over the threads");
 };
 
 // Key (within a 32-key block) supplied by MFMA row m, chosen so that the
@@ -77,17 +92,48 @@ __device__ __forceinline__ int sigma(int m) {
   return ((m >> 4) << 4) + (((m >> 2) & 1) << 3) + (((m >> 3) & 1) << 2) + (m & 3);
 }
 
+// Chunk swizzles (physical chunk = logical chunk ^ f(row)).  K: the MFMA A
+// operand reads rows sigma(0..7) = {0,1,2,3,8,9,10,11} (then +4) at one chunk;
+// a bit permutation of row & 15 sends any 8 of them to 8 distinct chunks.
+// V: a transposing read touches 4 consecutive rows x 2 adjacent chunks;
+// xor with 2*(row & 3) spreads them over 8 chunks and keeps pairs adjacent.
+template <int CR>
+__device__ __forceinline__ int swz_k(int row) {
+  const int r = row & 15;
+  return ((r & 3) | ((r & 8) >> 1) | ((r & 4) << 1)) & (CR - 1);
+}
+template <int CR>
+__device__ __forceinline__ int swz_v(int row) {
+  return (2 * (row & 3)) & (CR - 1);
+}
+
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
 
-template <int D>
-__global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(GqaArgs a) {
-  using T = Tile<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * T::kStage];
+// Max / sum of a value over lanes l and l^32 (the two lane halves hold the two
+// 16-key halves of one query's scores).  v_permlane32_swap with the value in
+// both operands leaves this lane's value in one result and its partner's in
+// the other, so max and sum of the pair need no lane-index select.
+__device__ __forceinline__ float half_max(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_sum(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int D, int KSPLIT>
+__global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
+  using C = Cfg<D, KSPLIT>;
+  constexpr int CR = C::kChunksRow;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[C::kSmemBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int col = lane & 31;  // query within the wavefront's block
+  const int w4 = wave & 3;     // (head, query block) slot
+  const int kh = wave >> 2;    // key part of each tile (0 when KSPLIT == 1)
+  const int col = lane & 31;   // query within the wavefront's block
   const int half = lane >> 5;
 
   // ---- work item: XCD-contiguous renumbering, longest tile first
@@ -115,8 +161,8 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(GqaArgs a) {
   if (q0 >= seq_end) return;  // uniform over the workgroup
 
   const int group = a.q_heads / a.kv_heads;
-  const int hsub = wave % a.hpw;
-  const int qb = wave / a.hpw;
+  const int hsub = w4 % a.hpw;
+  const int qb = w4 / a.hpw;
   const int qhead = hg * a.hpw + hsub;
   const int kvhead = (hg * a.hpw) / group;
 
@@ -128,6 +174,7 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(GqaArgs a) {
   const int qw0 = q0 + qb * kBlockM;  // first query of this wavefront
   const int qpos = qw0 + col;
   const bool qvalid = qpos < seq_end;
+  const float c = a.scale_log2;
 
   // Q^T as MFMA B operand: lane supplies Q[qpos][16kk + 8*half + 0..7].
   bf16x8_t qf[D / 16];
@@ -141,155 +188,160 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(GqaArgs a) {
   const int kend = min(q0 + qspan, seq_end);
   const int ntiles = (kend - seq_start + kBlockN - 1) / kBlockN;
 
-  // ---- global -> register staging of one K/V tile
-  uint4 kreg[T::kKChunks];
-  uint4 vreg[T::kVPerThread][4];
-  auto load_tile = [&](int t) {
+  // ---- global -> LDS copies of one K tile and one V tile (rows past the end
+  // of the sequence re-read its last row: finite data the mask discards)
+  auto issue_tile = [&](int t, int buf) {
     const int ks0 = seq_start + t * kBlockN;
+    unsigned char* kt = smem + buf * C::kStageBytes;
+    unsigned char* vt = kt + C::kTileBytes;
 #pragma unroll
-    for (int i = 0; i < T::kKChunks; ++i) {
-      const int c = tid + kThreads * i;
-      const int row = c / (D / 8), c8 = c % (D / 8);
-      const int key = ks0 + row;
-      kreg[i] = key < seq_end ? *reinterpret_cast<const uint4*>(kbase + key * a.ks[2] + c8 * 8)
-                              : make_uint4(0u, 0u, 0u, 0u);
-    }
-#pragma unroll
-    for (int i = 0; i < T::kVPerThread; ++i) {
-      const int c = tid + kThreads * i;
-      if (c < T::kVTasks) {
-        const int k4 = c % (kBlockN / 4), d8 = c / (kBlockN / 4);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = ks0 + k4 * 4 + r;
-          vreg[i][r] = key < seq_end ? *reinterpret_cast<const uint4*>(vbase + key * a.vs[2] + d8 * 8)
-                                     : make_uint4(0u, 0u, 0u, 0u);
-        }
-      }
-    }
-  };
-  auto store_tile = [&](int stage) {
-    uint16_t* ks_l = smem + stage * T::kStage;
-    uint16_t* vt_l = ks_l + T::kKElems;
-#pragma unroll
-    for (int i = 0; i < T::kKChunks; ++i) {
-      const int c = tid + kThreads * i;
-      const int row = c / (D / 8), c8 = c % (D / 8);
-      *reinterpret_cast<uint4*>(ks_l + row * T::kRow + c8 * 8) = kreg[i];
-    }
-#pragma unroll
-    for (int i = 0; i < T::kVPerThread; ++i) {
-      const int c = tid + kThreads * i;
-      if (c < T::kVTasks) {
-        const int k4 = c % (kBlockN / 4), d8 = c / (kBlockN / 4);
-        const uint32_t w0[4] = {vreg[i][0].x, vreg[i][0].y, vreg[i][0].z, vreg[i][0].w};
-        const uint32_t w1[4] = {vreg[i][1].x, vreg[i][1].y, vreg[i][1].z, vreg[i][1].w};
-        const uint32_t w2[4] = {vreg[i][2].x, vreg[i][2].y, vreg[i][2].z, vreg[i][2].w};
-        const uint32_t w3[4] = {vreg[i][3].x, vreg[i][3].y, vreg[i][3].z, vreg[i][3].w};
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          // dims 2p (low halves) and 2p+1 (high halves) of keys 4*k4 + 0..3
-          uint2 lo, hi;
-          lo.x = (w0[p] & 0xffffu) | (w1[p] << 16);
-          lo.y = (w2[p] & 0xffffu) | (w3[p] << 16);
-          hi.x = (w0[p] >> 16) | (w1[p] & 0xffff0000u);
-          hi.y = (w2[p] >> 16) | (w3[p] & 0xffff0000u);
-          *reinterpret_cast<uint2*>(vt_l + (d8 * 8 + 2 * p) * T::kVtRow + k4 * 4) = lo;
-          *reinterpret_cast<uint2*>(vt_l + (d8 * 8 + 2 * p + 1) * T::kVtRow + k4 * 4) = hi;
-        }
-      }
+    for (int i = 0; i < C::kLoads; ++i) {
+      const int blk = i * C::kWaves + wave;   // 1 KiB LDS block written by this instruction
+      const int slot = blk * 64 + lane;       // 16-byte chunk index within the tile
+      const int row = slot / CR;
+      const int pc = slot % CR;               // physical chunk
+      const int key = min(ks0 + row, seq_end - 1);
+      const uint16_t* kg = kbase + key * a.ks[2] + ((pc ^ swz_k<CR>(row)) * 8);
+      const uint16_t* vg = vbase + key * a.vs[2] + ((pc ^ swz_v<CR>(row)) * 8);
+      __builtin_amdgcn_global_load_lds(kg, (lds_void_t*)(kt + blk * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vg, (lds_void_t*)(vt + blk * 1024), 16, 0, 0);
     }
   };
 
+  const int krow = sigma(col);  // K row (within a 32-key block) this lane supplies
   f32x16_t o[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) o[db] = f32x16_t{};
-  float m_run = -__builtin_inff();
-  float l_run = 0.0f;
+  float m_run = -__builtin_inff();  // running max (log2-scaled units), may lag the true max by <= 8
+  float l_run = 0.0f;               // this lane's partial denominator
 
-  load_tile(0);
-  store_tile(0);
+  issue_tile(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  const int krow_a = sigma(col);  // K row this lane supplies as MFMA A operand
   for (int t = 0; t < ntiles; ++t) {
-    const int stage = t & 1;
-    if (t + 1 < ntiles) load_tile(t + 1);
+    const int buf = t & 1;
+    if (t + 1 < ntiles) issue_tile(t + 1, buf ^ 1);
+    const unsigned char* kt = smem + buf * C::kStageBytes;
+    const unsigned char* vt = kt + C::kTileBytes;
     const int ks0 = seq_start + t * kBlockN;
-    const uint16_t* ks_l = smem + stage * T::kStage;
-    const uint16_t* vt_l = ks_l + T::kKElems;
 
-    // Tiles entirely after this wavefront's last query carry no visible key.
-    if (ks0 <= qw0 + kBlockM - 1) {
-      // S^T for keys ks0 + [0,32) and ks0 + [32,64)
-      f32x16_t s[2];
+    // S^T for this wavefront's 32-key block(s) of the tile
+    f32x16_t s[C::kBlocks];
 #pragma unroll
-      for (int blk = 0; blk < 2; ++blk) {
-        s[blk] = f32x16_t{};
-        const uint16_t* kr = ks_l + (blk * 32 + krow_a) * T::kRow + half * 8;
+    for (int bl = 0; bl < C::kBlocks; ++bl) {
+      const int row = (kh * C::kBlocks + bl) * 32 + krow;
+      const unsigned char* kr = kt + row * CR * 16;
+      const int sw = swz_k<CR>(row);
+      bf16x8_t kf[D / 16];
 #pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk) {
-          const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(kr + kk * 16);
-          s[blk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, qf[kk], s[blk], 0, 0, 0);
-        }
-      }
-      // scale (log2 domain) + causal / end-of-sequence mask
-      const bool need_mask = (ks0 + kBlockN - 1 > qw0) || (ks0 + kBlockN > seq_end);
-      float mx = -__builtin_inff();
+      for (int kk = 0; kk < D / 16; ++kk)
+        kf[kk] = *reinterpret_cast<const bf16x8_t*>(kr + (((2 * kk + half) ^ sw) * 16));
+      s[bl] = f32x16_t{};
 #pragma unroll
-      for (int blk = 0; blk < 2; ++blk) {
+      for (int kk = 0; kk < D / 16; ++kk)
+        s[bl] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kk], qf[kk], s[bl], 0, 0, 0);
+    }
+
+    // causal / end-of-sequence mask on diagonal and tail tiles only
+    const int kb0 = ks0 + kh * C::kBlocks * 32;  // first key of this wavefront's part
+    if (kb0 + C::kBlocks * 32 - 1 > qw0 || kb0 + C::kBlocks * 32 > seq_end) {
+#pragma unroll
+      for (int bl = 0; bl < C::kBlocks; ++bl)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float x = s[blk][r] * a.scale_log2;
-          if (need_mask) {
-            const int key = ks0 + blk * 32 + (r >> 3) * 16 + half * 8 + (r & 7);
-            if (key > qpos || key >= seq_end) x = -__builtin_inff();
-          }
-          s[blk][r] = x;
-          mx = fmaxf(mx, x);
+          const int key = kb0 + bl * 32 + (r >> 3) * 16 + half * 8 + (r & 7);
+          if (key > qpos || key >= seq_end) s[bl][r] = -__builtin_inff();
         }
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx);
-      // m_new is finite: the first tile always holds key seq_start <= qpos.
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      m_run = m_new;
-      float psum = 0.0f;
-      bf16x8_t pb[4];
+    }
+
+    // online softmax (exp2 domain, lazily raised max)
+    float mx = -__builtin_inff();
 #pragma unroll
-      for (int blk = 0; blk < 2; ++blk) {
+    for (int bl = 0; bl < C::kBlocks; ++bl)
 #pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          f32x8_t pv;
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[bl][r]);
+    mx = half_max(mx) * c;
+    const bool grow = mx > m_run + 8.0f;
+    const float m_new = grow ? mx : m_run;
+    const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+    const float m_sub = (m_new == -__builtin_inff()) ? 0.0f : m_new;  // fully masked so far: p = 0
+    m_run = m_new;
+    float psum = 0.0f;
+    bf16x8_t pb[2 * C::kBlocks];
 #pragma unroll
-          for (int r = 0; r < 8; ++r) {
-            const float p = __builtin_amdgcn_exp2f(s[blk][h2 * 8 + r] - m_new);
-            psum += p;
-            pv[r] = p;
-          }
-          pb[blk * 2 + h2] = __builtin_convertvector(pv, bf16x8_t);
+    for (int bl = 0; bl < C::kBlocks; ++bl) {
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        f32x8_t pv;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[bl][h2 * 8 + r], c, -m_sub));
+          psum += p;
+          pv[r] = p;
         }
-      }
-      l_run = l_run * alpha + psum;
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db) o[db] *= alpha;
-      // O^T += V^T · P^T over four 16-key slices
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db) {
-        const uint16_t* vr = vt_l + (db * 32 + col) * T::kVtRow + half * 8;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(vr + c * 16);
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pb[c], o[db], 0, 0, 0);
-        }
+        pb[bl * 2 + h2] = __builtin_convertvector(pv, bf16x8_t);
       }
     }
-    if (t + 1 < ntiles) store_tile(stage ^ 1);
+    l_run = l_run * alpha + psum;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) o[db] *= alpha;
+    }
+
+    // O^T += V^T · P^T: the V^T A operand of each 16-key slice comes from two
+    // transposing reads of the row-major V tile (keys +0..3 and +4..7)
+    const int grp = lane >> 4;
+    const int li = lane & 15;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      const int dim = db * 32 + 16 * (grp & 1) + 4 * (li & 3);
+      const int dchunk = dim >> 3;
+      const int doff = (dim & 7) * 2;
+#pragma unroll
+      for (int cs = 0; cs < 2 * C::kBlocks; ++cs) {
+        const int slice = (kh * C::kBlocks) * 2 + cs;  // 16-key slice within the tile
+        v4i16_t part[2];
+#pragma unroll
+        for (int r2 = 0; r2 < 2; ++r2) {
+          const int row = slice * 16 + 8 * (grp >> 1) + 4 * r2 + (li >> 2);
+          const unsigned char* addr = vt + row * CR * 16 + ((dchunk ^ swz_v<CR>(row)) * 16) + doff;
+          part[r2] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(addr));
+        }
+        const v4i16_t lo = part[0], hi = part[1];
+        const short __attribute__((ext_vector_type(8))) vv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vv), pb[cs], o[db], 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's copies of tile t+1 have landed
     __syncthreads();
   }
 
-  // ---- epilogue: O = O^T / denominator, 4 consecutive dims per 8-byte store
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  // ---- merge the key parts of each (head, query block), then normalise and store
+  if (KSPLIT > 1) {
+    float* cmb = reinterpret_cast<float*>(smem) + (w4 * 64 + lane) * (D / 2 + 2);
+    if (kh == 1) {
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) cmb[db * 16 + r] = o[db][r];
+      cmb[D / 2] = m_run;
+      cmb[D / 2 + 1] = l_run;
+    }
+    __syncthreads();
+    if (kh == 1) return;
+    const float m1 = cmb[D / 2];
+    const float l1 = cmb[D / 2 + 1];
+    const float m = fmaxf(m_run, m1);
+    const float a0 = (m_run == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
+    const float a1 = (m1 == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m1 - m);
+    l_run = l_run * a0 + l1 * a1;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * a0 + cmb[db * 16 + r] * a1;
+  }
+  const float l_tot = half_sum(l_run);
   const float inv = 1.0f / l_tot;
   if (qvalid) {
     uint16_t* orow = obase + qpos * a.os[2];
@@ -298,10 +350,9 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(GqaArgs a) {
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         const int d = db * 32 + r4 * 8 + half * 4;
-        uint2 w;
-        w.x = fd_pack2(o[db][r4 * 4 + 0] * inv, o[db][r4 * 4 + 1] * inv);
-        w.y = fd_pack2(o[db][r4 * 4 + 2] * inv, o[db][r4 * 4 + 3] * inv);
-        *reinterpret_cast<uint2*>(orow + d) = w;
+        f32x4_t v4 = {o[db][r4 * 4 + 0] * inv, o[db][r4 * 4 + 1] * inv, o[db][r4 * 4 + 2] * inv,
+                      o[db][r4 * 4 + 3] * inv};
+        *reinterpret_cast<bf16x4_t*>(orow + d) = __builtin_convertvector(v4, bf16x4_t);
       }
     }
   }
@@ -376,8 +427,8 @@ extern "C" int fd_gqa_fwd(const void* q, const void* k, const void* v, void* out
   a.scale_log2 = scale * 1.4426950408889634f;
   a.cu = cu_seqlens;
   a.n_seqs = n_seqs;
-  a.hpw = gcd_int(group, kWaves);
-  a.qpw = kWaves / a.hpw;
+  a.hpw = gcd_int(group, 4);
+  a.qpw = 4 / a.hpw;
   a.n_qtiles = (span_len + kBlockM * a.qpw - 1) / (kBlockM * a.qpw);
   a.n_hgroups = q_heads / a.hpw;
   const int64_t items = static_cast<int64_t>(a.n_qtiles) * a.n_hgroups * n_slots;
@@ -385,11 +436,17 @@ extern "C" int fd_gqa_fwd(const void* q, const void* k, const void* v, void* out
   a.n_items = static_cast<int>(items);
   const int nblocks = static_cast<int>((items + kNumXcd - 1) / kNumXcd * kNumXcd);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  dim3 grid(nblocks), block(kThreads);
+  dim3 grid(nblocks);
   switch (head_dim) {
-    case 64: hipLaunchKernelGGL(gqa_fwd_kernel<64>, grid, block, 0, s, a); break;
-    case 128: hipLaunchKernelGGL(gqa_fwd_kernel<128>, grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL(gqa_fwd_kernel<256>, grid, block, 0, s, a); break;
+    case 64:
+      hipLaunchKernelGGL((gqa_fwd_kernel<64, 2>), grid, dim3(Cfg<64, 2>::kThreads), 0, s, a);
+      break;
+    case 128:
+      hipLaunchKernelGGL((gqa_fwd_kernel<128, 2>), grid, dim3(Cfg<128, 2>::kThreads), 0, s, a);
+      break;
+    default:
+      hipLaunchKernelGGL((gqa_fwd_kernel<256, 1>), grid, dim3(Cfg<256, 1>::kThreads), 0, s, a);
+      break;
   }
   return fd_check_launch("fd_gqa_fwd");
 }

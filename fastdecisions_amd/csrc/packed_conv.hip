@@ -18,10 +18,10 @@
 // were loaded by its predecessor into the same XCD's L2.
 //
 // fp32 sequence per output (the CPU restatement reproduces it bit for bit):
-//   acc = w[W-1]*x[t]; acc = acc + w[0]*x[t-W+1]; ...; acc = acc + w[W-2]*x[t-1]
+//   acc = w[W-1]*x[t]; acc = fma(w[0], x[t-W+1], acc); ...; acc = fma(w[W-2], x[t-1], acc)
 //   (+ bias), then y = acc / (1 + exp(-acc)) for SiLU, one bf16 rounding.
-// Products of two bf16 values are exact in fp32, so this equals the
-// reference's fused multiply-add chain (ref: :139-177).
+// The tap order is the reference's (ref: :139-177); a product of two bf16
+// values is exact in fp32, so each fma equals the multiply-then-add there.
 #include "fd_common.h"
 
 namespace {
@@ -50,7 +50,7 @@ __device__ __forceinline__ uint4 load16(const uint16_t* p) { return *reinterpret
 // runs on XCD b % 8; logical block L = (b % 8) * (nblocks / 8) + b / 8, so the
 // logical blocks of one XCD are contiguous: all channel columns of a run, then
 // the next run.
-template <int WIDTH, int RUN, bool SILU>
+template <int WIDTH, int RUN, bool SILU, bool HAS_BIAS>
 __global__ __launch_bounds__(kThreads) void packed_conv_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias,
     uint16_t* __restrict__ q, uint16_t* __restrict__ k, uint16_t* __restrict__ v, int total_rows, int seq_len,
@@ -86,8 +86,7 @@ __global__ __launch_bounds__(kThreads) void packed_conv_kernel(
     }
   }
   Vec8 bs;
-  const bool has_bias = bias != nullptr;
-  if (has_bias) bs = unpack8(load16(bias + c0));
+  if (HAS_BIAS) bs = unpack8(load16(bias + c0));
 
   // Sequence containing r0: [seg_start, seg_end).  For varlen, seg is the
   // largest index in [0, n_seqs) with cu_seqlens[seg] <= r0.
@@ -162,11 +161,8 @@ __global__ __launch_bounds__(kThreads) void packed_conv_kernel(
         const int e = 2 * p + h;
         float acc = wt[WIDTH - 1][e] * xc.v[e];
 #pragma unroll
-        for (int j = 0; j < WIDTH - 1; ++j) {
-          const float prod = wt[j][e] * win[j].v[e];
-          acc = acc + prod;
-        }
-        if (has_bias) acc = acc + bs.v[e];
+        for (int j = 0; j < WIDTH - 1; ++j) acc = __builtin_fmaf(wt[j][e], win[j].v[e], acc);
+        if (HAS_BIAS) acc = acc + bs.v[e];
         y2[h] = SILU ? fd_silu(acc) : acc;
       }
       o[p] = fd_pack2(y2[0], y2[1]);
@@ -196,16 +192,24 @@ int launch_run(const void* x, const void* w, const void* bias, void* q, void* k,
   auto qs = static_cast<uint16_t*>(q);
   auto ks = static_cast<uint16_t*>(k);
   auto vs = static_cast<uint16_t*>(v);
-  if (act == FD_ACT_SILU)
-    hipLaunchKernelGGL((packed_conv_kernel<WIDTH, RUN, true>), grid, block, 0, stream, xs, ws, bsp, qs, ks, vs,
-                       total_rows, seq_len, key_dim, value_dim, cu, n_seqs, n_runs, n_col);
-  else
-    hipLaunchKernelGGL((packed_conv_kernel<WIDTH, RUN, false>), grid, block, 0, stream, xs, ws, bsp, qs, ks, vs,
-                       total_rows, seq_len, key_dim, value_dim, cu, n_seqs, n_runs, n_col);
+#define FD_CONV_LAUNCH(SILU, BIAS)                                                                         \
+  hipLaunchKernelGGL((packed_conv_kernel<WIDTH, RUN, SILU, BIAS>), grid, block, 0, stream, xs, ws, bsp, qs, ks, vs, \
+                     total_rows, seq_len, key_dim, value_dim, cu, n_seqs, n_runs, n_col)
+  const bool silu = act == FD_ACT_SILU;
+  if (silu && bsp == nullptr) FD_CONV_LAUNCH(true, false);
+  else if (silu) FD_CONV_LAUNCH(true, true);
+  else if (bsp == nullptr) FD_CONV_LAUNCH(false, false);
+  else FD_CONV_LAUNCH(false, true);
+#undef FD_CONV_LAUNCH
   return fd_check_launch("fd_packed_conv_fwd");
 }
 
-constexpr int kRun = 16;
+#ifndef FD_CONV_RUN
+#define FD_CONV_RUN 8
+#endif
+// Tokens per thread: 8 gives 3 wavefronts per SIMD at B=1, T=2048, C=6144
+// (balanced over the 1024 SIMDs) for a 3/8 halo re-read from L2.
+constexpr int kRun = FD_CONV_RUN;
 
 }  // namespace
 

@@ -1,0 +1,89 @@
+"""``fastdecisions::native_gqa`` torch op and the attention-layer patch that uses it.
+
+The reference defines this op and its patched ``Qwen3_5Attention.forward``
+inside its model benchmark (ref: experiments/native_gqa/bench_native_gqa_model.py:34-56);
+here they are part of the package:
+
+* ``native_gqa`` — functional op ``(q, k, v) -> out`` over the HIP kernel, with a
+  fake implementation that states the permuted ``[B, T, H, D]`` output
+  (ref: :38-41), so it is one node under ``torch.compile`` and capturable in a
+  HIP graph;
+* ``native_gqa_varlen`` — the same over packed requests (``cu_seqlens``);
+* ``install_native_gqa(core)`` — binds ``candidate_forward`` on every
+  ``Qwen3_5Attention`` of a model and returns the count.  Unsupported calls
+  (KV cache, training, grad, non-CUDA, non-bf16) fall back to the original
+  forward, as the other install patches of the reference do
+  (ref: src/decider/packed_conv.py:27-38).
+"""
+from __future__ import annotations
+
+from types import MethodType
+
+import torch
+
+from .native_gqa_kernel import native_gqa_attention
+
+
+@torch.library.custom_op("fastdecisions::native_gqa", mutates_args=(), device_types="cuda")
+def native_gqa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    return native_gqa_attention(q, k, v)
+
+
+@native_gqa.register_fake
+def _native_gqa_fake(q, k, v):
+    b, h, t, d = q.shape
+    return q.new_empty((b, t, h, d)).permute(0, 2, 1, 3)
+
+
+@torch.library.custom_op("fastdecisions::native_gqa_varlen", mutates_args=(), device_types="cuda")
+def native_gqa_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
+                      max_seqlen: int) -> torch.Tensor:
+    return native_gqa_attention(q, k, v, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen)
+
+
+@native_gqa_varlen.register_fake
+def _native_gqa_varlen_fake(q, k, v, cu_seqlens, max_seqlen):
+    b, h, t, d = q.shape
+    return q.new_empty((b, t, h, d)).permute(0, 2, 1, 3)
+
+
+def candidate_forward(self, hidden_states, position_embeddings, attention_mask=None, past_key_values=None,
+                      **kwargs):
+    """Qwen3_5Attention.forward with the attention itself on the HIP kernel
+    (ref: experiments/native_gqa/bench_native_gqa_model.py:43-56).  The causal
+    mask is applied in-kernel; ``attention_mask`` must describe plain causal
+    attention over right-padded rows (the engine's contract, ref: src/decider/engine.py:3-5)."""
+    if (past_key_values is not None or self.training or torch.is_grad_enabled()
+            or not hidden_states.is_cuda or hidden_states.dtype != torch.bfloat16
+            or self.head_dim not in (64, 128, 256)):
+        return self._native_gqa_original_forward(hidden_states, position_embeddings, attention_mask,
+                                                 past_key_values=past_key_values, **kwargs)
+    from transformers.models.qwen3_5.modeling_qwen3_5 import apply_rotary_pos_emb
+    shape = hidden_states.shape[:-1]
+    heads_shape = (*shape, -1, self.head_dim)
+    q, gate = torch.chunk(self.q_proj(hidden_states).view(*shape, -1, self.head_dim * 2), 2, dim=-1)
+    gate = gate.reshape(*shape, -1)
+    q = self.q_norm(q.reshape(heads_shape)).transpose(1, 2)
+    k = self.k_norm(self.k_proj(hidden_states).view(heads_shape)).transpose(1, 2)
+    v = self.v_proj(hidden_states).view(heads_shape).transpose(1, 2)
+    q, k = apply_rotary_pos_emb(q, k, *position_embeddings)
+    cu_seqlens = kwargs.get("cu_seq_lens_q")
+    if cu_seqlens is not None:
+        out = native_gqa_varlen(q, k, v, cu_seqlens, int(kwargs["max_length_q"]))
+    else:
+        out = native_gqa(q, k, v)
+    out = out.transpose(1, 2).reshape(*shape, -1)
+    return self.o_proj(out * torch.sigmoid(gate)), None
+
+
+def install_native_gqa(core) -> int:
+    """Patch every Qwen3_5Attention of this model instance; return the number patched."""
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5Attention
+    count = 0
+    for module in core.modules():
+        if isinstance(module, Qwen3_5Attention):
+            if not hasattr(module, "_native_gqa_original_forward"):
+                module._native_gqa_original_forward = module.forward
+                module.forward = MethodType(candidate_forward, module)
+            count += 1
+    return count

@@ -1,0 +1,116 @@
+"""``fastdecisions::packed_conv`` torch op and the Gated-DeltaNet patch that uses it.
+
+Mirrors ref: src/decider/packed_conv.py:
+
+* ``packed_conv(x, weight) -> (q, k, v)`` — functional op over ``prep_qkv`` with
+  a fake that states the ``[B, T, 16, 128]`` outputs (ref: :12-21);
+  ``packed_conv_varlen`` adds ``cu_seqlens`` for packed requests;
+* ``_forward`` — replacement ``Qwen3_5GatedDeltaNet.forward`` (ref: :24-62):
+  ``in_proj_qkv`` -> packed conv straight into head-split q/k/v -> gates ->
+  gated delta rule -> gated RMSNorm -> ``out_proj``; falls back to the original
+  method for caches, training, grad, non-CUDA/non-bf16 inputs and other
+  geometries (ref: :27-38).  The reference also requires T == 2048; any T works here;
+* ``install_packed_conv(core)`` — binds it on every ``Qwen3_5GatedDeltaNet``
+  and returns the count (ref: :65-75).
+
+With packed requests (``cu_seq_lens_q`` in kwargs) the conv restarts its
+window at every request start, and the gated delta rule — whose eager torch
+form ignores ``cu_seqlens`` (transformers' torch_chunk_gated_delta_rule) — is
+run once per request, so no state crosses a request boundary.
+"""
+from __future__ import annotations
+
+from types import MethodType
+
+import torch
+import torch.nn.functional as F
+
+from .packed_conv_kernel import prep_qkv
+
+
+@torch.library.custom_op("fastdecisions::packed_conv", mutates_args=(), device_types="cuda")
+def packed_conv(x: torch.Tensor, weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    return prep_qkv(x, weight)
+
+
+@packed_conv.register_fake
+def _packed_conv_fake(x, weight):
+    batch, seq, channels = x.shape
+    shape = (batch, seq, channels // 3 // 128, 128)
+    return tuple(x.new_empty(shape) for _ in range(3))
+
+
+@torch.library.custom_op("fastdecisions::packed_conv_varlen", mutates_args=(), device_types="cuda")
+def packed_conv_varlen(x: torch.Tensor, weight: torch.Tensor,
+                       cu_seqlens: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    return prep_qkv(x, weight, cu_seqlens=cu_seqlens)
+
+
+@packed_conv_varlen.register_fake
+def _packed_conv_varlen_fake(x, weight, cu_seqlens):
+    batch, seq, channels = x.shape
+    shape = (batch, seq, channels // 3 // 128, 128)
+    return tuple(x.new_empty(shape) for _ in range(3))
+
+
+def _segments(kwargs):
+    """Host-side request boundaries of a packed batch (a list of (start, end)), or None."""
+    bounds = kwargs.get("fd_segments")
+    return None if bounds is None else list(bounds)
+
+
+def _forward(self, hidden_states, cache_params=None, attention_mask=None, **kwargs):
+    # The original method owns caches, training and other geometries (ref: src/decider/packed_conv.py:25-38).
+    if (cache_params is not None or self.training or torch.is_grad_enabled()
+            or not hidden_states.is_cuda or hidden_states.dtype != torch.bfloat16
+            or self.key_dim != self.value_dim or self.num_k_heads != self.num_v_heads
+            or self.head_k_dim != 128 or self.head_v_dim != 128
+            or self.conv1d.weight.shape != (3 * self.key_dim, 1, self.conv_kernel_size)
+            or not 1 <= self.conv_kernel_size <= 4
+            or self.conv1d.bias is not None or self.activation != "silu"):
+        return self._packed_original_forward(hidden_states, cache_params=cache_params,
+                                             attention_mask=attention_mask, **kwargs)
+
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as mq
+    hidden_states = mq.apply_mask_to_padding_states(hidden_states, attention_mask)
+    batch, seq, _ = hidden_states.shape
+    mixed = self.in_proj_qkv(hidden_states)
+    cu_seqlens = kwargs.get("cu_seq_lens_q")
+    if cu_seqlens is not None:
+        query, key, value = packed_conv_varlen(mixed, self.conv1d.weight, cu_seqlens)
+    else:
+        query, key, value = packed_conv(mixed, self.conv1d.weight)
+    z = self.in_proj_z(hidden_states).reshape(batch, seq, -1, self.head_v_dim)
+    b = self.in_proj_b(hidden_states)
+    a = self.in_proj_a(hidden_states)
+    beta = b.sigmoid()
+    g = -self.A_log.float().exp() * F.softplus(a.float() + self.dt_bias)
+    segments = _segments(kwargs)
+    if segments is None:
+        core_attn_out, _ = mq.torch_chunk_gated_delta_rule(
+            query, key, value, g=g, beta=beta, initial_state=None, output_final_state=False,
+            use_qk_l2norm_in_kernel=True)
+    else:
+        parts = []
+        for s, e in segments:
+            if e > s:
+                out, _ = mq.torch_chunk_gated_delta_rule(
+                    query[:, s:e], key[:, s:e], value[:, s:e], g=g[:, s:e], beta=beta[:, s:e],
+                    initial_state=None, output_final_state=False, use_qk_l2norm_in_kernel=True)
+                parts.append(out)
+        core_attn_out = torch.cat(parts, dim=1)
+    core_attn_out = self.norm(core_attn_out.reshape(-1, self.head_v_dim), z.reshape(-1, self.head_v_dim))
+    return self.out_proj(core_attn_out.reshape(batch, seq, -1))
+
+
+def install_packed_conv(core) -> int:
+    """Patch this model's Gated-DeltaNet modules only; return the number installed (ref: :65-75)."""
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5GatedDeltaNet
+    count = 0
+    for module in core.modules():
+        if isinstance(module, Qwen3_5GatedDeltaNet):
+            if not hasattr(module, "_packed_original_forward"):
+                module._packed_original_forward = module.forward
+                module.forward = MethodType(_forward, module)
+            count += 1
+    return count

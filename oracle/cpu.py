@@ -22,8 +22,8 @@ def _lib() -> ctypes.CDLL:
             _build.build()
         lib = ctypes.CDLL(str(_LIB_PATH))
         p = ctypes.c_void_p
-        lib.fd_oracle_expf.restype = ctypes.c_float
-        lib.fd_oracle_expf.argtypes = [ctypes.c_float]
+        lib.fd_oracle_exp_silu.restype = ctypes.c_float
+        lib.fd_oracle_exp_silu.argtypes = [ctypes.c_float]
         lib.fd_oracle_silu.restype = ctypes.c_float
         lib.fd_oracle_silu.argtypes = [ctypes.c_float]
         lib.fd_oracle_f32_to_bf16.restype = ctypes.c_uint16
@@ -56,9 +56,14 @@ def f32_to_bf16(x: np.ndarray) -> np.ndarray:
     return r
 
 
-def expf(x: float) -> float:
-    """The fp32 exp of the conv's SiLU (Cody–Waite + degree-7 Taylor)."""
-    return _lib().fd_oracle_expf(float(x))
+def exp_silu(t: float) -> float:
+    """The fp32 e^t of the conv's SiLU (t clamped to [-20, 89], Cody–Waite + degree-7 Taylor)."""
+    return _lib().fd_oracle_exp_silu(float(t))
+
+
+def silu(y: float) -> float:
+    """The conv's fp32 SiLU, y / (1 + e^-y)."""
+    return _lib().fd_oracle_silu(float(y))
 
 
 # ------------------------------------------------------------- packed conv

@@ -51,18 +51,19 @@ uint16_t fd_oracle_f32_to_bf16(float f) {
   return (uint16_t)(u >> 16);
 }
 
-/* exp(x): Cody–Waite reduction x = k ln2 + r with ln2 split into a head of 16
- * significant bits and a tail, degree-7 Taylor polynomial of e^r in Horner
- * form, exact scaling by 2^k (two steps into the subnormal range). */
-float fd_oracle_expf(float x) {
-  if (x != x) return x;
-  if (x > 88.72283935546875f) return bits_f32(0x7f800000u);
-  if (x < -103.972084045410156f) return 0.0f;
+/* e^t as the conv's SiLU computes it: t clamped to [-20, 89]; Cody–Waite
+ * reduction t = k ln2 + r with ln2 split into a head of 16 significant bits and
+ * a tail; degree-7 Taylor polynomial of e^r in Horner form; exact scaling by
+ * 2^k (k in [-29, 129]).  Every step is one IEEE fp32 operation.  The clamp is
+ * invisible to the SiLU: below -17.4, 1 + e^t == 1 in fp32; above 88.73, e^t
+ * overflows to +inf either way. */
+float fd_oracle_exp_silu(float t) {
   const float log2e = 1.44269502162933349609375f;
   const float ln2_hi = 0.693145751953125f;
   const float ln2_lo = 1.428606765330187045e-06f;
-  float k = rintf(x * log2e);
-  float r = fmaf(-k, ln2_hi, x);
+  t = fminf(fmaxf(t, -20.0f), 89.0f);
+  float k = rintf(t * log2e);
+  float r = fmaf(-k, ln2_hi, t);
   r = fmaf(-k, ln2_lo, r);
   float p = 1.0f / 5040.0f;
   p = fmaf(p, r, 1.0f / 720.0f);
@@ -72,13 +73,11 @@ float fd_oracle_expf(float x) {
   p = fmaf(p, r, 0.5f);
   p = fmaf(p, r, 1.0f);
   p = fmaf(p, r, 1.0f);
-  int ki = (int)k;
-  if (ki > 127) return (p * 1.7014118346046923e38f) * bits_f32((uint32_t)(ki) << 23);
-  if (ki < -126) return (p * bits_f32((uint32_t)(ki + 64 + 127) << 23)) * 5.421010862427522e-20f;
-  return p * bits_f32((uint32_t)(ki + 127) << 23);
+  return ldexpf(p, (int)k);
 }
 
-float fd_oracle_silu(float y) { return y / (1.0f + fd_oracle_expf(-y)); }
+/* SiLU as the reference writes it, y / (1 + exp(-y)) (ref: src/decider/packed_conv_kernel.py:178-182). */
+float fd_oracle_silu(float y) { return y / (1.0f + fd_oracle_exp_silu(-y)); }
 
 /* Packed causal depthwise conv1d + activation, token-major [B, T, C] input,
  * C = 2*key_dim + value_dim, weight [C, width], optional bias [C].
@@ -106,8 +105,7 @@ int fd_oracle_packed_conv(const uint16_t* x, const uint16_t* w, const uint16_t* 
       for (int j = 0; j < width - 1; ++j) {
         const int64_t src = r - (width - 1) + j;
         const float xv = src >= start ? bf16_to_f32(x[(size_t)src * C + c]) : 0.0f;
-        const float prod = wt[j] * xv;
-        acc = acc + prod;
+        acc = fmaf(wt[j], xv, acc);
       }
       if (bias) acc = acc + bf16_to_f32(bias[c]);
       const float y = activation == 1 ? fd_oracle_silu(acc) : acc;

@@ -1,0 +1,106 @@
+"""TEST INFRASTRUCTURE — the reference PyTorch path timed on host CPU cores.
+
+Used only by bench.py's cpu_baseline leg.  Every function runs the eager
+PyTorch recipe that the GPU kernels replace, on the CPU, and returns the
+median wall time of repeated runs after warm-up:
+
+* ``gqa_config1`` — BASELINE config 1 exactly: B=1, T=1024, 16 q / 4 kv heads,
+  D=128, fp32, q/k/v ~ N(0,1)/sqrt(128) drawn in that order from seed 0;
+  ``F.scaled_dot_product_attention(q, repeat_kv(k,4), repeat_kv(v,4), is_causal=True)``;
+* ``conv_config2`` — fp32 depthwise ``F.conv1d`` + SiLU on [1, 2048, 6144];
+* ``rmsnorm_config3`` — eager ``residual + x`` and Qwen3.5 RMSNorm on [4, 2048, 2048];
+* ``decider_forward_sample`` — the eager decider forward (transformers' Qwen3.5
+  layers: SDPA, F.conv1d, eager RMSNorm, torch gated-delta rule) at B=1,
+  T=2048 in fp32 over a bounded slice of the 28 layers, scaled to the whole
+  forward.
+"""
+from __future__ import annotations
+
+import os
+import platform
+import statistics
+import time
+
+import torch
+import torch.nn.functional as F
+
+
+def cpu_info() -> dict:
+    model = platform.processor() or ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return dict(cores_visible=len(os.sched_getaffinity(0)), torch_threads=torch.get_num_threads(), cpu_model=model)
+
+
+def _median_ms(fn, warmup: int, runs: int) -> float:
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(times)
+
+
+@torch.no_grad()
+def gqa_config1(warmup: int = 3, runs: int = 10) -> float:
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn((1, 16, 1024, 128), generator=g) / 128 ** 0.5
+    k = torch.randn((1, 4, 1024, 128), generator=g) / 128 ** 0.5
+    v = torch.randn((1, 4, 1024, 128), generator=g) / 128 ** 0.5
+
+    def run():
+        kr = k[:, :, None].expand(1, 4, 4, 1024, 128).reshape(1, 16, 1024, 128)
+        vr = v[:, :, None].expand(1, 4, 4, 1024, 128).reshape(1, 16, 1024, 128)
+        return F.scaled_dot_product_attention(q, kr, vr, is_causal=True)
+    return _median_ms(run, warmup, runs)
+
+
+@torch.no_grad()
+def conv_config2(warmup: int = 3, runs: int = 10) -> float:
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn((1, 2048, 6144), generator=g).to(torch.bfloat16)
+    w = (torch.randn((6144, 4), generator=g) * 0.25).to(torch.bfloat16)
+
+    def run():
+        y = F.conv1d(x.float().transpose(1, 2), w.float()[:, None], padding=3, groups=6144)[..., :2048]
+        y = F.silu(y).transpose(1, 2).to(torch.bfloat16)
+        return [t.contiguous().view(1, 2048, 16, 128) for t in y.split(2048, dim=-1)]
+    return _median_ms(run, warmup, runs)
+
+
+@torch.no_grad()
+def rmsnorm_config3(warmup: int = 3, runs: int = 10) -> float:
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn((4, 2048, 2048), generator=g).to(torch.bfloat16)
+    r = torch.randn((4, 2048, 2048), generator=g).to(torch.bfloat16)
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5RMSNorm
+    norm = Qwen3_5RMSNorm(2048, eps=1e-6)
+    norm.weight.data = (torch.randn((2048,), generator=g) * 0.02).to(torch.bfloat16)
+
+    def run():
+        h = r + x
+        return norm(h), h
+    return _median_ms(run, warmup, runs)
+
+
+@torch.no_grad()
+def decider_forward_sample(layers: int = 4, seq_len: int = 2048, warmup: int = 1, runs: int = 3) -> dict:
+    """Eager fp32 forward of the first ``layers`` decoder layers (3 Gated-DeltaNet + 1 GQA
+    for 4) of the decider-2b-shaped model, plus embedding, final norm and readout; the
+    per-layer time is scaled to 28 layers (21 linear-attention + 7 full-attention)."""
+    from dataclasses import replace
+
+    from fastdecisions_amd.model import DECIDER_2B_SHAPED, build_decider, synthetic_ids
+    shape = replace(DECIDER_2B_SHAPED, num_hidden_layers=layers)
+    model = build_decider(shape, seed=0, device="cpu", dtype=torch.float32)
+    ids = synthetic_ids(1, seq_len, shape.vocab_size, seed=1, device="cpu")
+    ms = _median_ms(lambda: model(ids), warmup, runs)
+    scale = DECIDER_2B_SHAPED.num_hidden_layers / layers
+    return dict(sample_ms=ms, scaled_forward_ms=ms * scale, layers=layers, scale=scale)

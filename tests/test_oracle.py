@@ -21,25 +21,31 @@ def concat_qkv(q, k, v):
 
 # ------------------------------------------------------------------ exp / SiLU
 
-def test_expf_accuracy_over_full_range(oracle):
-    xs = np.concatenate([np.linspace(-103.9, 88.7, 40001), np.linspace(-1, 1, 2001)]).astype(np.float32)
-    got = np.array([oracle.expf(float(x)) for x in xs], np.float64)
+def test_exp_accuracy_over_the_silu_range(oracle):
+    xs = np.concatenate([np.linspace(-20, 88.7, 40001), np.linspace(-1, 1, 2001)]).astype(np.float32)
+    got = np.array([oracle.exp_silu(float(x)) for x in xs], np.float64)
     ref = np.exp(xs.astype(np.float64))
-    normal = (ref > 1.2e-38) & (ref < 3.4e38)
-    ulp = np.abs(got[normal] - ref[normal]) / (np.spacing(ref[normal].astype(np.float32)).astype(np.float64))
+    ulp = np.abs(got - ref) / np.spacing(ref.astype(np.float32)).astype(np.float64)
     assert ulp.max() < 2.0, ulp.max()
 
 
-def test_expf_special_values(oracle):
-    assert oracle.expf(0.0) == 1.0
-    assert oracle.expf(float("inf")) == float("inf")
-    assert oracle.expf(float("-inf")) == 0.0
-    assert np.isnan(oracle.expf(float("nan")))
-    assert oracle.expf(89.0) == float("inf")
-    assert oracle.expf(-110.0) == 0.0
-    # subnormal results are rounded once: within 1 subnormal ulp of the truth
-    for x in (-90.0, -100.0, -103.0):
-        assert abs(oracle.expf(x) - np.exp(x)) <= 2.0 ** -149
+def test_silu_special_values(oracle):
+    assert oracle.exp_silu(0.0) == 1.0
+    assert oracle.exp_silu(89.0) == float("inf")  # overflow, as an unclamped exp
+    assert oracle.silu(0.0) == 0.0
+    assert oracle.silu(100.0) == 100.0             # 1 + e^-100 == 1
+    assert oracle.silu(-100.0) == 0.0 and np.signbit(oracle.silu(-100.0))  # y / (1 + inf) = -0
+    assert np.isnan(oracle.silu(float("nan")))
+    # the clamp at -20 is invisible: 1 + e^t == 1 for every t below -17.4
+    for t in (-17.5, -20.0, -30.0, -103.0):
+        assert np.float32(1.0) + np.float32(oracle.exp_silu(t)) == np.float32(1.0)
+    # against fp64 on a dense grid: |error| <= 3 ulp of fp32 (exp <= 2 ulp, plus the roundings of
+    # 1 + e and of the division that the reference formula itself performs)
+    ys = np.linspace(-30, 30, 6001).astype(np.float32)
+    got = np.array([oracle.silu(float(y)) for y in ys], np.float64)
+    ref = ys.astype(np.float64) / (1 + np.exp(-ys.astype(np.float64)))
+    ok = np.abs(got - ref) <= 3 * np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64) + 1e-45
+    assert ok.all()
 
 
 # ------------------------------------------------------------------ packed conv
