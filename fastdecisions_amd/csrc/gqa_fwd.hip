@@ -81,8 +81,14 @@ struct Cfg {
   static constexpr int kTileBytes = kBlockN * kChunksRow * 16;
   static constexpr int kLoads = kBlockN * kChunksRow / kThreads;  // global_load_lds per thread per K (or V) tile
   static constexpr int kStageBytes = 2 * kTileBytes;         // K tile + V tile
+  // LDS ring depth: tile t+2 is in flight while tile t is consumed (3 stages
+  // where they fit next to the merge area, else 2)
+  static constexpr int kStages = 3 * kStageBytes <= 160 * 1024 ? 3 : 2;
   static constexpr int kCombineBytes = KSPLIT > 1 ? 4 * 64 * (D / 2 + 2) * 4 : 0;
-  static constexpr int kSmemBytes = (2 * kStageBytes > kCombineBytes) ? 2 * kStageBytes : kCombineBytes;
+  static constexpr int kSmemBytes =
+      (kStages * kStageBytes > kCombineBytes) ? kStages * kStageBytes : kCombineBytes;
+  // s_waitcnt immediate: vmcnt(N) with expcnt / lgkmcnt left alone (gfx9 encoding)
+  static constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
   static_assert(kLoads * kThreads == kBlockN * kChunksRow, "tile must split evenly over the threads");
 };
 
@@ -95,8 +101,8 @@ __device__ __forceinline__ int sigma(int m) {
 // Chunk swizzles (physical chunk = logical chunk ^ f(row)).  K: the MFMA A
 // operand reads rows sigma(0..7) = {0,1,2,3,8,9,10,11} (then +4) at one chunk;
 // a bit permutation of row & 15 sends any 8 of them to 8 distinct chunks.
-// V: a transposing read touches 4 consecutive rows x 2 adjacent chunks;
-// xor with 2*(row & 3) spreads them over 8 chunks and keeps pairs adjacent.
+// V: 16 lanes of a transposing read touch 4 consecutive rows x 2 adjacent
+// chunks, 32 lanes 4 rows x 4 chunks; the xor keeps chunk pairs adjacent.
 template <int CR>
 __device__ __forceinline__ int swz_k(int row) {
   const int r = row & 15;
@@ -104,7 +110,9 @@ __device__ __forceinline__ int swz_k(int row) {
 }
 template <int CR>
 __device__ __forceinline__ int swz_v(int row) {
-  return (2 * (row & 3)) & (CR - 1);
+  // 16+ chunks per row: xor with 4*(row & 3) puts the 4 rows x 4 chunks that
+  // 32 lanes of a transposing read touch on 16 distinct chunks (all banks).
+  return CR >= 16 ? 4 * (row & 3) : (2 * (row & 3)) & (CR - 1);
 }
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
@@ -188,59 +196,136 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
   const int kend = min(q0 + qspan, seq_end);
   const int ntiles = (kend - seq_start + kBlockN - 1) / kBlockN;
 
-  // ---- global -> LDS copies of one K tile and one V tile (rows past the end
-  // of the sequence re-read its last row: finite data the mask discards)
-  auto issue_tile = [&](int t, int buf) {
-    const int ks0 = seq_start + t * kBlockN;
-    unsigned char* kt = smem + buf * C::kStageBytes;
-    unsigned char* vt = kt + C::kTileBytes;
+  // ---- per-lane addressing, computed once.  LDS: [K stage 0..S-1][V stage
+  // 0..S-1]; K and V reads each use one base register plus an immediate
+  // stage offset (< 64 KiB), the loop being unrolled by the stage count.
+  unsigned char* const k_lds = smem;
+  unsigned char* const v_lds = smem + C::kStages * C::kTileBytes;
+  // global -> LDS copies: copy i of this lane moves 16-byte chunk `slot` of a
+  // tile (row = slot / CR, physical chunk = slot % CR, global chunk unswizzled)
+  auto cp_row = [&](int i) { return ((i * C::kWaves + wave) * 64 + lane) / CR; };
+  auto cp_koff = [&](int i) {
+    const int slot = (i * C::kWaves + wave) * 64 + lane;
+    return ((slot % CR) ^ swz_k<CR>(slot / CR)) * 8;
+  };
+  auto cp_voff = [&](int i) {
+    const int slot = (i * C::kWaves + wave) * 64 + lane;
+    return ((slot % CR) ^ swz_v<CR>(slot / CR)) * 8;
+  };
+  // K A operand: lane reads row (kh*kBlocks + bl)*32 + sigma(col), logical chunk 2kk + half.
+  // V^T A operand: two transposing reads per (dim block, 16-key slice).
+  // With two wavefronts per SIMD the byte offsets fit in registers and are
+  // computed once; the 4-wavefront head_dim-256 variant recomputes them.
+  const int grp = lane >> 4;
+  const int li = lane & 15;
+  auto k_off_calc = [&](int bl, int kk) {
+    const int row = (kh * C::kBlocks + bl) * 32 + sigma(col);
+    return row * CR * 16 + (((2 * kk + half) ^ swz_k<CR>(row)) * 16);
+  };
+  auto v_off_calc = [&](int db, int cs, int r2) {
+    const int dim = db * 32 + 16 * (grp & 1) + 4 * (li & 3);
+    const int row = ((kh * C::kBlocks) * 2 + cs) * 16 + 8 * (grp >> 1) + 4 * r2 + (li >> 2);
+    return row * CR * 16 + (((dim >> 3) ^ swz_v<CR>(row)) * 16) + (dim & 7) * 2;
+  };
+  constexpr bool kHoist = KSPLIT > 1;
+  int k_rd[kHoist ? C::kBlocks : 1][kHoist ? D / 16 : 1];
+  int v_rd[kHoist ? D / 32 : 1][kHoist ? 2 * C::kBlocks : 1][2];
+  if constexpr (kHoist) {
+#pragma unroll
+    for (int bl = 0; bl < C::kBlocks; ++bl)
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk) k_rd[bl][kk] = k_off_calc(bl, kk);
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int cs = 0; cs < 2 * C::kBlocks; ++cs)
+#pragma unroll
+        for (int r2 = 0; r2 < 2; ++r2) v_rd[db][cs][r2] = v_off_calc(db, cs, r2);
+  }
+  int cp_krel[kHoist ? C::kLoads : 1], cp_vrel[kHoist ? C::kLoads : 1];
+  if constexpr (kHoist) {
 #pragma unroll
     for (int i = 0; i < C::kLoads; ++i) {
-      const int blk = i * C::kWaves + wave;   // 1 KiB LDS block written by this instruction
-      const int slot = blk * 64 + lane;       // 16-byte chunk index within the tile
-      const int row = slot / CR;
-      const int pc = slot % CR;               // physical chunk
-      const int key = min(ks0 + row, seq_end - 1);
-      const uint16_t* kg = kbase + key * a.ks[2] + ((pc ^ swz_k<CR>(row)) * 8);
-      const uint16_t* vg = vbase + key * a.vs[2] + ((pc ^ swz_v<CR>(row)) * 8);
-      __builtin_amdgcn_global_load_lds(kg, (lds_void_t*)(kt + blk * 1024), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vg, (lds_void_t*)(vt + blk * 1024), 16, 0, 0);
+      cp_krel[i] = cp_row(i) * static_cast<int>(a.ks[2]) + cp_koff(i);
+      cp_vrel[i] = cp_row(i) * static_cast<int>(a.vs[2]) + cp_voff(i);
+    }
+  }
+  auto k_off = [&](int bl, int kk) {
+    if constexpr (kHoist) return k_rd[bl][kk]; else return k_off_calc(bl, kk);
+  };
+  auto v_off = [&](int db, int cs, int r2) {
+    if constexpr (kHoist) return v_rd[db][cs][r2]; else return v_off_calc(db, cs, r2);
+  };
+
+  // rows past the end of the sequence re-read its last row: finite data the mask discards
+  auto issue_tile = [&](int t, int buf) {
+    const int ks0 = seq_start + t * kBlockN;
+    unsigned char* kt = k_lds + buf * C::kTileBytes;
+    unsigned char* vt = v_lds + buf * C::kTileBytes;
+    const uint16_t* kg = kbase + ks0 * a.ks[2];
+    const uint16_t* vg = vbase + ks0 * a.vs[2];
+    const bool full = ks0 + kBlockN <= seq_end;
+    const int last = seq_end - 1 - ks0;  // last valid row of this tile
+#pragma unroll
+    for (int i = 0; i < C::kLoads; ++i) {
+      const int blk = i * C::kWaves + wave;
+      int krel, vrel;
+      if (full) {
+        krel = kHoist ? cp_krel[i] : cp_row(i) * static_cast<int>(a.ks[2]) + cp_koff(i);
+        vrel = kHoist ? cp_vrel[i] : cp_row(i) * static_cast<int>(a.vs[2]) + cp_voff(i);
+      } else {
+        const int r = cp_row(i) < last ? cp_row(i) : last;
+        krel = r * static_cast<int>(a.ks[2]) + cp_koff(i);
+        vrel = r * static_cast<int>(a.vs[2]) + cp_voff(i);
+      }
+      __builtin_amdgcn_global_load_lds(kg + krel, (lds_void_t*)(kt + blk * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vg + vrel, (lds_void_t*)(vt + blk * 1024), 16, 0, 0);
     }
   };
 
-  const int krow = sigma(col);  // K row (within a 32-key block) this lane supplies
   f32x16_t o[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) o[db] = f32x16_t{};
   float m_run = -__builtin_inff();  // running max (log2-scaled units), may lag the true max by <= 8
   float l_run = 0.0f;               // this lane's partial denominator
 
+  // Prologue: tiles 0 (and 1) in flight; wait for tile 0 only.  Each
+  // issue_tile is 2*kLoads VMEM instructions per thread.
+  constexpr int kPerTile = 2 * C::kLoads;
+  constexpr int kAhead = C::kStages - 1;  // prefetch distance in tiles
   issue_tile(0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
+  if (C::kStages == 3 && ntiles > 1) {
+    issue_tile(1, 1);
+    __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(kPerTile));
+  } else {
+    __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(0));
+  }
   __syncthreads();
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) issue_tile(t + 1, buf ^ 1);
-    const unsigned char* kt = smem + buf * C::kStageBytes;
-    const unsigned char* vt = kt + C::kTileBytes;
+  // One 64-key tile in LDS stage BUF (a constant after inlining where the loop
+  // is unrolled by the stage count).
+  auto tile_step = [&](int t, int BUF) {
+    const bool issued = t + kAhead < ntiles;
+    if (issued) issue_tile(t + kAhead, (BUF + kAhead) % C::kStages);
+    const unsigned char* kt = k_lds + BUF * C::kTileBytes;
+    const unsigned char* vt = v_lds + BUF * C::kTileBytes;
     const int ks0 = seq_start + t * kBlockN;
 
     // S^T for this wavefront's 32-key block(s) of the tile
     f32x16_t s[C::kBlocks];
 #pragma unroll
     for (int bl = 0; bl < C::kBlocks; ++bl) {
-      const int row = (kh * C::kBlocks + bl) * 32 + krow;
-      const unsigned char* kr = kt + row * CR * 16;
-      const int sw = swz_k<CR>(row);
-      bf16x8_t kf[D / 16];
-#pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk)
-        kf[kk] = *reinterpret_cast<const bf16x8_t*>(kr + (((2 * kk + half) ^ sw) * 16));
       s[bl] = f32x16_t{};
+      constexpr int kGroup = D / 16 < 8 ? D / 16 : 8;  // operand reads issued ahead of their MFMAs
 #pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk)
-        s[bl] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kk], qf[kk], s[bl], 0, 0, 0);
+      for (int k0 = 0; k0 < D / 16; k0 += kGroup) {
+        bf16x8_t kf[kGroup];
+#pragma unroll
+        for (int kk = 0; kk < kGroup; ++kk) kf[kk] = *reinterpret_cast<const bf16x8_t*>(kt + k_off(bl, k0 + kk));
+#pragma unroll
+        for (int kk = 0; kk < kGroup; ++kk)
+          s[bl] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kk], qf[k0 + kk], s[bl], 0, 0, 0);
+      }
     }
 
     // causal / end-of-sequence mask on diagonal and tail tiles only
@@ -291,30 +376,36 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
 
     // O^T += V^T · P^T: the V^T A operand of each 16-key slice comes from two
     // transposing reads of the row-major V tile (keys +0..3 and +4..7)
-    const int grp = lane >> 4;
-    const int li = lane & 15;
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) {
-      const int dim = db * 32 + 16 * (grp & 1) + 4 * (li & 3);
-      const int dchunk = dim >> 3;
-      const int doff = (dim & 7) * 2;
 #pragma unroll
       for (int cs = 0; cs < 2 * C::kBlocks; ++cs) {
-        const int slice = (kh * C::kBlocks) * 2 + cs;  // 16-key slice within the tile
-        v4i16_t part[2];
-#pragma unroll
-        for (int r2 = 0; r2 < 2; ++r2) {
-          const int row = slice * 16 + 8 * (grp >> 1) + 4 * r2 + (li >> 2);
-          const unsigned char* addr = vt + row * CR * 16 + ((dchunk ^ swz_v<CR>(row)) * 16) + doff;
-          part[r2] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(addr));
-        }
-        const v4i16_t lo = part[0], hi = part[1];
+        const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(vt + v_off(db, cs, 0)));
+        const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(vt + v_off(db, cs, 1)));
         const short __attribute__((ext_vector_type(8))) vv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vv), pb[cs], o[db], 0, 0, 0);
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's copies of tile t+1 have landed
+    // tile t+1 must have landed (only tile t+kAhead may still be in flight);
+    // the barrier makes every thread's copies visible and frees stage BUF
+    if (C::kStages == 3 && issued)
+      __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(kPerTile));
+    else
+      __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(0));
     __syncthreads();
+  };
+
+  if constexpr (C::kStages == 3) {
+    int t = 0;
+    for (; t + 3 <= ntiles; t += 3) {
+      tile_step(t, 0);
+      tile_step(t + 1, 1);
+      tile_step(t + 2, 2);
+    }
+    if (t < ntiles) tile_step(t, 0);
+    if (t + 1 < ntiles) tile_step(t + 1, 1);
+  } else {
+    for (int t = 0; t < ntiles; ++t) tile_step(t, t & 1);
   }
 
   // ---- merge the key parts of each (head, query block), then normalise and store
@@ -394,6 +485,9 @@ extern "C" int fd_gqa_fwd(const void* q, const void* k, const void* v, void* out
              "fd_gqa_fwd: innermost strides must be 1 and the others multiples of 8 elements (16 bytes)");
   FD_REQUIRE(fd_aligned16(q) && fd_aligned16(k) && fd_aligned16(v) && fd_aligned16(out), FD_ERR_ALIGNMENT,
              "fd_gqa_fwd: tensors must be 16-byte aligned");
+  // K/V tile rows are addressed with 32-bit offsets from the tile's first row
+  FD_REQUIRE(k_strides[2] >= 0 && v_strides[2] >= 0 && k_strides[2] < (1 << 24) && v_strides[2] < (1 << 24),
+             FD_ERR_UNSUPPORTED, "fd_gqa_fwd: K/V token strides must be in [0, 2^24) elements");
   int n_slots;
   int span_len;
   if (cu_seqlens != nullptr) {
