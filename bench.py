@@ -6,8 +6,8 @@ T=2048, 28 layers 3:1 Gated-DeltaNet/GQA, bf16, seeded random weights,
 synthetic token ids) with the three HIP kernels installed, replayed from a
 captured HIP graph; the metric is the median GPU forward time (ms).  The same
 model on the reference PyTorch path (SDPA / F.conv1d / eager RMSNorm, also
-graph-replayed) is timed interleaved with it, and the argmax decisions of the
-4 tail slots are compared.
+graph-replayed) is timed for the same number of steps after the timed region,
+and the argmax decisions of the 4 tail slots are compared.
 
 Per kernel, at its BASELINE configuration, the HIP kernel and the PyTorch-ROCm
 eager op it replaces are timed from HIP events on the launch stream (graph
@@ -37,6 +37,19 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+GQA_PROFILE = ROOT / "profiles" / "gqa_fwd_kernel_B1_T2048_H16x4_D128.md"
+
+
+def profiled_traffic(path: Path):
+    """HBM bytes per launch recorded by the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    of `path` (its line `HBM traffic per launch (bytes): N`), or None."""
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("HBM traffic per launch (bytes):"):
+                return int(line.split(":", 1)[1].strip().replace(",", ""))
+    except OSError:
+        pass
+    return None
 
 
 def log(msg: str) -> None:
@@ -53,8 +66,9 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-kernels", action="store_true", help="skip the per-kernel micro-benchmarks")
     p.add_argument("--no-forward", action="store_true", help="skip the full-forward benchmark")
-    p.add_argument("--only-kernel", choices=["gqa", "conv", "rmsnorm"], default=None,
-                   help="profiling aid: run just this kernel's HIP timing loop")
+    p.add_argument("--only-kernel", choices=["gqa", "conv", "rmsnorm", "copy"], default=None,
+                   help="profiling aid: run just this kernel's HIP timing loop ('copy' is the plain device "
+                        "copy used to calibrate HBM byte counters)")
     return p.parse_args()
 
 
@@ -122,7 +136,8 @@ def bench_gqa(samples: int, only: bool = False) -> dict:
     v = (torch.randn((B, T, Hkv, D), generator=g) / D ** 0.5).to(torch.bfloat16).cuda().permute(0, 2, 1, 3)
     flops = 4 * B * Hq * D * T * T / 2
     bytes_ = 2 * (q.numel() + k.numel() + v.numel() + q.numel())
-    graphs = {"hip": graph_of([lambda: native_gqa_attention(q, k, v)])}
+    reps = 10  # launches per graph: per-launch time excludes the graph launch gap
+    graphs = {"hip": graph_of([lambda: native_gqa_attention(q, k, v)] * reps)}
     backend = None
     if not only:
         def sdpa_gqa():
@@ -132,10 +147,10 @@ def bench_gqa(samples: int, only: bool = False) -> dict:
             kr = k[:, :, None].expand(B, Hkv, Hq // Hkv, T, D).reshape(B, Hq, T, D)
             vr = v[:, :, None].expand(B, Hkv, Hq // Hkv, T, D).reshape(B, Hq, T, D)
             return F.scaled_dot_product_attention(q, kr, vr, is_causal=True)
-        graphs["eager_sdpa_enable_gqa"] = graph_of([sdpa_gqa])
-        graphs["eager_sdpa_repeat_kv"] = graph_of([sdpa_repeat])
+        graphs["eager_sdpa_enable_gqa"] = graph_of([sdpa_gqa] * reps)
+        graphs["eager_sdpa_repeat_kv"] = graph_of([sdpa_repeat] * reps)
         backend = _sdpa_backend(q, k, v)
-    times = time_graphs(graphs, {k_: 1 for k_ in graphs}, samples, 20)
+    times = time_graphs(graphs, {k_: reps for k_ in graphs}, samples, 2)
     res = {name: summary(t) for name, t in times.items()}
     us = res["hip"]["median_us"]
     out = dict(config="B=1 T=2048 Hq=16 Hkv=4 D=128 bf16", bound="mfma", flops=flops, bytes=bytes_,
@@ -212,7 +227,7 @@ def bench_rmsnorm(samples: int, only: bool = False) -> dict:
     w = (torch.randn((2048,), generator=g) * 0.02).to(torch.bfloat16).cuda()
     n = 4 * 2048 * 2048
     bytes_ = 2 * 4 * n + 2 * 2048
-    graphs = {"hip": graph_of([lambda x=x, r=r: fused_add_rms_norm(x, r, w) for x, r in zip(xs, rs)])}
+    graphs = {"hip": graph_of([lambda x=x, r=r: fused_add_rms_norm(x, r, w) for x, r in zip(xs, rs)] * 2)}
     if not only:
         from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5RMSNorm
         norm = Qwen3_5RMSNorm(2048, eps=1e-6).cuda().to(torch.bfloat16)
@@ -221,8 +236,8 @@ def bench_rmsnorm(samples: int, only: bool = False) -> dict:
         def eager(x, r):
             h = r + x
             return norm(h), h
-        graphs["eager_add_qwen3_5_rmsnorm"] = graph_of([lambda x=x, r=r: eager(x, r) for x, r in zip(xs, rs)])
-    times = time_graphs(graphs, {k_: sets for k_ in graphs}, samples, 5)
+        graphs["eager_add_qwen3_5_rmsnorm"] = graph_of([lambda x=x, r=r: eager(x, r) for x, r in zip(xs, rs)] * 2)
+    times = time_graphs(graphs, {k_: 2 * sets for k_ in graphs}, samples, 3)
     res = {name: summary(t) for name, t in times.items()}
     us = res["hip"]["median_us"]
     out = dict(config="[4,2048,2048] bf16 eps=1e-6", bound="hbm", bytes=bytes_, hip=res["hip"],
@@ -232,6 +247,20 @@ def bench_rmsnorm(samples: int, only: bool = False) -> dict:
         out.update(eager_add_qwen3_5_rmsnorm=res["eager_add_qwen3_5_rmsnorm"],
                    speedup_vs_eager=res["eager_add_qwen3_5_rmsnorm"]["median_us"] / us)
     return out
+
+
+def bench_copy(samples: int, only: bool = True) -> dict:
+    """Plain device copy of 5 rotated 64 MiB bf16 buffers: a kernel of known HBM traffic
+    (read 64 MiB + write 64 MiB per launch) to calibrate FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    n = 32 * 1024 * 1024
+    xs = [torch.randn(n, device="cuda").to(torch.bfloat16) for _ in range(5)]
+    ys = [torch.empty_like(x) for x in xs]
+    graphs = {"copy": graph_of([lambda x=x, y=y: y.copy_(x) for x, y in zip(xs, ys)])}
+    times = time_graphs(graphs, {"copy": 5}, samples, 5)
+    us = summary(times["copy"])["median_us"]
+    return dict(bytes=4 * n, hip=summary(times["copy"]), gbs=4 * n / us / 1e3, peak_gbs=HBM_PEAK_GBS,
+                frac=4 * n / us / 1e3 / HBM_PEAK_GBS)
 
 
 # --------------------------------------------------------------------------- full forward
@@ -324,7 +353,7 @@ def main() -> int:
     log(f"device: {torch.cuda.get_device_name(0)}")
 
     if args.only_kernel:
-        fn = dict(gqa=bench_gqa, conv=bench_conv, rmsnorm=bench_rmsnorm)[args.only_kernel]
+        fn = dict(gqa=bench_gqa, conv=bench_conv, rmsnorm=bench_rmsnorm, copy=bench_copy)[args.only_kernel]
         print(json.dumps({args.only_kernel: fn(args.kernel_samples, only=True)}), flush=True)
         return 0
 
@@ -353,7 +382,7 @@ def main() -> int:
         gq = kernels["gqa"]
         roofline = dict(bound="mfma", kernel="gqa_fwd_kernel<128> (B=1 T=2048 16/4 heads D=128)",
                         achieved=gq["tflops"], peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s", frac=gq["frac"],
-                        traffic=None)
+                        traffic=profiled_traffic(GQA_PROFILE), traffic_source=str(GQA_PROFILE.relative_to(ROOT)))
     line = {
         "metric": "median GPU forward ms, B=1 T=2048 decider-2b-shaped; per-kernel % roofline",
         "value": fwd["median_ms"] if fwd else None,

@@ -41,8 +41,14 @@ __device__ __forceinline__ uint32_t fd_f32_to_bf16(float f) {
 // Two bf16 packed in one 32-bit word (low half = lower address).
 __device__ __forceinline__ float fd_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float fd_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+// v_cvt_pk_bf16_f32: round-to-nearest-even, identical to fd_f32_to_bf16 for
+// every non-NaN input (checked exhaustively over all 2^32 fp32 patterns on
+// gfx950); a NaN input gives a quiet NaN.
 __device__ __forceinline__ uint32_t fd_pack2(float lo, float hi) {
-  return fd_f32_to_bf16(lo) | (fd_f32_to_bf16(hi) << 16);
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 // e^t for the SiLU, branch-free: t is first clamped to [-20, 89] (v_med3);

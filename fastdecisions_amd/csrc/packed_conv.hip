@@ -205,10 +205,11 @@ int launch_run(const void* x, const void* w, const void* bias, void* q, void* k,
 }
 
 #ifndef FD_CONV_RUN
-#define FD_CONV_RUN 8
+#define FD_CONV_RUN 4
 #endif
-// Tokens per thread: 8 gives 3 wavefronts per SIMD at B=1, T=2048, C=6144
-// (balanced over the 1024 SIMDs) for a 3/8 halo re-read from L2.
+// Tokens per thread: 4 gives 6 wavefronts per SIMD at B=1, T=2048, C=6144
+// (balanced over the 1024 SIMDs; the exact SiLU makes the kernel VALU-heavy,
+// so occupancy matters more than the 3/4 halo re-read, which hits L2).
 constexpr int kRun = FD_CONV_RUN;
 
 }  // namespace
