@@ -14,7 +14,9 @@
 //   at the end).  Two wavefronts per SIMD let one run softmax VALU work while
 //   the other issues MFMAs.  head_dim 256 runs 4 wavefronts (register budget).
 // * K and V tiles (64 keys) are copied global -> LDS with global_load_lds
-//   (no staging registers, no VALU), double buffered, one barrier per tile.
+//   (no staging registers, no VALU) into a ring of 3 stages (2 for
+//   head_dim 256, whose 3 stages would not fit the 160 KiB LDS), one barrier
+//   per tile.
 //   16-byte chunks are XOR-swizzled per row so that the MFMA operand reads
 //   below are bank-conflict free.
 // * The score tile is computed transposed, S^T = K · Q^T, with
