@@ -13,7 +13,12 @@ repository's oracle or kernels:
 * GQA: ``F.scaled_dot_product_attention`` (MATH backend, fp32) on K/V repeated
   per group with a causal mask, the reference oracle
   (ref: experiments/native_gqa/bench_native_gqa.py:46-48), per request for varlen;
-* readout: brute-force argmax over the allowed letters.
+* readout: brute-force argmax over the allowed letters;
+* gated delta rule: transformers' ``torch_chunk_gated_delta_rule`` (fp32 CPU,
+  ``use_qk_l2norm_in_kernel=True`` on bf16 q/k, as the decider's layers call it,
+  ref: src/decider/packed_conv.py:55-59), per request for varlen, q/k heads
+  expanded by ``repeat_interleave`` as ``Qwen3_5GatedDeltaNet.forward`` does,
+  and transformers' ``l2norm`` on bf16 rows.
 
 bf16 arrays are stored as uint16 bit patterns.  Each fixture is small (< 1 MB).
 """
@@ -164,9 +169,64 @@ def make_readout(g: torch.Generator) -> dict:
     return dict(logits=logits.numpy(), nopts=nopts.numpy(), choice=choice)
 
 
-def main() -> None:
+def make_gated_delta(g: torch.Generator) -> dict:
+    """q/k are stored after transformers' ``l2norm`` (the rule then runs with
+    ``use_qk_l2norm_in_kernel=False``, which is the same computation): torch's CPU
+    bf16 rsqrt rounds twice on rows its vectorised loop leaves to the scalar tail,
+    which the GPU does not, so the normalisation is pinned on its own fixture."""
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as mq
+    out = {}
+
+    def inputs(T, hk, hv, g_lo, g_hi):
+        q = torch.randn((1, T, hk, 128), generator=g).to(torch.bfloat16)
+        k = torch.randn((1, T, hk, 128), generator=g).to(torch.bfloat16)
+        v = torch.randn((1, T, hv, 128), generator=g).to(torch.bfloat16)
+        # g = -exp(A_log) * softplus(a + dt_bias) spans these ranges in the decider
+        gg = -torch.exp(torch.empty((1, T, hv)).uniform_(g_lo, g_hi, generator=g))
+        beta = torch.rand((1, T, hv), generator=g).to(torch.bfloat16)
+        return mq.l2norm(q, dim=-1, eps=1e-6), mq.l2norm(k, dim=-1, eps=1e-6), v, gg, beta
+
+    def run(q, k, v, gg, beta, state=None, final=False):
+        r = v.shape[2] // q.shape[2]
+        if r > 1:
+            q, k = q.repeat_interleave(r, dim=2), k.repeat_interleave(r, dim=2)
+        return mq.torch_chunk_gated_delta_rule(q, k, v, g=gg, beta=beta, initial_state=state,
+                                               output_final_state=final, use_qk_l2norm_in_kernel=False)
+
+    # dense: T = 140 (two full chunks and a ragged one), 2 heads, long memory, final state
+    q, k, v, gg, beta = inputs(140, 2, 2, -3.0, 0.5)
+    o, fs = run(q, k, v, gg, beta, final=True)
+    out.update(d_q=bits(q), d_k=bits(k), d_v=bits(v), d_g=gg.numpy(), d_beta=bits(beta), d_o=bits(o),
+               d_final=fs.numpy())
+    # decider-like decay, 1 key head shared by 2 value heads, an initial state
+    q, k, v, gg, beta = inputs(96, 1, 2, 0.0, 2.5)
+    s0 = torch.randn((1, 2, 128, 128), generator=g) * 0.05
+    o, fs = run(q, k, v, gg, beta, state=s0, final=True)
+    out.update(s_q=bits(q), s_k=bits(k), s_v=bits(v), s_g=gg.numpy(), s_beta=bits(beta), s_init=s0.numpy(),
+               s_o=bits(o), s_final=fs.numpy())
+    # varlen: 4 requests packed on T = 150 (one empty), each run alone with a fresh state
+    cu = [0, 70, 71, 71, 150]
+    q, k, v, gg, beta = inputs(150, 2, 2, -2.0, 1.0)
+    parts = [run(q[:, a:b], k[:, a:b], v[:, a:b], gg[:, a:b], beta[:, a:b])[0]
+             for a, b in zip(cu[:-1], cu[1:]) if b > a]
+    out.update(v_q=bits(q), v_k=bits(k), v_v=bits(v), v_g=gg.numpy(), v_beta=bits(beta),
+               v_cu=np.array(cu, np.int32), v_o=bits(torch.cat(parts, dim=1)))
+    # l2norm on 64 bf16 rows of 128 (all in torch's vectorised loop), tiny to large
+    x = torch.randn((64, 128), generator=g) * torch.logspace(-3, 3, 64)[:, None]
+    xb = x.to(torch.bfloat16)
+    out.update(l2_x=bits(xb), l2_y=bits(mq.l2norm(xb, dim=-1, eps=1e-6)))
+    return out
+
+
+FIXTURES = (("conv", make_conv), ("rmsnorm", make_rms), ("gqa", make_gqa), ("readout", make_readout),
+            ("gated_delta", make_gated_delta))
+
+
+def main(names=None) -> None:
     torch.manual_seed(0)
-    for name, fn in (("conv", make_conv), ("rmsnorm", make_rms), ("gqa", make_gqa), ("readout", make_readout)):
+    for name, fn in FIXTURES:
+        if names and name not in names:
+            continue
         g = torch.Generator().manual_seed(20260101)
         data = fn(g)
         path = HERE / f"{name}.npz"
@@ -175,4 +235,5 @@ def main() -> None:
 
 
 if __name__ == "__main__":
-    main()
+    import sys
+    main(sys.argv[1:])

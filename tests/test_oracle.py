@@ -270,3 +270,135 @@ def test_readout_matches_golden(oracle, golden):
     assert np.array_equal(choice, d["choice"])
     assert np.allclose(p.sum(axis=1), 1.0)
     assert all((p[i, n:] == 0).all() for i, n in enumerate(d["nopts"]))
+
+
+# ------------------------------------------------------------------ gated delta rule
+
+@pytest.fixture(scope="module")
+def gd():
+    from oracle import gated_delta
+    return gated_delta
+
+
+def _bf16_out(oracle, o):
+    return oracle.f32_to_bf16(o.astype(np.float32))
+
+
+def _close_to_bf16_golden(oracle, o, want_bits, rel=2 ** -7, floor=1e-3):
+    """fp64 result vs a bf16 golden: within a bf16 rounding of fp32 work (abs bound
+    scaled by the output's magnitude)."""
+    want = oracle.bf16_to_f32(want_bits).astype(np.float64)
+    err = np.abs(o - want)
+    return bool((err <= rel * np.abs(want) + floor * np.abs(want).max()).all())
+
+
+def test_gated_delta_l2norm_matches_transformers_bitexact(oracle, gd, golden):
+    d = golden("gated_delta")
+    assert np.array_equal(gd.l2norm_bf16(d["l2_x"]), d["l2_y"])
+
+
+def test_gated_delta_l2norm_rounds_every_step_to_bf16(oracle, gd):
+    """A row whose fp32 sum of squares is not a bf16 value: the sum, the rsqrt and
+    the product are each rounded (transformers' l2norm on bf16 tensors)."""
+    x = oracle.f32_to_bf16(np.array([[3.0, 4.0, 0.1] + [0.0] * 5], np.float32))
+    y = oracle.bf16_to_f32(gd.l2norm_bf16(x))[0]
+    sq = oracle.bf16_to_f32(oracle.f32_to_bf16(oracle.bf16_to_f32(x)[0] ** 2))
+    s = oracle.bf16_to_f32(oracle.f32_to_bf16(np.float32(sq.sum(dtype=np.float32))))
+    inv = oracle.bf16_to_f32(oracle.f32_to_bf16(np.float32(1 / np.sqrt(np.float32(s + np.float32(1e-6))))))
+    assert np.array_equal(y[:3], oracle.bf16_to_f32(oracle.f32_to_bf16(oracle.bf16_to_f32(x)[0][:3] * inv)))
+    assert y[3:].tolist() == [0.0] * 5
+
+
+@pytest.mark.parametrize("case", ["d", "s", "v"])
+def test_gated_delta_matches_transformers_golden(oracle, gd, golden, case):
+    d = golden("gated_delta")
+    kw = dict(l2norm=False)
+    if case == "s":
+        kw["initial_state"] = d["s_init"]
+    if case == "v":
+        kw["cu_seqlens"] = d["v_cu"]
+    o, final = gd.chunked(d[f"{case}_q"], d[f"{case}_k"], d[f"{case}_v"], d[f"{case}_g"], d[f"{case}_beta"], **kw)
+    assert _close_to_bf16_golden(oracle, o, d[f"{case}_o"])
+    if f"{case}_final" in d:
+        want = d[f"{case}_final"]
+        assert np.abs(final - want).max() <= 1e-5 * max(1.0, np.abs(want).max())
+
+
+def test_gated_delta_chunked_equals_recurrent(oracle, gd):
+    """Two independent algorithms for the same recurrence: dense, ragged, varlen,
+    shared key heads and an initial state."""
+    rng = np.random.default_rng(11)
+    T, hk, hv = 150, 1, 2
+    q = oracle.f32_to_bf16(rng.standard_normal((1, T, hk, 128)).astype(np.float32))
+    k = oracle.f32_to_bf16(rng.standard_normal((1, T, hk, 128)).astype(np.float32))
+    v = oracle.f32_to_bf16(rng.standard_normal((1, T, hv, 128)).astype(np.float32))
+    g = -np.exp(rng.uniform(-3, 1, (1, T, hv))).astype(np.float32)
+    beta = rng.uniform(0, 1, (1, T, hv)).astype(np.float32)
+    s0 = rng.standard_normal((3, hv, 128, 128)) * 0.1
+    cu = np.array([0, 65, 65, 150], np.int32)
+    for kw in (dict(), dict(cu_seqlens=cu, initial_state=s0)):
+        a, fa = gd.chunked(q, k, v, g, beta, **kw)
+        b, fb = gd.recurrent(q, k, v, g, beta, **kw)
+        assert np.abs(a - b).max() < 1e-10 and np.abs(fa - fb).max() < 1e-10
+
+
+def test_gated_delta_closed_forms(oracle, gd):
+    rng = np.random.default_rng(3)
+    T = 70
+    q = oracle.f32_to_bf16(rng.standard_normal((1, T, 1, 128)).astype(np.float32))
+    k = oracle.f32_to_bf16(rng.standard_normal((1, T, 1, 128)).astype(np.float32))
+    v = oracle.f32_to_bf16(rng.standard_normal((1, T, 1, 128)).astype(np.float32))
+    g = -np.exp(rng.uniform(-2, 0, (1, T, 1))).astype(np.float32)
+    # beta = 0: nothing is ever written, the output is zero
+    o, f = gd.chunked(q, k, v, g, np.zeros((1, T, 1), np.float32))
+    assert np.abs(o).max() == 0 and np.abs(f).max() == 0
+    # first token: o_0 = beta_0 (scale q_0 . k_0) v_0 on the normalised q/k
+    beta = rng.uniform(0.2, 1, (1, T, 1)).astype(np.float32)
+    o, _ = gd.chunked(q, k, v, g, beta)
+    qn = oracle.bf16_to_f32(gd.l2norm_bf16(q)).astype(np.float64)
+    kn = oracle.bf16_to_f32(gd.l2norm_bf16(k)).astype(np.float64)
+    vv = oracle.bf16_to_f32(v).astype(np.float64)
+    scale = float(np.float32(1 / np.sqrt(128)))
+    assert np.allclose(o[0, 0, 0], beta[0, 0, 0] * scale * (qn[0, 0, 0] @ kn[0, 0, 0]) * vv[0, 0, 0])
+    # orthonormal keys, no decay, beta = 1: the state stores v_i under k_i exactly
+    basis = np.eye(128, dtype=np.float32)[:T]
+    kb = oracle.f32_to_bf16(basis[None, :, None, :])
+    o, f = gd.chunked(kb, kb, v, np.zeros((1, T, 1), np.float32), np.ones((1, T, 1), np.float32), scale=1.0)
+    assert np.allclose(f[0, 0][:T], vv[0, :, 0])
+    assert np.allclose(o[0, :, 0], vv[0, :, 0])
+    # constant decay e^g per token scales an untouched state: beta = 0 with an initial state
+    s0 = rng.standard_normal((1, 1, 128, 128))
+    _, f = gd.chunked(q, k, v, np.full((1, T, 1), -0.01, np.float32), np.zeros((1, T, 1), np.float32),
+                      initial_state=s0)
+    assert np.allclose(f, s0 * np.exp(-0.01 * T))
+
+
+def test_planted_gated_delta_slips_fail_the_golden(oracle, gd, golden):
+    """Slips planted in a copy of the recurrence must fail the transformers golden."""
+    d = golden("gated_delta")
+    q, k, v, g, beta = (d[f"d_{n}"] for n in ("q", "k", "v", "g", "beta"))
+    want = d["d_o"]
+    assert _close_to_bf16_golden(oracle, gd.recurrent(q, k, v, g, beta, l2norm=False)[0], want)
+
+    def slipped(slip):
+        qq, kk, vv, gg, bb = gd._prepare(q, k, v, g, beta, None, False)
+        T, H = vv.shape[1], vv.shape[2]
+        S = np.zeros((H, 128, 128))
+        o = np.zeros(vv.shape[1:])
+        for t in range(T):
+            decay = np.exp(gg[0, t]) if slip != "no_decay" else np.ones(H)
+            if slip != "decay_after":
+                S = S * decay[:, None, None]
+            mem = np.einsum("hk,hkv->hv", kk[0, t], S)
+            dlt = (vv[0, t] - mem) if slip != "beta_outside" else vv[0, t] - mem * bb[0, t][:, None]
+            dlt = dlt * bb[0, t][:, None] if slip != "beta_outside" else dlt
+            if slip == "sign":
+                dlt = vv[0, t] + mem
+            S = S + kk[0, t][:, :, None] * dlt[:, None, :]
+            if slip == "decay_after":
+                S = S * decay[:, None, None]
+            o[t] = np.einsum("hk,hkv->hv", qq[0, t], S if slip != "output_before_write" else S - kk[0, t][:, :, None] * dlt[:, None, :])
+        return o[None]
+
+    for slip in ("no_decay", "decay_after", "beta_outside", "sign", "output_before_write"):
+        assert not _close_to_bf16_golden(oracle, slipped(slip), want), slip
