@@ -51,6 +51,17 @@ SIGNATURES = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, ctypes.c_int64, ctypes.c_int,
          ctypes.c_float, ctypes.c_int, ctypes.c_int, _c_void_p],
     ),
+    "fd_gated_delta_workspace_bytes": (
+        ctypes.c_int64,
+        [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int],
+    ),
+    "fd_gated_delta_fwd": (
+        ctypes.c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p, ctypes.c_int64,
+         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+         ctypes.c_float, ctypes.c_int, ctypes.c_int, _c_void_p, ctypes.c_int, _c_void_p],
+    ),
 }
 
 _LIB = None

@@ -1,0 +1,724 @@
+// Chunked gated delta rule forward for gfx950 (fp32 arithmetic, MFMA).
+//
+// Computes what transformers' torch_chunk_gated_delta_rule computes for the
+// decider's linear-attention layers (called at ref: src/decider/packed_conv.py:55-59
+// with use_qk_l2norm_in_kernel=True; transformers modeling_qwen3_5.py:249-328),
+// per value head h (key head h / (Hv/Hk), the repeat_interleave mapping):
+//
+//   q, k <- l2norm(q), l2norm(k) on the bf16 rows, each step rounded to bf16
+//   q <- q * scale;  per 64-token chunk: gc = cumsum(g),  D_ij = e^{gc_i - gc_j} (j <= i)
+//   L = strictly-lower(beta_i k_i.k_j D_ij),  T = (I + L)^-1
+//   u = T (beta v),  w = T (beta e^{gc} k),   A = (q k^T) o D (j <= i)
+//   across chunks, state S [dk, dv] (zero or the initial state):
+//     v' = u - w S;  o = (q e^{gc}) S + A v';  S <- e^{gc_last} S + (k e^{gc_last - gc})^T v'
+//
+// Packed requests (cu_seqlens) are chunked per request and each request starts
+// from its own state, so no state crosses a request boundary.
+//
+// Four launches, all on the caller's stream, intermediates in a caller-provided
+// workspace (fd_gated_delta_workspace_bytes):
+//   1. gd_chunk_table — one workgroup: chunk -> (first row, length), request ->
+//      first chunk.
+//   2. gd_prep_kernel — one workgroup per (chunk, value head), chunk-parallel:
+//      l2norm, cumsum, the Gram and q.k tiles on bf16 MFMA (the normalised q/k
+//      are bf16 values, so these products are exact before fp32 accumulation),
+//      T by forward substitution (one lane per column), u and w on fp32 MFMA.
+//   3. gd_state_kernel — one workgroup per (request, value head, 16 value
+//      columns): the only sequential part.  Each state column evolves on its
+//      own, so the 128 value columns split over 8 workgroups.  The state slice
+//      lives in registers; the next chunk's operands are prefetched into
+//      registers while the current chunk runs.
+//   4. gd_out_kernel — one workgroup per (chunk, value head), chunk-parallel:
+//      o = scale e^{gc} (q S_chunk) + A v'.
+// All fp32 products run on v_mfma_f32_16x16x4_f32 (lane l supplies A[l%16][l/16]
+// and B[l/16][l%16]; D[4*(l/16)+r][l%16] in register r).  The reduction index k
+// of 16 consecutive MFMAs is assigned as k = 16*(l/16) + s (s = step), so that
+// each lane reads its operands as contiguous runs.
+#include "fd_common.h"
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+namespace {
+
+constexpr int kC = 64;                 // tokens per chunk
+constexpr int kD = 128;                // head_k_dim == head_v_dim
+constexpr int kSlice = 16;             // value columns per state workgroup
+constexpr int kSlices = kD / kSlice;   // state workgroups per (request, head)
+constexpr int kThreads = 256;
+
+struct GdArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const float* g;
+  const void* beta;
+  uint16_t* o;
+  const float* s0;   // [N, Hv, Dk, Dv] or null
+  float* sN;         // [N, Hv, Dk, Dv] or null
+  int32_t* row0;     // [nc]  first packed row of each chunk
+  int32_t* len;      // [nc]  valid rows of each chunk (0 = unused)
+  int32_t* first;    // [N+1] first chunk of each request
+  float* gc;         // [Hv, nc, 64]
+  uint16_t* qn;      // [Hv, nc, 64, 128] bf16
+  uint16_t* kn;      // [Hv, nc, 64, 128] bf16
+  float* w;          // [Hv, nc, 64, 128]
+  float* u;          // [Hv, nc, 64, 128]
+  float* vn;         // [Hv, nc, 128 (dv), 64 (t)]  v' transposed
+  float* aq;         // [Hv, nc, 64, 64]
+  float* sc;         // [Hv, nc, 128 (dv), 128 (dk)] state at chunk start, transposed
+  int hk, hv, nc, nseq;
+  int beta_f32, l2norm;
+  float scale;
+};
+
+__device__ __forceinline__ f32x4_t mfma4(float a, float b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float bf16r(float x) { return fd_bf16_to_f32(fd_f32_to_bf16(x)); }
+
+__device__ __forceinline__ void unpack8(uint4 raw, float* x) {
+  const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = fd_lo(wd[i]);
+    x[2 * i + 1] = fd_hi(wd[i]);
+  }
+}
+
+__device__ __forceinline__ uint4 pack8(const float* x) {
+  uint4 r;
+  r.x = fd_f32_to_bf16(x[0]) | (fd_f32_to_bf16(x[1]) << 16);
+  r.y = fd_f32_to_bf16(x[2]) | (fd_f32_to_bf16(x[3]) << 16);
+  r.z = fd_f32_to_bf16(x[4]) | (fd_f32_to_bf16(x[5]) << 16);
+  r.w = fd_f32_to_bf16(x[6]) | (fd_f32_to_bf16(x[7]) << 16);
+  return r;
+}
+
+// transformers' l2norm on a bf16 row of 128 held by 16 consecutive lanes (8
+// values each): x*x rounded to bf16, summed in fp32 (lane chunk order, then an
+// xor butterfly over the 16 lanes), the sum, sum + eps and 1/sqrt each rounded
+// to bf16, then x * inv rounded to bf16.  Every lane of the wavefront must call it.
+__device__ __forceinline__ uint4 l2norm_row8(uint4 raw) {
+  float x[8];
+  unpack8(raw, x);
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s = s + bf16r(x[e] * x[e]);
+  s = s + __shfl_xor(s, 8);
+  s = s + __shfl_xor(s, 4);
+  s = s + __shfl_xor(s, 2);
+  s = s + __shfl_xor(s, 1);
+  const float e = bf16r(bf16r(s) + 1e-6f);
+  const float inv = bf16r(1.0f / __builtin_sqrtf(e));
+  float y[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) y[i] = x[i] * inv;
+  return pack8(y);
+}
+
+// ---------------------------------------------------------------------------
+// 1. chunk table (one workgroup)
+__global__ __launch_bounds__(kThreads) void gd_chunk_table(const int32_t* __restrict__ cu, int nseq, int seq_len,
+                                                           int total, GdArgs a) {
+  __shared__ int scan[kThreads];
+  const int t = threadIdx.x;
+  int carry = 0;
+  for (int base = 0; base < nseq; base += kThreads) {
+    const int s = base + t;
+    int start = 0, end = 0;
+    if (s < nseq) {
+      if (cu != nullptr) {
+        start = min(max(cu[s], 0), total);
+        end = min(max(cu[s + 1], start), total);
+      } else {
+        start = s * seq_len;
+        end = start + seq_len;
+      }
+    }
+    const int n = (end - start + kC - 1) / kC;
+    scan[t] = n;
+    __syncthreads();
+    for (int off = 1; off < kThreads; off <<= 1) {
+      const int add = t >= off ? scan[t - off] : 0;
+      __syncthreads();
+      scan[t] += add;
+      __syncthreads();
+    }
+    const int f = carry + scan[t] - n;
+    const int block_total = scan[kThreads - 1];
+    __syncthreads();
+    if (s < nseq) {
+      a.first[s] = f;
+      for (int j = 0; j < n && f + j < a.nc; ++j) {
+        a.row0[f + j] = start + j * kC;
+        a.len[f + j] = min(kC, end - start - j * kC);
+      }
+    }
+    carry += block_total;
+  }
+  if (t == 0) a.first[nseq] = carry;
+  for (int c = carry + t; c < a.nc; c += kThreads) {
+    a.row0[c] = 0;
+    a.len[c] = 0;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. per-chunk preparation
+constexpr int kRowK = kD + 8;    // bf16 row stride of the row-major q/k tiles (272 B)
+constexpr int kRowT = kC + 8;    // bf16 row stride of the transposed k/v tiles (144 B)
+constexpr int kRowF = kC + 4;    // fp32 row stride of the 64x64 tiles (272 B)
+constexpr int kPrepK = 0;                                   // bf16 [64][kRowK], later sTg
+constexpr int kPrepQ = kPrepK + kC * kRowK * 2;             // bf16 [64][kRowK], later sTb
+constexpr int kPrepKt = kPrepQ + kC * kRowK * 2;            // bf16 [128][kRowT]
+constexpr int kPrepVt = kPrepKt + kD * kRowT * 2;           // bf16 [128][kRowT]
+constexpr int kPrepL = kPrepVt + kD * kRowT * 2;            // fp32 [64][kRowF]
+constexpr int kPrepG = kPrepL + kC * kRowF * 4;             // fp32 [64]
+constexpr int kPrepB = kPrepG + kC * 4;                     // fp32 [64]
+constexpr int kPrepBytes = kPrepB + kC * 4;
+static_assert(kC * kRowF * 4 <= kC * kRowK * 2, "T tiles must fit in the q/k tiles they reuse");
+
+__global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
+  const int h = blockIdx.x % a.hv;
+  const int c = blockIdx.x / a.hv;
+  const int L = a.len[c];
+  if (L <= 0) return;
+  const int r0 = a.row0[c];
+  const int hk = h / (a.hv / a.hk);
+  const size_t hc = static_cast<size_t>(h) * a.nc + c;
+
+  __shared__ __attribute__((aligned(16))) unsigned char smem[kPrepBytes];
+  uint16_t* sK = reinterpret_cast<uint16_t*>(smem + kPrepK);
+  uint16_t* sQ = reinterpret_cast<uint16_t*>(smem + kPrepQ);
+  uint16_t* sKt = reinterpret_cast<uint16_t*>(smem + kPrepKt);
+  uint16_t* sVt = reinterpret_cast<uint16_t*>(smem + kPrepVt);
+  float* sL = reinterpret_cast<float*>(smem + kPrepL);
+  float* sTg = reinterpret_cast<float*>(smem + kPrepK);
+  float* sTb = reinterpret_cast<float*>(smem + kPrepQ);
+  float* sG = reinterpret_cast<float*>(smem + kPrepG);
+  float* sB = reinterpret_cast<float*>(smem + kPrepB);
+
+  const int tid = threadIdx.x;
+  const int wv = tid >> 6;
+  const int l = tid & 63;
+  const int g4 = l >> 4;
+  const int c16 = l & 15;
+
+  // q, k, v rows: 16 lanes per row, 8 values (16 bytes) per lane
+  const size_t qk_row = static_cast<size_t>(a.hk) * kD;
+  const size_t v_row = static_cast<size_t>(a.hv) * kD;
+  uint16_t* gq = a.qn + hc * kC * kD;
+  uint16_t* gk = a.kn + hc * kC * kD;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int row = it * 16 + wv * 4 + g4;
+    const bool valid = row < L;
+    const size_t grow = static_cast<size_t>(r0 + (valid ? row : 0));
+    const uint4 zero = make_uint4(0, 0, 0, 0);
+    uint4 rq = valid ? *reinterpret_cast<const uint4*>(a.q + grow * qk_row + hk * kD + c16 * 8) : zero;
+    uint4 rk = valid ? *reinterpret_cast<const uint4*>(a.k + grow * qk_row + hk * kD + c16 * 8) : zero;
+    const uint4 rv = valid ? *reinterpret_cast<const uint4*>(a.v + grow * v_row + h * kD + c16 * 8) : zero;
+    if (a.l2norm) {
+      rq = l2norm_row8(rq);
+      rk = l2norm_row8(rk);
+    }
+    *reinterpret_cast<uint4*>(sQ + row * kRowK + c16 * 8) = rq;
+    *reinterpret_cast<uint4*>(sK + row * kRowK + c16 * 8) = rk;
+    *reinterpret_cast<uint4*>(gq + row * kD + c16 * 8) = rq;
+    *reinterpret_cast<uint4*>(gk + row * kD + c16 * 8) = rk;
+    const uint32_t kw[4] = {rk.x, rk.y, rk.z, rk.w};
+    const uint32_t vw[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sKt[(c16 * 8 + 2 * e) * kRowT + row] = static_cast<uint16_t>(kw[e] & 0xffffu);
+      sKt[(c16 * 8 + 2 * e + 1) * kRowT + row] = static_cast<uint16_t>(kw[e] >> 16);
+      sVt[(c16 * 8 + 2 * e) * kRowT + row] = static_cast<uint16_t>(vw[e] & 0xffffu);
+      sVt[(c16 * 8 + 2 * e + 1) * kRowT + row] = static_cast<uint16_t>(vw[e] >> 16);
+    }
+  }
+  // g (inclusive cumsum over the chunk) and beta; padded rows carry g = beta = 0
+  if (wv == 0) {
+    const bool valid = l < L;
+    const size_t idx = static_cast<size_t>(r0 + (valid ? l : 0)) * a.hv + h;
+    float gv = valid ? a.g[idx] : 0.0f;
+    float bv = 0.0f;
+    if (valid) bv = a.beta_f32 ? static_cast<const float*>(a.beta)[idx]
+                               : fd_bf16_to_f32(static_cast<const uint16_t*>(a.beta)[idx]);
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float up = __shfl_up(gv, off);
+      if (l >= off) gv = gv + up;
+    }
+    sG[l] = gv;
+    sB[l] = bv;
+    a.gc[hc * kC + l] = gv;
+  }
+  __syncthreads();
+
+  // Gram (k.k) and q.k lower 32x32 tiles on bf16 MFMA; wave 3 zeroes A's upper tile
+  float* gaq = a.aq + hc * kC * kC;
+  if (wv < 3) {
+    const int I = wv == 0 ? 0 : 1;
+    const int J = wv == 2 ? 1 : 0;
+    f32x16_t accG = {};
+    f32x16_t accA = {};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int kc = 16 * s + 8 * (l >> 5);
+      const bf16x8_t ak = *reinterpret_cast<const bf16x8_t*>(sK + (32 * I + (l & 31)) * kRowK + kc);
+      const bf16x8_t aq = *reinterpret_cast<const bf16x8_t*>(sQ + (32 * I + (l & 31)) * kRowK + kc);
+      const bf16x8_t bk = *reinterpret_cast<const bf16x8_t*>(sK + (32 * J + (l & 31)) * kRowK + kc);
+      accG = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ak, bk, accG, 0, 0, 0);
+      accA = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, bk, accA, 0, 0, 0);
+    }
+    const int j = 32 * J + (l & 31);
+    const float gj = sG[j];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = 32 * I + (r >> 2) * 8 + (l >> 5) * 4 + (r & 3);
+      const float dec = i >= j ? expf(sG[i] - gj) : 0.0f;
+      sL[i * kRowF + j] = i > j ? (sB[i] * accG[r]) * dec : 0.0f;
+      gaq[i * kC + j] = i >= j ? (a.scale * accA[r]) * dec : 0.0f;
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) gaq[(r * 2 + (l >> 5)) * kC + 32 + (l & 31)] = 0.0f;
+  }
+  __syncthreads();
+
+  // T = (I + L)^-1 by forward substitution: lane j owns column j
+  if (wv == 0) {
+    const int j = l;
+    float t[kC];
+#pragma unroll
+    for (int i = 0; i < kC; ++i) {
+      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+      for (int m = 0; m + 4 <= i; m += 4) {
+        const f32x4_t lv = *reinterpret_cast<const f32x4_t*>(sL + i * kRowF + m);
+        a0 = fmaf(lv[0], t[m], a0);
+        a1 = fmaf(lv[1], t[m + 1], a1);
+        a2 = fmaf(lv[2], t[m + 2], a2);
+        a3 = fmaf(lv[3], t[m + 3], a3);
+      }
+#pragma unroll
+      for (int m = i & ~3; m < i; ++m) a0 = fmaf(sL[i * kRowF + m], t[m], a0);
+      t[i] = (i == j ? 1.0f : 0.0f) - ((a0 + a1) + (a2 + a3));
+    }
+    const float bj = sB[j];
+    const float bgj = bj * expf(sG[j]);
+#pragma unroll
+    for (int i = 0; i < kC; ++i) {
+      sTb[i * kRowF + j] = t[i] * bj;
+      sTg[i * kRowF + j] = t[i] * bgj;
+    }
+  }
+  __syncthreads();
+
+  // u = (T beta) v and w = (T beta e^gc) k on fp32 MFMA; wave wv owns rows 16wv..16wv+15
+  float aT[16], aG[16];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const f32x4_t tb = *reinterpret_cast<const f32x4_t*>(sTb + (16 * wv + c16) * kRowF + 16 * g4 + 4 * p);
+    const f32x4_t tg = *reinterpret_cast<const f32x4_t*>(sTg + (16 * wv + c16) * kRowF + 16 * g4 + 4 * p);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      aT[4 * p + e] = tb[e];
+      aG[4 * p + e] = tg[e];
+    }
+  }
+  float* gu = a.u + hc * kC * kD;
+  float* gw = a.w + hc * kC * kD;
+#pragma unroll 2
+  for (int n = 0; n < 8; ++n) {
+    float bv[16], bk[16];
+    const uint16_t* pv = sVt + (16 * n + c16) * kRowT + 16 * g4;
+    const uint16_t* pk = sKt + (16 * n + c16) * kRowT + 16 * g4;
+    unpack8(*reinterpret_cast<const uint4*>(pv), bv);
+    unpack8(*reinterpret_cast<const uint4*>(pv + 8), bv + 8);
+    unpack8(*reinterpret_cast<const uint4*>(pk), bk);
+    unpack8(*reinterpret_cast<const uint4*>(pk + 8), bk + 8);
+    f32x4_t accU = {};
+    f32x4_t accW = {};
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      accU = mfma4(aT[s], bv[s], accU);
+      accW = mfma4(aG[s], bk[s], accW);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * wv + 4 * g4 + r;
+      gu[row * kD + 16 * n + c16] = accU[r];
+      gw[row * kD + 16 * n + c16] = accW[r];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 3. sequential state pass over the chunks of one request
+constexpr int kRowS = kD + 4;    // fp32 row stride of the transposed state slice
+constexpr int kRowV = kC + 4;    // fp32 row stride of the transposed v' slice
+
+__global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
+  const int js = blockIdx.x % kSlices;
+  const int h = (blockIdx.x / kSlices) % a.hv;
+  const int sq = blockIdx.x / (kSlices * a.hv);
+  const int first = a.first[sq];
+  const int last = min(a.first[sq + 1], a.nc);
+
+  __shared__ __attribute__((aligned(16))) float sSt[kSlice * kRowS];
+  __shared__ __attribute__((aligned(16))) uint16_t sKt[kD * kRowT];
+  __shared__ __attribute__((aligned(16))) float sVd[kSlice * kRowV];
+  __shared__ float sGc[kC];
+
+  const int tid = threadIdx.x;
+  const int wv = tid >> 6;
+  const int l = tid & 63;
+  const int g4 = l >> 4;
+  const int c16 = l & 15;
+  const int col = kSlice * js + c16;  // value column owned in the C layout
+
+  // state slice in the C layout: S[m][r] = S[dk = 32wv + 16m + 4g4 + r][col]
+  float S[2][4];
+  const size_t state_base = (static_cast<size_t>(sq) * a.hv + h) * kD * kD;
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      S[m][r] = a.s0 ? a.s0[state_base + static_cast<size_t>(32 * wv + 16 * m + 4 * g4 + r) * kD + col] : 0.0f;
+
+  // prefetch registers for one chunk
+  uint4 pk[4];
+  f32x4_t pw[8];
+  float pu[4];
+  float pg = 0.0f;
+  auto prefetch = [&](int c) {
+    const size_t hc = static_cast<size_t>(h) * a.nc + c;
+    const uint16_t* kn = a.kn + hc * kC * kD;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pk[i] = *reinterpret_cast<const uint4*>(kn + ((tid >> 4) + 16 * i) * kD + (tid & 15) * 8);
+    const float* w = a.w + hc * kC * kD + (16 * wv + c16) * kD + 32 * g4;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pw[i] = *reinterpret_cast<const f32x4_t*>(w + 4 * i);
+    const float* u = a.u + hc * kC * kD;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pu[r] = u[(16 * wv + 4 * g4 + r) * kD + col];
+    if (wv == 0) pg = a.gc[hc * kC + l];
+  };
+  if (first < last) prefetch(first);
+
+  for (int c = first; c < last; ++c) {
+    const size_t hc = static_cast<size_t>(h) * a.nc + c;
+    // stage this chunk's k (transposed) and gc; keep w / u in registers
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = (tid >> 4) + 16 * i;
+      const uint32_t kw[4] = {pk[i].x, pk[i].y, pk[i].z, pk[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sKt[((tid & 15) * 8 + 2 * e) * kRowT + row] = static_cast<uint16_t>(kw[e] & 0xffffu);
+        sKt[((tid & 15) * 8 + 2 * e + 1) * kRowT + row] = static_cast<uint16_t>(kw[e] >> 16);
+      }
+    }
+    if (wv == 0) sGc[l] = pg;
+    float cw[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) cw[4 * i + e] = pw[i][e];
+    float cu[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) cu[r] = pu[r];
+    if (c + 1 < last) prefetch(c + 1);
+
+    // state at the chunk start: to LDS (transposed, for w S) and to the workspace (for the output pass)
+    float* sc = a.sc + hc * kD * kD + static_cast<size_t>(col) * kD;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const f32x4_t sv = {S[m][0], S[m][1], S[m][2], S[m][3]};
+      const int dk = 32 * wv + 16 * m + 4 * g4;
+      *reinterpret_cast<f32x4_t*>(sSt + c16 * kRowS + dk) = sv;
+      *reinterpret_cast<f32x4_t*>(sc + dk) = sv;
+    }
+    __syncthreads();
+
+    // v' = u - w S for rows 16wv..16wv+15 of this slice
+    float bS[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const f32x4_t sv = *reinterpret_cast<const f32x4_t*>(sSt + c16 * kRowS + 32 * g4 + 4 * i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bS[4 * i + e] = sv[e];
+    }
+    f32x4_t acc = {};
+#pragma unroll
+    for (int s = 0; s < 32; ++s) acc = mfma4(cw[s], bS[s], acc);
+    const float gl = sGc[kC - 1];
+    f32x4_t vnew, vdec;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      vnew[r] = cu[r] - acc[r];
+      vdec[r] = vnew[r] * expf(gl - sGc[16 * wv + 4 * g4 + r]);
+    }
+    *reinterpret_cast<f32x4_t*>(a.vn + hc * kD * kC + static_cast<size_t>(col) * kC + 16 * wv + 4 * g4) = vnew;
+    *reinterpret_cast<f32x4_t*>(sVd + c16 * kRowV + 16 * wv + 4 * g4) = vdec;
+    __syncthreads();
+
+    // S <- e^{gl} S + k^T (e^{gl - gc} v'), dk rows 32wv..32wv+31
+    float bV[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4_t vv = *reinterpret_cast<const f32x4_t*>(sVd + c16 * kRowV + 16 * g4 + 4 * i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bV[4 * i + e] = vv[e];
+    }
+    const float egl = expf(gl);
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      float ak[16];
+      const uint16_t* pkt = sKt + (32 * wv + 16 * m + c16) * kRowT + 16 * g4;
+      unpack8(*reinterpret_cast<const uint4*>(pkt), ak);
+      unpack8(*reinterpret_cast<const uint4*>(pkt + 8), ak + 8);
+      f32x4_t st = {S[m][0] * egl, S[m][1] * egl, S[m][2] * egl, S[m][3] * egl};
+#pragma unroll
+      for (int s = 0; s < 16; ++s) st = mfma4(ak[s], bV[s], st);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) S[m][r] = st[r];
+    }
+    __syncthreads();
+  }
+
+  if (a.sN != nullptr) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        a.sN[state_base + static_cast<size_t>(32 * wv + 16 * m + 4 * g4 + r) * kD + col] = S[m][r];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4. per-chunk output: o = scale e^{gc} (q S) + A v'
+__global__ __launch_bounds__(kThreads) void gd_out_kernel(GdArgs a) {
+  const int h = blockIdx.x % a.hv;
+  const int c = blockIdx.x / a.hv;
+  const int L = a.len[c];
+  if (L <= 0) return;
+  const int r0 = a.row0[c];
+  const size_t hc = static_cast<size_t>(h) * a.nc + c;
+
+  __shared__ __attribute__((aligned(16))) uint16_t sQ[kC * kRowK];
+  __shared__ __attribute__((aligned(16))) float sA[kC * kRowF];
+  __shared__ float sG[kC];
+
+  const int tid = threadIdx.x;
+  const int wv = tid >> 6;
+  const int l = tid & 63;
+  const int g4 = l >> 4;
+  const int c16 = l & 15;
+
+  const uint16_t* gq = a.qn + hc * kC * kD;
+  const float* gaq = a.aq + hc * kC * kC;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = (tid >> 4) + 16 * i;
+    *reinterpret_cast<uint4*>(sQ + row * kRowK + (tid & 15) * 8) =
+        *reinterpret_cast<const uint4*>(gq + row * kD + (tid & 15) * 8);
+    const int idx = 4 * tid + 1024 * i;
+    *reinterpret_cast<f32x4_t*>(sA + (idx >> 6) * kRowF + (idx & 63)) = *reinterpret_cast<const f32x4_t*>(gaq + idx);
+  }
+  if (wv == 0) sG[l] = a.gc[hc * kC + l];
+  __syncthreads();
+
+  const size_t o_row = static_cast<size_t>(a.hv) * kD;
+#pragma unroll 1
+  for (int nn = 0; nn < 2; ++nn) {
+    const int n = 2 * wv + nn;  // 16 value columns
+    float bS[32], bN[16];
+    const float* sc = a.sc + hc * kD * kD + static_cast<size_t>(16 * n + c16) * kD + 32 * g4;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const f32x4_t sv = *reinterpret_cast<const f32x4_t*>(sc + 4 * i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bS[4 * i + e] = sv[e];
+    }
+    const float* vn = a.vn + hc * kD * kC + static_cast<size_t>(16 * n + c16) * kC + 16 * g4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4_t vv = *reinterpret_cast<const f32x4_t*>(vn + 4 * i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bN[4 * i + e] = vv[e];
+    }
+#pragma unroll 1
+    for (int rt = 0; rt < 4; ++rt) {
+      float aQ[32], aA[16];
+      const uint16_t* pq = sQ + (16 * rt + c16) * kRowK + 32 * g4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) unpack8(*reinterpret_cast<const uint4*>(pq + 8 * i), aQ + 8 * i);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4_t av = *reinterpret_cast<const f32x4_t*>(sA + (16 * rt + c16) * kRowF + 16 * g4 + 4 * i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) aA[4 * i + e] = av[e];
+      }
+      f32x4_t acc1 = {};
+      f32x4_t acc2 = {};
+#pragma unroll
+      for (int s = 0; s < 32; ++s) acc1 = mfma4(aQ[s], bS[s], acc1);
+#pragma unroll
+      for (int s = 0; s < 16; ++s) acc2 = mfma4(aA[s], bN[s], acc2);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * rt + 4 * g4 + r;
+        if (t < L) {
+          const float val = (a.scale * expf(sG[t])) * acc1[r] + acc2[r];
+          a.o[static_cast<size_t>(r0 + t) * o_row + h * kD + 16 * n + c16] = static_cast<uint16_t>(fd_f32_to_bf16(val));
+        }
+      }
+    }
+  }
+}
+
+struct GdLayout {
+  size_t row0, len, first, gc, qn, kn, w, u, vn, aq, sc, total;
+};
+
+GdLayout gd_layout(int64_t nc, int64_t hv, int64_t nseq) {
+  auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+  const size_t hc = static_cast<size_t>(hv) * static_cast<size_t>(nc);
+  GdLayout L;
+  size_t off = 0;
+  L.row0 = off;
+  off = al(off + static_cast<size_t>(nc) * 4);
+  L.len = off;
+  off = al(off + static_cast<size_t>(nc) * 4);
+  L.first = off;
+  off = al(off + static_cast<size_t>(nseq + 1) * 4);
+  L.gc = off;
+  off = al(off + hc * kC * 4);
+  L.qn = off;
+  off = al(off + hc * kC * kD * 2);
+  L.kn = off;
+  off = al(off + hc * kC * kD * 2);
+  L.w = off;
+  off = al(off + hc * kC * kD * 4);
+  L.u = off;
+  off = al(off + hc * kC * kD * 4);
+  L.vn = off;
+  off = al(off + hc * kD * kC * 4);
+  L.aq = off;
+  off = al(off + hc * kC * kC * 4);
+  L.sc = off;
+  off = al(off + hc * kD * kD * 4);
+  L.total = off;
+  return L;
+}
+
+// chunks and requests of a launch; false if the sizes are out of range
+bool gd_counts(int batch, int seq_len, int n_seqs, bool varlen, int64_t* nc, int64_t* nseq) {
+  if (batch < 0 || seq_len < 0) return false;
+  const int64_t total = static_cast<int64_t>(batch) * seq_len;
+  if (total >= (1LL << 31)) return false;
+  if (varlen) {
+    if (n_seqs < 1 || batch != 1) return false;
+    *nseq = n_seqs;
+    *nc = (total + kC - 1) / kC + n_seqs;
+  } else {
+    *nseq = batch;
+    *nc = static_cast<int64_t>(batch) * ((seq_len + kC - 1) / kC);
+  }
+  return true;
+}
+
+}  // namespace
+
+extern "C" FD_API int64_t fd_gated_delta_workspace_bytes(int batch, int seq_len, int v_heads, int head_k_dim,
+                                                         int head_v_dim, int n_seqs) {
+  if (v_heads <= 0 || head_k_dim != kD || head_v_dim != kD) return FD_ERR_UNSUPPORTED;
+  int64_t nc = 0, nseq = 0;
+  if (!gd_counts(batch, seq_len, n_seqs, n_seqs > 0, &nc, &nseq)) return FD_ERR_INVALID_ARGUMENT;
+  return static_cast<int64_t>(gd_layout(nc, v_heads, nseq).total);
+}
+
+extern "C" FD_API int fd_gated_delta_fwd(const void* q, const void* k, const void* v, const float* g,
+                                         const void* beta, void* out, const float* initial_state,
+                                         float* final_state, void* workspace, int64_t workspace_bytes, int batch,
+                                         int seq_len, int k_heads, int v_heads, int head_k_dim, int head_v_dim,
+                                         float scale, int beta_dtype, int l2norm_qk, const int32_t* cu_seqlens,
+                                         int n_seqs, void* stream) {
+  FD_REQUIRE(q && k && v && g && beta && out && workspace, FD_ERR_INVALID_ARGUMENT,
+             "fd_gated_delta_fwd: q, k, v, g, beta, out and workspace must be non-null");
+  FD_REQUIRE(k_heads > 0 && v_heads > 0 && v_heads % k_heads == 0, FD_ERR_INVALID_ARGUMENT,
+             "fd_gated_delta_fwd: v_heads (%d) must be a positive multiple of k_heads (%d)", v_heads, k_heads);
+  FD_REQUIRE(head_k_dim == kD && head_v_dim == kD, FD_ERR_UNSUPPORTED,
+             "fd_gated_delta_fwd: head_k_dim and head_v_dim must be 128 (got %d, %d)", head_k_dim, head_v_dim);
+  FD_REQUIRE(beta_dtype == FD_DTYPE_BF16 || beta_dtype == FD_DTYPE_F32, FD_ERR_INVALID_ARGUMENT,
+             "fd_gated_delta_fwd: beta_dtype must be FD_DTYPE_BF16 or FD_DTYPE_F32");
+  FD_REQUIRE(scale > 0.0f && scale < 1e30f, FD_ERR_INVALID_ARGUMENT, "fd_gated_delta_fwd: scale must be positive");
+  FD_REQUIRE(fd_aligned16(q) && fd_aligned16(k) && fd_aligned16(v) && fd_aligned16(out) && fd_aligned16(workspace),
+             FD_ERR_ALIGNMENT, "fd_gated_delta_fwd: q, k, v, out and workspace must be 16-byte aligned");
+  FD_REQUIRE((reinterpret_cast<uintptr_t>(g) & 3u) == 0 && (reinterpret_cast<uintptr_t>(beta) & 1u) == 0 &&
+                 (beta_dtype != FD_DTYPE_F32 || (reinterpret_cast<uintptr_t>(beta) & 3u) == 0),
+             FD_ERR_ALIGNMENT, "fd_gated_delta_fwd: g and beta must be aligned to their element size");
+  const bool varlen = cu_seqlens != nullptr;
+  if (varlen) {
+    FD_REQUIRE(batch == 1, FD_ERR_INVALID_ARGUMENT, "fd_gated_delta_fwd: cu_seqlens requires batch == 1 (got %d)",
+               batch);
+    FD_REQUIRE(n_seqs >= 1, FD_ERR_INVALID_ARGUMENT, "fd_gated_delta_fwd: n_seqs must be >= 1 with cu_seqlens");
+  }
+  int64_t nc = 0, nseq = 0;
+  FD_REQUIRE(gd_counts(batch, seq_len, n_seqs, varlen, &nc, &nseq), FD_ERR_INVALID_ARGUMENT,
+             "fd_gated_delta_fwd: batch and seq_len must be >= 0 with batch * seq_len < 2^31");
+  FD_REQUIRE(nc * v_heads < (1LL << 31) && nseq * v_heads * kSlices < (1LL << 31), FD_ERR_INVALID_ARGUMENT,
+             "fd_gated_delta_fwd: problem too large");
+  if (nseq == 0) return FD_OK;  // empty batch: nothing to launch
+  const GdLayout lay = gd_layout(nc, v_heads, nseq);
+  FD_REQUIRE(workspace_bytes >= static_cast<int64_t>(lay.total), FD_ERR_INVALID_ARGUMENT,
+             "fd_gated_delta_fwd: workspace too small (%lld bytes, need %lld)",
+             static_cast<long long>(workspace_bytes), static_cast<long long>(lay.total));
+
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  GdArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.g = g;
+  a.beta = beta;
+  a.o = static_cast<uint16_t*>(out);
+  a.s0 = initial_state;
+  a.sN = final_state;
+  a.row0 = reinterpret_cast<int32_t*>(ws + lay.row0);
+  a.len = reinterpret_cast<int32_t*>(ws + lay.len);
+  a.first = reinterpret_cast<int32_t*>(ws + lay.first);
+  a.gc = reinterpret_cast<float*>(ws + lay.gc);
+  a.qn = reinterpret_cast<uint16_t*>(ws + lay.qn);
+  a.kn = reinterpret_cast<uint16_t*>(ws + lay.kn);
+  a.w = reinterpret_cast<float*>(ws + lay.w);
+  a.u = reinterpret_cast<float*>(ws + lay.u);
+  a.vn = reinterpret_cast<float*>(ws + lay.vn);
+  a.aq = reinterpret_cast<float*>(ws + lay.aq);
+  a.sc = reinterpret_cast<float*>(ws + lay.sc);
+  a.hk = k_heads;
+  a.hv = v_heads;
+  a.nc = static_cast<int>(nc);
+  a.nseq = static_cast<int>(nseq);
+  a.beta_f32 = beta_dtype == FD_DTYPE_F32;
+  a.l2norm = l2norm_qk != 0;
+  a.scale = scale;
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int total = batch * seq_len;
+  hipLaunchKernelGGL(gd_chunk_table, dim3(1), dim3(kThreads), 0, s, cu_seqlens, a.nseq, seq_len, total, a);
+  if (nc > 0) {
+    hipLaunchKernelGGL(gd_prep_kernel, dim3(static_cast<unsigned>(nc * v_heads)), dim3(kThreads), 0, s, a);
+  }
+  hipLaunchKernelGGL(gd_state_kernel, dim3(static_cast<unsigned>(nseq * v_heads * kSlices)), dim3(kThreads), 0, s,
+                     a);
+  if (nc > 0) {
+    hipLaunchKernelGGL(gd_out_kernel, dim3(static_cast<unsigned>(nc * v_heads)), dim3(kThreads), 0, s, a);
+  }
+  return fd_check_launch("fd_gated_delta_fwd");
+}

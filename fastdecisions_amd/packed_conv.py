@@ -14,9 +14,11 @@ Mirrors ref: src/decider/packed_conv.py:
   and returns the count (ref: :65-75).
 
 With packed requests (``cu_seq_lens_q`` in kwargs) the conv restarts its
-window at every request start, and the gated delta rule — whose eager torch
-form ignores ``cu_seqlens`` (transformers' torch_chunk_gated_delta_rule) — is
-run once per request, so no state crosses a request boundary.
+window at every request start.  The gated delta rule runs on the HIP kernels
+(``fastdecisions::gated_delta_rule``, per-request states from ``cu_seqlens``)
+once ``install_gated_delta_rule`` has switched the layer; otherwise it runs
+transformers' torch form, which ignores ``cu_seqlens``, once per request
+(``fd_segments``), so no state crosses a request boundary either way.
 """
 from __future__ import annotations
 
@@ -86,7 +88,10 @@ def _forward(self, hidden_states, cache_params=None, attention_mask=None, **kwar
     beta = b.sigmoid()
     g = -self.A_log.float().exp() * F.softplus(a.float() + self.dt_bias)
     segments = _segments(kwargs)
-    if segments is None:
+    if getattr(self, "_fd_gated_delta", False):
+        from .gated_delta import gated_delta_rule
+        core_attn_out = gated_delta_rule(query, key, value, g, beta, cu_seqlens)
+    elif segments is None:
         core_attn_out, _ = mq.torch_chunk_gated_delta_rule(
             query, key, value, g=g, beta=beta, initial_state=None, output_final_state=False,
             use_qk_l2norm_in_kernel=True)

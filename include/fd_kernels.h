@@ -1,8 +1,8 @@
 /*
  * fd_kernels.h — C ABI of the FastDecisions MI355X (gfx950) hot-path kernels.
  *
- * Three forward kernels of the decider model, each a drop-in for one Python
- * launcher of the reference:
+ * Forward kernels of the decider model, each a drop-in for one Python
+ * launcher or call of the reference:
  *
  *   fd_gqa_fwd          native GQA causal attention
  *                       replaces native_gqa_attention(q, k, v)
@@ -14,6 +14,9 @@
  *                       replaces residual_rms(a, b, weight)
  *                       (ref: src/decider/persistent_residual_rms_kernel.py:75-104, kernel :49-72;
  *                        eps placement as ref: src/decider/residual_rms_baseline.py:75-78)
+ *   fd_gated_delta_fwd  chunked gated delta rule of the Gated-DeltaNet layers
+ *                       replaces the torch_chunk_gated_delta_rule call
+ *                       (ref: src/decider/packed_conv.py:55-59)
  *
  * Conventions shared by every entry point:
  *   - every tensor pointer is a device pointer; bf16 tensors are passed as raw
@@ -39,7 +42,7 @@ extern "C" {
 #define FD_API
 #endif
 
-#define FD_ABI_VERSION 1
+#define FD_ABI_VERSION 2
 
 #define FD_OK 0
 #define FD_ERR_INVALID_ARGUMENT (-1) /* shape, size, stride or flag out of range */
@@ -130,6 +133,48 @@ FD_API int fd_packed_conv_fwd(const void* x, const void* weight, const void* bia
 FD_API int fd_add_rmsnorm_fwd(const void* x, const void* residual, const void* weight, void* out,
                        void* residual_out, int64_t rows, int width, float eps,
                        int weight_dtype, int gain_offset, void* stream);
+
+/*
+ * Bytes of device workspace fd_gated_delta_fwd needs for these sizes
+ * (n_seqs = number of packed requests with cu_seqlens, 0 for a padded batch),
+ * or a negative FD_ERR_* code.
+ */
+FD_API int64_t fd_gated_delta_workspace_bytes(int batch, int seq_len, int v_heads, int head_k_dim,
+                                              int head_v_dim, int n_seqs);
+
+/*
+ * Chunked gated delta rule forward (the linear attention of the decider's
+ * Gated-DeltaNet layers), fp32 arithmetic, bf16 in/out.  Replaces the
+ * reference call of transformers' torch_chunk_gated_delta_rule
+ * (ref: src/decider/packed_conv.py:55-59; transformers modeling_qwen3_5.py:249-328).
+ *
+ *   q, k  [batch, seq_len, k_heads, head_k_dim] bf16 contiguous
+ *   v     [batch, seq_len, v_heads, head_v_dim] bf16 contiguous
+ *   g     [batch, seq_len, v_heads] fp32 (log decay, <= 0)
+ *   beta  [batch, seq_len, v_heads] of beta_dtype (FD_DTYPE_BF16 or FD_DTYPE_F32)
+ *   out   [batch, seq_len, v_heads, head_v_dim] bf16
+ *   initial_state, final_state  [n, v_heads, head_k_dim, head_v_dim] fp32 or NULL
+ *                               (n = batch, or n_seqs with cu_seqlens)
+ *
+ * Value head h uses key head h / (v_heads / k_heads).  With l2norm_qk, q and k
+ * rows are first normalised as transformers' l2norm does on bf16 tensors
+ * (eps 1e-6, every step rounded to bf16); q is then scaled by `scale`.  Per
+ * value head, with state S [head_k_dim, head_v_dim] (zero or initial_state):
+ *   S <- e^{g_t} S;  S <- S + k_t (beta_t (v_t - S^T k_t))^T;  out_t = S^T q_t
+ * evaluated in 64-token chunks as the reference does.  Varlen: cu_seqlens
+ * (device int32[n_seqs + 1], non-decreasing, from 0 to seq_len) with batch == 1;
+ * each request starts from its own state and no state crosses a request.
+ * Work runs in `workspace` (fd_gated_delta_workspace_bytes, 16-byte aligned).
+ *
+ * Limits: head_k_dim == head_v_dim == 128; v_heads % k_heads == 0;
+ * batch * seq_len < 2^31.
+ */
+FD_API int fd_gated_delta_fwd(const void* q, const void* k, const void* v, const float* g,
+                              const void* beta, void* out, const float* initial_state,
+                              float* final_state, void* workspace, int64_t workspace_bytes,
+                              int batch, int seq_len, int k_heads, int v_heads, int head_k_dim,
+                              int head_v_dim, float scale, int beta_dtype, int l2norm_qk,
+                              const int32_t* cu_seqlens, int n_seqs, void* stream);
 
 #ifdef __cplusplus
 }

@@ -21,7 +21,7 @@ def declared_functions() -> set[str]:
 
 def test_header_declares_the_expected_entry_points():
     assert declared_functions() == {"fd_abi_version", "fd_last_error", "fd_gqa_fwd", "fd_packed_conv_fwd",
-                                    "fd_add_rmsnorm_fwd"}
+                                    "fd_add_rmsnorm_fwd", "fd_gated_delta_workspace_bytes", "fd_gated_delta_fwd"}
 
 
 def test_library_exports_every_declared_symbol_and_nothing_else():
@@ -104,6 +104,36 @@ def test_gqa_argument_errors():
     assert call(cu=f, n=2, mx=4096, T=2048) == _lib.FD_ERR_INVALID_ARGUMENT
     assert call(B=2, cu=f, n=2, mx=10) == _lib.FD_ERR_INVALID_ARGUMENT
     assert call(T=0) == _lib.FD_OK
+
+
+def test_gated_delta_argument_errors():
+    from fastdecisions_amd import _lib
+    lib = _lib.lib()
+    f = 1 << 20
+    need = lib.fd_gated_delta_workspace_bytes(1, 2048, 16, 128, 128, 0)
+    # 32 chunks x 16 heads x 208.25 KiB of per-chunk intermediates, plus the chunk table
+    assert need >= 32 * 16 * 213248 and need < 32 * 16 * 213248 + 4096
+    assert lib.fd_gated_delta_workspace_bytes(1, 2048, 16, 64, 128, 0) == _lib.FD_ERR_UNSUPPORTED
+    assert lib.fd_gated_delta_workspace_bytes(2, 100, 4, 128, 128, 3) == _lib.FD_ERR_INVALID_ARGUMENT
+    # varlen: one extra (partial) chunk per request at most
+    assert lib.fd_gated_delta_workspace_bytes(1, 2048, 16, 128, 128, 4) > need
+
+    def call(q=f, B=1, T=2048, hk=16, hv=16, dk=128, bdt=0, ws=need, cu=None, n=0, scale=0.088, work=f):
+        return lib.fd_gated_delta_fwd(q, f, f, f, f, f, None, None, work, ws, B, T, hk, hv, dk, 128, scale, bdt, 1,
+                                      cu, n, None)
+
+    assert call(dk=64) == _lib.FD_ERR_UNSUPPORTED
+    assert call(hk=3) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert "multiple of k_heads" in _err(lib)
+    assert call(bdt=7) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert call(q=f + 8) == _lib.FD_ERR_ALIGNMENT
+    assert call(ws=need - 1) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert "workspace too small" in _err(lib)
+    assert call(B=2, cu=f, n=1) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert "batch == 1" in _err(lib)
+    assert call(scale=0.0) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert call(work=None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert call(B=0, ws=0) == _lib.FD_OK  # empty batch: nothing to launch
 
 
 def test_python_wrappers_keep_the_reference_errors_on_cpu_tensors():

@@ -1,7 +1,8 @@
 """GPU parity of the whole decider forward with the HIP kernels installed.
 
 Bar (north_star): identical argmax decisions on every synthetic request, HIP
-path vs the reference PyTorch path (SDPA / F.conv1d / eager RMSNorm) on the
+path (the four kernels) vs the reference PyTorch path (SDPA / F.conv1d / eager
+RMSNorm / transformers' torch gated delta rule) on the
 same seeded model and inputs — BASELINE config 4 (B=1, T=2048, 4 tail slots)
 and config 5 (4 packed requests, per-request causal masking, each compared
 with the request run alone through the eager model).
@@ -30,13 +31,15 @@ def _uninstall(model):
             if hasattr(m, attr):
                 m.forward = getattr(m, attr)
                 delattr(m, attr)
+        if hasattr(m, "_fd_gated_delta"):
+            delattr(m, "_fd_gated_delta")
 
 
 def test_install_counts_and_fallback(full_model):
     from fastdecisions_amd.model import install_hip_kernels
     counts = install_hip_kernels(full_model)
     try:
-        assert counts == dict(packed_conv=21, native_gqa=7, residual_rms=28)
+        assert counts == dict(packed_conv=21, native_gqa=7, residual_rms=28, gated_delta=21)
         # guarded fallbacks: grad mode goes to the original eager methods
         ids = torch.randint(0, 100, (1, 64), device="cuda")
         with torch.enable_grad():
