@@ -3,11 +3,12 @@
 
 Step = one forward of the decider-2b-shaped model (B=1,
 T=2048, 28 layers 3:1 Gated-DeltaNet/GQA, bf16, seeded random weights,
-synthetic token ids) with the three HIP kernels installed, replayed from a
+synthetic token ids) with the four HIP kernels installed, replayed from a
 captured HIP graph; the metric is the median GPU forward time (ms).  The same
-model on the reference PyTorch path (SDPA / F.conv1d / eager RMSNorm, also
-graph-replayed) is timed for the same number of steps after the timed region,
-and the argmax decisions of the 4 tail slots are compared.
+model on the reference PyTorch path (SDPA / F.conv1d / eager RMSNorm /
+transformers' torch gated delta rule, also graph-replayed) is timed for the
+same number of steps after the timed region, and the argmax decisions of the
+4 tail slots are compared.
 
 Per kernel, at its BASELINE configuration, the HIP kernel and the PyTorch-ROCm
 eager op it replaces are timed from HIP events on the launch stream (graph
@@ -17,6 +18,7 @@ computed from its algorithmic work:
   GQA   4*B*Hq*D*T^2/2 flop (causal) vs dense bf16 MFMA 2.5 PFLOP/s
   conv  x + w + q/k/v bytes vs HBM 8 TB/s
   norm  x + residual + out + residual_out + gain bytes vs HBM 8 TB/s
+  delta 11.6 Mflop per (64-token chunk, head) vs dense fp32 MFMA 157.3 TFLOP/s
 
 The reference CPU PyTorch path (oracle/reference_cpu.py) is timed on the host
 cores as a reported baseline.  Prints one JSON line.
@@ -37,6 +39,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+MFMA_FP32_PEAK_TFLOPS = 157.3
 GQA_PROFILE = ROOT / "profiles" / "gqa_fwd_kernel_B1_T2048_H16x4_D128.md"
 
 
@@ -66,7 +69,7 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-kernels", action="store_true", help="skip the per-kernel micro-benchmarks")
     p.add_argument("--no-forward", action="store_true", help="skip the full-forward benchmark")
-    p.add_argument("--only-kernel", choices=["gqa", "conv", "rmsnorm", "copy"], default=None,
+    p.add_argument("--only-kernel", choices=["gqa", "conv", "rmsnorm", "gdr", "copy"], default=None,
                    help="profiling aid: run just this kernel's HIP timing loop ('copy' is the plain device "
                         "copy used to calibrate HBM byte counters)")
     return p.parse_args()
@@ -249,6 +252,46 @@ def bench_rmsnorm(samples: int, only: bool = False) -> dict:
     return out
 
 
+GDR_FLOPS_PER_CHUNK_HEAD = (
+    4 * 2 * 64 * 64 * 128      # k.k^T, q.k^T, u = T(beta v), w = T(beta e^g k)
+    + 2 * 64 * 64 * 128        # A v'
+    + 3 * 2 * 64 * 128 * 128   # w S, q S, k^T v'
+    + 2 * 64 ** 3 // 6)        # T = (I + L)^-1 by substitution
+
+
+def bench_gated_delta(samples: int, only: bool = False) -> dict:
+    """One Gated-DeltaNet layer's delta rule at the decider shape (B=1, T=2048,
+    16 heads of 128, q/k l2norm in the kernel, bf16 beta)."""
+    import torch
+    from fastdecisions_amd.gated_delta_kernel import chunk_gated_delta_rule
+    B, T, H, D = 1, 2048, 16, 128
+    g_ = torch.Generator().manual_seed(0)
+    q = torch.randn((B, T, H, D), generator=g_).to(torch.bfloat16).cuda()
+    k = torch.randn((B, T, H, D), generator=g_).to(torch.bfloat16).cuda()
+    v = torch.randn((B, T, H, D), generator=g_).to(torch.bfloat16).cuda()
+    g = (-torch.exp(torch.empty((B, T, H)).uniform_(-1.0, 2.5, generator=g_))).cuda()
+    beta = torch.rand((B, T, H), generator=g_).to(torch.bfloat16).cuda()
+    flops = GDR_FLOPS_PER_CHUNK_HEAD * (T // 64) * H * B
+    bytes_ = 2 * 3 * B * T * H * D + 4 * B * T * H + 2 * B * T * H + 2 * B * T * H * D
+    reps = 5
+    graphs = {"hip": graph_of([lambda: chunk_gated_delta_rule(q, k, v, g, beta, use_qk_l2norm_in_kernel=True)]
+                              * reps)}
+    if not only:
+        from transformers.models.qwen3_5 import modeling_qwen3_5 as mq
+        graphs["eager_torch_chunk_gated_delta_rule"] = graph_of([lambda: mq.torch_chunk_gated_delta_rule(
+            q, k, v, g=g, beta=beta, use_qk_l2norm_in_kernel=True)])
+    times = time_graphs(graphs, {"hip": reps, "eager_torch_chunk_gated_delta_rule": 1}, samples, 2)
+    res = {name: summary(t) for name, t in times.items()}
+    us = res["hip"]["median_us"]
+    out = dict(config="B=1 T=2048 H=16 Dk=Dv=128 chunk 64, l2norm(q,k), bf16 in/out, fp32 arithmetic",
+               bound="mfma (fp32)", flops=flops, bytes=bytes_, hip=res["hip"], tflops=flops / us / 1e6,
+               peak_tflops=MFMA_FP32_PEAK_TFLOPS, frac=flops / us / 1e6 / MFMA_FP32_PEAK_TFLOPS)
+    if not only:
+        out.update(eager_torch_chunk_gated_delta_rule=res["eager_torch_chunk_gated_delta_rule"],
+                   speedup_vs_eager=res["eager_torch_chunk_gated_delta_rule"]["median_us"] / us)
+    return out
+
+
 def bench_copy(samples: int, only: bool = True) -> dict:
     """Plain device copy of 5 rotated 64 MiB bf16 buffers: a kernel of known HBM traffic
     (read 64 MiB + write 64 MiB per launch) to calibrate FETCH_SIZE / WRITE_SIZE."""
@@ -353,7 +396,8 @@ def main() -> int:
     log(f"device: {torch.cuda.get_device_name(0)}")
 
     if args.only_kernel:
-        fn = dict(gqa=bench_gqa, conv=bench_conv, rmsnorm=bench_rmsnorm, copy=bench_copy)[args.only_kernel]
+        fn = dict(gqa=bench_gqa, conv=bench_conv, rmsnorm=bench_rmsnorm, gdr=bench_gated_delta,
+                  copy=bench_copy)[args.only_kernel]
         print(json.dumps({args.only_kernel: fn(args.kernel_samples, only=True)}), flush=True)
         return 0
 
@@ -366,6 +410,9 @@ def main() -> int:
         log(f"conv: {kernels['packed_conv']['hip']['median_us']:.1f} us, {kernels['packed_conv']['gbs']:.0f} GB/s")
         kernels["add_rmsnorm"] = bench_rmsnorm(args.kernel_samples)
         log(f"rmsnorm: {kernels['add_rmsnorm']['hip']['median_us']:.1f} us, {kernels['add_rmsnorm']['gbs']:.0f} GB/s")
+        kernels["gated_delta"] = bench_gated_delta(args.kernel_samples)
+        log(f"gated delta: {kernels['gated_delta']['hip']['median_us']:.1f} us, "
+            f"{kernels['gated_delta']['tflops']:.1f} TFLOP/s")
         torch.cuda.empty_cache()
 
     fwd = None

@@ -15,22 +15,23 @@
 // Packed requests (cu_seqlens) are chunked per request and each request starts
 // from its own state, so no state crosses a request boundary.
 //
-// Four launches, all on the caller's stream, intermediates in a caller-provided
-// workspace (fd_gated_delta_workspace_bytes):
-//   1. gd_chunk_table — one workgroup: chunk -> (first row, length), request ->
-//      first chunk.
+// Up to four launches, all on the caller's stream, intermediates in a
+// caller-provided workspace (fd_gated_delta_workspace_bytes):
+//   1. gd_chunk_table — packed requests only, one workgroup: chunk -> (first
+//      row, length), request -> first chunk.  A padded batch needs no table.
 //   2. gd_prep_kernel — one workgroup per (chunk, value head), chunk-parallel:
 //      l2norm, cumsum, the Gram and q.k tiles on bf16 MFMA (the normalised q/k
 //      are bf16 values, so these products are exact before fp32 accumulation),
-//      T by forward substitution (one lane per column), u and w on fp32 MFMA.
+//      then u and w as the solutions of (I + L) x = rhs by forward substitution,
+//      one right-hand-side column per thread (256 columns: 128 of u, 128 of w).
 //   3. gd_state_kernel — one workgroup per (request, value head, 16 value
 //      columns): the only sequential part.  Each state column evolves on its
 //      own, so the 128 value columns split over 8 workgroups.  The state slice
-//      lives in registers; the next chunk's operands are prefetched into
-//      registers while the current chunk runs.
+//      lives in registers; every operand of the next chunk is loaded straight
+//      into registers while the current chunk runs; two barriers per chunk.
 //   4. gd_out_kernel — one workgroup per (chunk, value head), chunk-parallel:
 //      o = scale e^{gc} (q S_chunk) + A v'.
-// All fp32 products run on v_mfma_f32_16x16x4_f32 (lane l supplies A[l%16][l/16]
+// The fp32 products run on v_mfma_f32_16x16x4_f32 (lane l supplies A[l%16][l/16]
 // and B[l/16][l%16]; D[4*(l/16)+r][l%16] in register r).  The reduction index k
 // of 16 consecutive MFMAs is assigned as k = 16*(l/16) + s (s = step), so that
 // each lane reads its operands as contiguous runs.
@@ -62,13 +63,14 @@ struct GdArgs {
   int32_t* first;    // [N+1] first chunk of each request
   float* gc;         // [Hv, nc, 64]
   uint16_t* qn;      // [Hv, nc, 64, 128] bf16
-  uint16_t* kn;      // [Hv, nc, 64, 128] bf16
+  uint16_t* kn;      // [Hv, nc, 128 (dk), 64 (t)] bf16, transposed
   float* w;          // [Hv, nc, 64, 128]
   float* u;          // [Hv, nc, 64, 128]
   float* vn;         // [Hv, nc, 128 (dv), 64 (t)]  v' transposed
   float* aq;         // [Hv, nc, 64, 64]
   float* sc;         // [Hv, nc, 128 (dv), 128 (dk)] state at chunk start, transposed
   int hk, hv, nc, nseq;
+  int varlen, seq_len, nct;  // packed requests (table) or a padded batch of nct chunks per sequence
   int beta_f32, l2norm;
   float scale;
 };
@@ -167,39 +169,64 @@ __global__ __launch_bounds__(kThreads) void gd_chunk_table(const int32_t* __rest
 }
 
 // ---------------------------------------------------------------------------
-// 2. per-chunk preparation
-constexpr int kRowK = kD + 8;    // bf16 row stride of the row-major q/k tiles (272 B)
-constexpr int kRowT = kC + 8;    // bf16 row stride of the transposed k/v tiles (144 B)
-constexpr int kRowF = kC + 4;    // fp32 row stride of the 64x64 tiles (272 B)
-constexpr int kPrepK = 0;                                   // bf16 [64][kRowK], later sTg
-constexpr int kPrepQ = kPrepK + kC * kRowK * 2;             // bf16 [64][kRowK], later sTb
-constexpr int kPrepKt = kPrepQ + kC * kRowK * 2;            // bf16 [128][kRowT]
-constexpr int kPrepVt = kPrepKt + kD * kRowT * 2;           // bf16 [128][kRowT]
-constexpr int kPrepL = kPrepVt + kD * kRowT * 2;            // fp32 [64][kRowF]
-constexpr int kPrepG = kPrepL + kC * kRowF * 4;             // fp32 [64]
-constexpr int kPrepB = kPrepG + kC * 4;                     // fp32 [64]
-constexpr int kPrepBytes = kPrepB + kC * 4;
-static_assert(kC * kRowF * 4 <= kC * kRowK * 2, "T tiles must fit in the q/k tiles they reuse");
+// chunk and request ranges: from the table for packed requests, by arithmetic
+// for a padded batch (no table launch)
+__device__ __forceinline__ void chunk_rows(const GdArgs& a, int c, int* r0, int* len) {
+  if (a.varlen) {
+    *r0 = a.row0[c];
+    *len = a.len[c];
+  } else {
+    const int s = c / a.nct;
+    const int j = c - s * a.nct;
+    *r0 = s * a.seq_len + j * kC;
+    *len = min(kC, a.seq_len - j * kC);
+  }
+}
 
+__device__ __forceinline__ void request_chunks(const GdArgs& a, int s, int* first, int* last) {
+  if (a.varlen) {
+    *first = a.first[s];
+    *last = min(a.first[s + 1], a.nc);
+  } else {
+    *first = s * a.nct;
+    *last = (s + 1) * a.nct;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. per-chunk preparation
+constexpr int kRowK = kD + 8;    // bf16 row stride of the row-major q/k/v tiles (272 B)
+constexpr int kRowF = kC + 4;    // fp32 row stride of the 64x64 tiles (272 B)
+constexpr int kPrepK = 0;                                   // bf16 [64][kRowK]
+constexpr int kPrepQ = kPrepK + kC * kRowK * 2;             // bf16 [64][kRowK]
+constexpr int kPrepV = kPrepQ + kC * kRowK * 2;             // bf16 [64][kRowK]
+constexpr int kPrepL = kPrepV + kC * kRowK * 2;             // fp32 [64][kRowF]
+constexpr int kPrepG = kPrepL + kC * kRowF * 4;             // fp32 [64]  gc
+constexpr int kPrepB = kPrepG + kC * 4;                     // fp32 [64]  beta
+constexpr int kPrepBG = kPrepB + kC * 4;                    // fp32 [64]  beta e^gc
+constexpr int kPrepBytes = kPrepBG + kC * 4;
+
+// One workgroup per (chunk, value head).  u = T (beta v) and w = T (beta e^gc k)
+// are the solutions of (I + L) x = rhs; thread j < 128 solves for column j of
+// u, thread 128 + j for column j of w, by forward substitution with the rows of
+// L read from LDS (every lane reads the same address: broadcast).
 __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
   const int h = blockIdx.x % a.hv;
   const int c = blockIdx.x / a.hv;
-  const int L = a.len[c];
+  int r0, L;
+  chunk_rows(a, c, &r0, &L);
   if (L <= 0) return;
-  const int r0 = a.row0[c];
   const int hk = h / (a.hv / a.hk);
   const size_t hc = static_cast<size_t>(h) * a.nc + c;
 
   __shared__ __attribute__((aligned(16))) unsigned char smem[kPrepBytes];
   uint16_t* sK = reinterpret_cast<uint16_t*>(smem + kPrepK);
   uint16_t* sQ = reinterpret_cast<uint16_t*>(smem + kPrepQ);
-  uint16_t* sKt = reinterpret_cast<uint16_t*>(smem + kPrepKt);
-  uint16_t* sVt = reinterpret_cast<uint16_t*>(smem + kPrepVt);
+  uint16_t* sV = reinterpret_cast<uint16_t*>(smem + kPrepV);
   float* sL = reinterpret_cast<float*>(smem + kPrepL);
-  float* sTg = reinterpret_cast<float*>(smem + kPrepK);
-  float* sTb = reinterpret_cast<float*>(smem + kPrepQ);
   float* sG = reinterpret_cast<float*>(smem + kPrepG);
   float* sB = reinterpret_cast<float*>(smem + kPrepB);
+  float* sBG = reinterpret_cast<float*>(smem + kPrepBG);
 
   const int tid = threadIdx.x;
   const int wv = tid >> 6;
@@ -211,7 +238,6 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
   const size_t qk_row = static_cast<size_t>(a.hk) * kD;
   const size_t v_row = static_cast<size_t>(a.hv) * kD;
   uint16_t* gq = a.qn + hc * kC * kD;
-  uint16_t* gk = a.kn + hc * kC * kD;
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int row = it * 16 + wv * 4 + g4;
@@ -227,17 +253,8 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
     }
     *reinterpret_cast<uint4*>(sQ + row * kRowK + c16 * 8) = rq;
     *reinterpret_cast<uint4*>(sK + row * kRowK + c16 * 8) = rk;
+    *reinterpret_cast<uint4*>(sV + row * kRowK + c16 * 8) = rv;
     *reinterpret_cast<uint4*>(gq + row * kD + c16 * 8) = rq;
-    *reinterpret_cast<uint4*>(gk + row * kD + c16 * 8) = rk;
-    const uint32_t kw[4] = {rk.x, rk.y, rk.z, rk.w};
-    const uint32_t vw[4] = {rv.x, rv.y, rv.z, rv.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      sKt[(c16 * 8 + 2 * e) * kRowT + row] = static_cast<uint16_t>(kw[e] & 0xffffu);
-      sKt[(c16 * 8 + 2 * e + 1) * kRowT + row] = static_cast<uint16_t>(kw[e] >> 16);
-      sVt[(c16 * 8 + 2 * e) * kRowT + row] = static_cast<uint16_t>(vw[e] & 0xffffu);
-      sVt[(c16 * 8 + 2 * e + 1) * kRowT + row] = static_cast<uint16_t>(vw[e] >> 16);
-    }
   }
   // g (inclusive cumsum over the chunk) and beta; padded rows carry g = beta = 0
   if (wv == 0) {
@@ -254,6 +271,7 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
     }
     sG[l] = gv;
     sB[l] = bv;
+    sBG[l] = bv * expf(gv);
     a.gc[hc * kC + l] = gv;
   }
   __syncthreads();
@@ -289,71 +307,45 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
   }
   __syncthreads();
 
-  // T = (I + L)^-1 by forward substitution: lane j owns column j
-  if (wv == 0) {
-    const int j = l;
-    float t[kC];
+  // forward substitution (I + L) x = rhs, one column per thread
+  const bool is_w = tid >= kD;   // waves 2, 3
+  const int j = tid & (kD - 1);
+  const uint16_t* src = is_w ? sK : sV;
+  float x[kC];
+  uint32_t kbits[kC / 2];
 #pragma unroll
-    for (int i = 0; i < kC; ++i) {
-      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-#pragma unroll
-      for (int m = 0; m + 4 <= i; m += 4) {
-        const f32x4_t lv = *reinterpret_cast<const f32x4_t*>(sL + i * kRowF + m);
-        a0 = fmaf(lv[0], t[m], a0);
-        a1 = fmaf(lv[1], t[m + 1], a1);
-        a2 = fmaf(lv[2], t[m + 2], a2);
-        a3 = fmaf(lv[3], t[m + 3], a3);
-      }
-#pragma unroll
-      for (int m = i & ~3; m < i; ++m) a0 = fmaf(sL[i * kRowF + m], t[m], a0);
-      t[i] = (i == j ? 1.0f : 0.0f) - ((a0 + a1) + (a2 + a3));
-    }
-    const float bj = sB[j];
-    const float bgj = bj * expf(sG[j]);
-#pragma unroll
-    for (int i = 0; i < kC; ++i) {
-      sTb[i * kRowF + j] = t[i] * bj;
-      sTg[i * kRowF + j] = t[i] * bgj;
-    }
+  for (int i = 0; i < kC; ++i) {
+    const uint32_t bits = src[i * kRowK + j];
+    if (i & 1)
+      kbits[i >> 1] |= bits << 16;
+    else
+      kbits[i >> 1] = bits;
+    x[i] = (is_w ? sBG[i] : sB[i]) * fd_bf16_to_f32(bits);
   }
-  __syncthreads();
-
-  // u = (T beta) v and w = (T beta e^gc) k on fp32 MFMA; wave wv owns rows 16wv..16wv+15
-  float aT[16], aG[16];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const f32x4_t tb = *reinterpret_cast<const f32x4_t*>(sTb + (16 * wv + c16) * kRowF + 16 * g4 + 4 * p);
-    const f32x4_t tg = *reinterpret_cast<const f32x4_t*>(sTg + (16 * wv + c16) * kRowF + 16 * g4 + 4 * p);
+  for (int i = 1; i < kC; ++i) {
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      aT[4 * p + e] = tb[e];
-      aG[4 * p + e] = tg[e];
+    for (int m = 0; m + 4 <= i; m += 4) {
+      const f32x4_t lv = *reinterpret_cast<const f32x4_t*>(sL + i * kRowF + m);
+      a0 = fmaf(lv[0], x[m], a0);
+      a1 = fmaf(lv[1], x[m + 1], a1);
+      a2 = fmaf(lv[2], x[m + 2], a2);
+      a3 = fmaf(lv[3], x[m + 3], a3);
     }
+#pragma unroll
+    for (int m = i & ~3; m < i; ++m) a0 = fmaf(sL[i * kRowF + m], x[m], a0);
+    x[i] = x[i] - ((a0 + a1) + (a2 + a3));
   }
-  float* gu = a.u + hc * kC * kD;
-  float* gw = a.w + hc * kC * kD;
-#pragma unroll 2
-  for (int n = 0; n < 8; ++n) {
-    float bv[16], bk[16];
-    const uint16_t* pv = sVt + (16 * n + c16) * kRowT + 16 * g4;
-    const uint16_t* pk = sKt + (16 * n + c16) * kRowT + 16 * g4;
-    unpack8(*reinterpret_cast<const uint4*>(pv), bv);
-    unpack8(*reinterpret_cast<const uint4*>(pv + 8), bv + 8);
-    unpack8(*reinterpret_cast<const uint4*>(pk), bk);
-    unpack8(*reinterpret_cast<const uint4*>(pk + 8), bk + 8);
-    f32x4_t accU = {};
-    f32x4_t accW = {};
+  float* dst = (is_w ? a.w : a.u) + hc * kC * kD + j;
 #pragma unroll
-    for (int s = 0; s < 16; ++s) {
-      accU = mfma4(aT[s], bv[s], accU);
-      accW = mfma4(aG[s], bk[s], accW);
-    }
+  for (int i = 0; i < kC; ++i) dst[i * kD] = x[i];
+  if (is_w) {
+    // normalised k, transposed ([dk][t]), for the state pass's k^T v' product
+    uint4* kt = reinterpret_cast<uint4*>(a.kn + hc * kC * kD + static_cast<size_t>(j) * kC);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 16 * wv + 4 * g4 + r;
-      gu[row * kD + 16 * n + c16] = accU[r];
-      gw[row * kD + 16 * n + c16] = accW[r];
-    }
+    for (int i = 0; i < kC / 8; ++i)
+      kt[i] = make_uint4(kbits[4 * i], kbits[4 * i + 1], kbits[4 * i + 2], kbits[4 * i + 3]);
   }
 }
 
@@ -363,16 +355,19 @@ constexpr int kRowS = kD + 4;    // fp32 row stride of the transposed state slic
 constexpr int kRowV = kC + 4;    // fp32 row stride of the transposed v' slice
 
 __global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
-  const int js = blockIdx.x % kSlices;
-  const int h = (blockIdx.x / kSlices) % a.hv;
-  const int sq = blockIdx.x / (kSlices * a.hv);
-  const int first = a.first[sq];
-  const int last = min(a.first[sq + 1], a.nc);
+  // XCD-aware order: block b runs on XCD b % 8; the logical index below gives
+  // each XCD a contiguous range, so the 8 column slices of one head (which read
+  // the same w / k tiles) share one L2.  The grid is a multiple of 8.
+  const int nb = gridDim.x;
+  const int lb = (blockIdx.x % 8) * (nb / 8) + blockIdx.x / 8;
+  const int js = lb % kSlices;
+  const int h = (lb / kSlices) % a.hv;
+  const int sq = lb / (kSlices * a.hv);
+  int first, last;
+  request_chunks(a, sq, &first, &last);
 
   __shared__ __attribute__((aligned(16))) float sSt[kSlice * kRowS];
-  __shared__ __attribute__((aligned(16))) uint16_t sKt[kD * kRowT];
   __shared__ __attribute__((aligned(16))) float sVd[kSlice * kRowV];
-  __shared__ float sGc[kC];
 
   const int tid = threadIdx.x;
   const int wv = tid >> 6;
@@ -390,40 +385,34 @@ __global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
     for (int r = 0; r < 4; ++r)
       S[m][r] = a.s0 ? a.s0[state_base + static_cast<size_t>(32 * wv + 16 * m + 4 * g4 + r) * kD + col] : 0.0f;
 
-  // prefetch registers for one chunk
-  uint4 pk[4];
-  f32x4_t pw[8];
-  float pu[4];
-  float pg = 0.0f;
+  // operands of one chunk, loaded straight into registers one chunk ahead
+  f32x4_t pw[8];   // w[16wv + c16][32g4 .. 32g4 + 31]       (A of w S)
+  float pu[4];     // u[16wv + 4g4 + r][col]                 (C layout)
+  uint4 pk[2][2];  // k^T[32wv + 16m + c16][16g4 .. +15]     (A of k^T v')
+  f32x4_t pgc;     // gc[16wv + 4g4 .. +3]
+  float pgl;       // gc[63]
   auto prefetch = [&](int c) {
     const size_t hc = static_cast<size_t>(h) * a.nc + c;
-    const uint16_t* kn = a.kn + hc * kC * kD;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pk[i] = *reinterpret_cast<const uint4*>(kn + ((tid >> 4) + 16 * i) * kD + (tid & 15) * 8);
     const float* w = a.w + hc * kC * kD + (16 * wv + c16) * kD + 32 * g4;
 #pragma unroll
     for (int i = 0; i < 8; ++i) pw[i] = *reinterpret_cast<const f32x4_t*>(w + 4 * i);
-    const float* u = a.u + hc * kC * kD;
+    const float* u = a.u + hc * kC * kD + col;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) pu[r] = u[(16 * wv + 4 * g4 + r) * kD + col];
-    if (wv == 0) pg = a.gc[hc * kC + l];
+    for (int r = 0; r < 4; ++r) pu[r] = u[(16 * wv + 4 * g4 + r) * kD];
+    const uint16_t* kt = a.kn + hc * kC * kD + 16 * g4;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const uint16_t* row = kt + (32 * wv + 16 * m + c16) * kC;
+      pk[m][0] = *reinterpret_cast<const uint4*>(row);
+      pk[m][1] = *reinterpret_cast<const uint4*>(row + 8);
+    }
+    pgc = *reinterpret_cast<const f32x4_t*>(a.gc + hc * kC + 16 * wv + 4 * g4);
+    pgl = a.gc[hc * kC + kC - 1];
   };
   if (first < last) prefetch(first);
 
   for (int c = first; c < last; ++c) {
     const size_t hc = static_cast<size_t>(h) * a.nc + c;
-    // stage this chunk's k (transposed) and gc; keep w / u in registers
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = (tid >> 4) + 16 * i;
-      const uint32_t kw[4] = {pk[i].x, pk[i].y, pk[i].z, pk[i].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        sKt[((tid & 15) * 8 + 2 * e) * kRowT + row] = static_cast<uint16_t>(kw[e] & 0xffffu);
-        sKt[((tid & 15) * 8 + 2 * e + 1) * kRowT + row] = static_cast<uint16_t>(kw[e] >> 16);
-      }
-    }
-    if (wv == 0) sGc[l] = pg;
     float cw[32];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
@@ -432,6 +421,14 @@ __global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
     float cu[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) cu[r] = pu[r];
+    float ak[2][16];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      unpack8(pk[m][0], ak[m]);
+      unpack8(pk[m][1], ak[m] + 8);
+    }
+    const f32x4_t gct = pgc;
+    const float gl = pgl;
     if (c + 1 < last) prefetch(c + 1);
 
     // state at the chunk start: to LDS (transposed, for w S) and to the workspace (for the output pass)
@@ -445,7 +442,7 @@ __global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
     }
     __syncthreads();
 
-    // v' = u - w S for rows 16wv..16wv+15 of this slice
+    // v' = u - w S for rows 16wv..16wv+15 of this slice (two independent MFMA chains)
     float bS[32];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -453,15 +450,18 @@ __global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) bS[4 * i + e] = sv[e];
     }
-    f32x4_t acc = {};
+    f32x4_t acc0 = {};
+    f32x4_t acc1 = {};
 #pragma unroll
-    for (int s = 0; s < 32; ++s) acc = mfma4(cw[s], bS[s], acc);
-    const float gl = sGc[kC - 1];
+    for (int s = 0; s < 16; ++s) {
+      acc0 = mfma4(cw[s], bS[s], acc0);
+      acc1 = mfma4(cw[16 + s], bS[16 + s], acc1);
+    }
     f32x4_t vnew, vdec;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      vnew[r] = cu[r] - acc[r];
-      vdec[r] = vnew[r] * expf(gl - sGc[16 * wv + 4 * g4 + r]);
+      vnew[r] = cu[r] - (acc0[r] + acc1[r]);
+      vdec[r] = vnew[r] * expf(gl - gct[r]);
     }
     *reinterpret_cast<f32x4_t*>(a.vn + hc * kD * kC + static_cast<size_t>(col) * kC + 16 * wv + 4 * g4) = vnew;
     *reinterpret_cast<f32x4_t*>(sVd + c16 * kRowV + 16 * wv + 4 * g4) = vdec;
@@ -476,19 +476,20 @@ __global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
       for (int e = 0; e < 4; ++e) bV[4 * i + e] = vv[e];
     }
     const float egl = expf(gl);
+    f32x4_t st0 = {S[0][0] * egl, S[0][1] * egl, S[0][2] * egl, S[0][3] * egl};
+    f32x4_t st1 = {S[1][0] * egl, S[1][1] * egl, S[1][2] * egl, S[1][3] * egl};
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      float ak[16];
-      const uint16_t* pkt = sKt + (32 * wv + 16 * m + c16) * kRowT + 16 * g4;
-      unpack8(*reinterpret_cast<const uint4*>(pkt), ak);
-      unpack8(*reinterpret_cast<const uint4*>(pkt + 8), ak + 8);
-      f32x4_t st = {S[m][0] * egl, S[m][1] * egl, S[m][2] * egl, S[m][3] * egl};
-#pragma unroll
-      for (int s = 0; s < 16; ++s) st = mfma4(ak[s], bV[s], st);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) S[m][r] = st[r];
+    for (int s = 0; s < 16; ++s) {
+      st0 = mfma4(ak[0][s], bV[s], st0);
+      st1 = mfma4(ak[1][s], bV[s], st1);
     }
-    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      S[0][r] = st0[r];
+      S[1][r] = st1[r];
+    }
+    // no third barrier: the next writes of sSt follow this iteration's second
+    // barrier, and the next writes of sVd follow the next iteration's first
   }
 
   if (a.sN != nullptr) {
@@ -505,9 +506,9 @@ __global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
 __global__ __launch_bounds__(kThreads) void gd_out_kernel(GdArgs a) {
   const int h = blockIdx.x % a.hv;
   const int c = blockIdx.x / a.hv;
-  const int L = a.len[c];
+  int r0, L;
+  chunk_rows(a, c, &r0, &L);
   if (L <= 0) return;
-  const int r0 = a.row0[c];
   const size_t hc = static_cast<size_t>(h) * a.nc + c;
 
   __shared__ __attribute__((aligned(16))) uint16_t sQ[kC * kRowK];
@@ -705,13 +706,16 @@ extern "C" FD_API int fd_gated_delta_fwd(const void* q, const void* k, const voi
   a.hv = v_heads;
   a.nc = static_cast<int>(nc);
   a.nseq = static_cast<int>(nseq);
+  a.varlen = varlen;
+  a.seq_len = seq_len;
+  a.nct = (seq_len + kC - 1) / kC;
   a.beta_f32 = beta_dtype == FD_DTYPE_F32;
   a.l2norm = l2norm_qk != 0;
   a.scale = scale;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int total = batch * seq_len;
-  hipLaunchKernelGGL(gd_chunk_table, dim3(1), dim3(kThreads), 0, s, cu_seqlens, a.nseq, seq_len, total, a);
+  if (varlen) hipLaunchKernelGGL(gd_chunk_table, dim3(1), dim3(kThreads), 0, s, cu_seqlens, a.nseq, seq_len, total, a);
   if (nc > 0) {
     hipLaunchKernelGGL(gd_prep_kernel, dim3(static_cast<unsigned>(nc * v_heads)), dim3(kThreads), 0, s, a);
   }
