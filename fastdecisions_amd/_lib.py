@@ -55,6 +55,11 @@ SIGNATURES = {
         ctypes.c_int64,
         [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int],
     ),
+    "fd_gate_transform_fwd": (
+        ctypes.c_int,
+        [_c_void_p, _c_void_p, ctypes.c_int64, ctypes.c_int64, _c_void_p, ctypes.c_int, _c_void_p, ctypes.c_int,
+         _c_void_p, _c_void_p, ctypes.c_int64, ctypes.c_int, _c_void_p],
+    ),
     "fd_gated_delta_fwd": (
         ctypes.c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,

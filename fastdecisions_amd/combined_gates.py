@@ -1,0 +1,51 @@
+"""Combined a/b gate projection and the ``fastdecisions::unpack_gate`` op.
+
+Mirrors ref: src/decider/combined_gates.py: ``unpack_gate_op(combined, a_log,
+dt_bias) -> (decay, beta)`` over ``unpack_gate`` (ref: :6-16), and
+``install_combined_gates(core)`` (ref: :19-43), which snapshots
+``cat(in_proj_a.weight, in_proj_b.weight)`` into a non-persistent buffer so the
+packed Gated-DeltaNet forward computes both gate projections with one GEMM and
+the transform with one kernel (``fastdecisions_amd.packed_conv._forward``).
+Reinvoke after changing the projection weights.  Any head count works (the
+reference requires two bias-free [16, 2048] projections).
+"""
+from __future__ import annotations
+
+import torch
+
+from .unpack_gate_transform_kernel import unpack_gate
+
+
+@torch.library.custom_op("fastdecisions::unpack_gate", mutates_args=(), device_types="cuda")
+def unpack_gate_op(combined: torch.Tensor, a_log: torch.Tensor,
+                   dt_bias: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    return unpack_gate(combined, a_log, dt_bias)
+
+
+@unpack_gate_op.register_fake
+def _fake(combined, a_log, dt_bias):
+    shape = (*combined.shape[:-1], combined.shape[-1] // 2)
+    return (combined.new_empty(shape, dtype=torch.float32),
+            combined.new_empty(shape, dtype=torch.bfloat16))
+
+
+def install_combined_gates(core) -> int:
+    """Snapshot the combined a/b weight of every Gated-DeltaNet layer; return the count."""
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5GatedDeltaNet
+    from .packed_conv import install_packed_conv
+    install_packed_conv(core)
+    count = 0
+    for module in core.modules():
+        if isinstance(module, Qwen3_5GatedDeltaNet):
+            a, b = module.in_proj_a, module.in_proj_b
+            if (a.weight.shape != b.weight.shape or a.weight.shape[0] != module.num_v_heads
+                    or a.bias is not None or b.bias is not None):
+                raise ValueError("Combined gates require two bias-free [num_v_heads, hidden] projections")
+            with torch.no_grad():
+                weight = torch.cat((a.weight, b.weight), dim=0).detach()
+            if "_combined_gate_weight" in module._buffers:
+                module._combined_gate_weight = weight
+            else:
+                module.register_buffer("_combined_gate_weight", weight, persistent=False)
+            count += 1
+    return count

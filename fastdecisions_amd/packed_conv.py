@@ -83,10 +83,16 @@ def _forward(self, hidden_states, cache_params=None, attention_mask=None, **kwar
     else:
         query, key, value = packed_conv(mixed, self.conv1d.weight)
     z = self.in_proj_z(hidden_states).reshape(batch, seq, -1, self.head_v_dim)
-    b = self.in_proj_b(hidden_states)
-    a = self.in_proj_a(hidden_states)
-    beta = b.sigmoid()
-    g = -self.A_log.float().exp() * F.softplus(a.float() + self.dt_bias)
+    if hasattr(self, "_combined_gate_weight"):
+        # one GEMM for both gate projections, one kernel for both transforms (ref: :45-48)
+        from .combined_gates import unpack_gate_op
+        combined = F.linear(hidden_states, self._combined_gate_weight)
+        g, beta = unpack_gate_op(combined, self.A_log, self.dt_bias)
+    else:
+        b = self.in_proj_b(hidden_states)
+        a = self.in_proj_a(hidden_states)
+        beta = b.sigmoid()
+        g = -self.A_log.float().exp() * F.softplus(a.float() + self.dt_bias)
     segments = _segments(kwargs)
     if getattr(self, "_fd_gated_delta", False):
         from .gated_delta import gated_delta_rule

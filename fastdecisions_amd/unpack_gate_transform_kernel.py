@@ -1,0 +1,69 @@
+"""Gate transform of the Gated-DeltaNet layers on the gfx950 HIP kernel ``fd_gate_transform_fwd``.
+
+Drop-in for the reference's ``unpack_gate(combined, a_log, dt_bias)``
+(ref: src/decider/unpack_gate_transform_kernel.py:94-133): ``combined`` is the
+``[B, T, 2H]`` bf16 output of the combined a/b projection (a in the first H
+channels, b in the last H), ``a_log`` / ``dt_bias`` are ``[H]`` bf16 or fp32;
+returns ``decay = -exp(a_log) * softplus(a + dt_bias)`` fp32 ``[B, T, H]`` and
+``beta = sigmoid(b)`` bf16 ``[B, T, H]``, launched on the current stream.  The
+reference fixes H = 16; any H works here.
+
+``gate_transform(a, b, a_log, dt_bias)`` takes the two projections separately
+(any row-contiguous ``[B, T, H]`` views, e.g. of one combined tensor).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_PARAM_DTYPES = {torch.bfloat16: _lib.FD_DTYPE_BF16, torch.float32: _lib.FD_DTYPE_F32}
+
+
+def _check_params(a_log, dt_bias, heads, device):
+    for name, parameter in (("a_log", a_log), ("dt_bias", dt_bias)):
+        if parameter.shape != (heads,):
+            raise ValueError(f"{name} must have shape [{heads}]")
+        if parameter.device != device:
+            raise ValueError(f"{name} must share combined's device")
+        if parameter.dtype not in _PARAM_DTYPES:
+            raise ValueError(f"{name} must be BF16 or FP32")
+        if not parameter.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+
+
+def gate_transform(a: torch.Tensor, b: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor):
+    if not a.is_cuda or a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16 or b.device != a.device:
+        raise ValueError("a and b must be CUDA BF16 on one device")
+    if a.ndim != 3 or a.shape != b.shape:
+        raise ValueError("a and b must have the same shape [B, T, H]")
+    B, T, H = a.shape
+    if B < 1 or T < 1:
+        raise ValueError("B and T must be positive")
+    for t in (a, b):
+        if t.stride(2) != 1 or t.stride(0) != T * t.stride(1):
+            raise ValueError("a and b must be row-contiguous views [B, T, H] (unit head stride, packed rows)")
+    _check_params(a_log, dt_bias, H, a.device)
+    with torch.cuda.device(a.device):
+        decay = torch.empty((B, T, H), device=a.device, dtype=torch.float32)
+        beta = torch.empty((B, T, H), device=a.device, dtype=torch.bfloat16)
+        _lib.check("fd_gate_transform_fwd", _lib.lib().fd_gate_transform_fwd(
+            a.data_ptr(), b.data_ptr(), a.stride(1), b.stride(1), a_log.data_ptr(), _PARAM_DTYPES[a_log.dtype],
+            dt_bias.data_ptr(), _PARAM_DTYPES[dt_bias.dtype], decay.data_ptr(), beta.data_ptr(), B * T, H,
+            _lib.stream_handle(a.device)))
+    return decay, beta
+
+
+def unpack_gate(combined: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor):
+    # combined: contiguous BF16 [B, T, 2H]
+    if combined.ndim != 3 or combined.shape[-1] % 2:
+        raise ValueError("combined must have shape [B, T, 2H]")
+    if not combined.is_cuda or combined.dtype != torch.bfloat16:
+        raise ValueError("combined must be CUDA BF16")
+    if not combined.is_contiguous():
+        raise ValueError("combined must be contiguous")
+    B, T, H2 = combined.shape
+    if B < 1 or T < 1:
+        raise ValueError("B and T must be positive")
+    H = H2 // 2
+    return gate_transform(combined[..., :H], combined[..., H:], a_log, dt_bias)

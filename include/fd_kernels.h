@@ -17,6 +17,9 @@
  *   fd_gated_delta_fwd  chunked gated delta rule of the Gated-DeltaNet layers
  *                       replaces the torch_chunk_gated_delta_rule call
  *                       (ref: src/decider/packed_conv.py:55-59)
+ *   fd_gate_transform_fwd  gate transform (decay g and beta) of the Gated-DeltaNet layers
+ *                       replaces unpack_gate(combined, a_log, dt_bias)
+ *                       (ref: src/decider/unpack_gate_transform_kernel.py:94-133, kernel :51-91)
  *
  * Conventions shared by every entry point:
  *   - every tensor pointer is a device pointer; bf16 tensors are passed as raw
@@ -42,7 +45,7 @@ extern "C" {
 #define FD_API
 #endif
 
-#define FD_ABI_VERSION 2
+#define FD_ABI_VERSION 3
 
 #define FD_OK 0
 #define FD_ERR_INVALID_ARGUMENT (-1) /* shape, size, stride or flag out of range */
@@ -175,6 +178,26 @@ FD_API int fd_gated_delta_fwd(const void* q, const void* k, const void* v, const
                               int batch, int seq_len, int k_heads, int v_heads, int head_k_dim,
                               int head_v_dim, float scale, int beta_dtype, int l2norm_qk,
                               const int32_t* cu_seqlens, int n_seqs, void* stream);
+
+/*
+ * Gate transform of the Gated-DeltaNet layers (ref: src/decider/unpack_gate_transform_kernel.py:51-91,
+ * the eager form at ref: src/decider/packed_conv.py:49-53):
+ *   g[r, h]    = -exp(a_log[h]) * softplus(a[r, h] + dt_bias[h])   fp32
+ *                softplus(x) = x > 20 ? x : log1p(exp(x))
+ *   beta[r, h] = bf16(1 / (1 + exp(-b[r, h])))
+ * fp32 arithmetic with the same library exp / log1p as PyTorch's elementwise kernels.
+ *
+ *   a, b          [rows, heads] bf16 with row strides a_row_stride, b_row_stride
+ *                 (elements; a and b may be the two halves of one combined
+ *                 projection output, ref: src/decider/combined_gates.py:19-43)
+ *   a_log, dt_bias [heads] of a_log_dtype / dt_bias_dtype (FD_DTYPE_BF16 or FD_DTYPE_F32)
+ *   g             [rows, heads] fp32 contiguous
+ *   beta          [rows, heads] bf16 contiguous
+ */
+FD_API int fd_gate_transform_fwd(const void* a, const void* b, int64_t a_row_stride,
+                                 int64_t b_row_stride, const void* a_log, int a_log_dtype,
+                                 const void* dt_bias, int dt_bias_dtype, float* g, void* beta,
+                                 int64_t rows, int heads, void* stream);
 
 #ifdef __cplusplus
 }

@@ -231,6 +231,19 @@ def gqa_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, *, scale: float |
 
 # ---------------------------------------------------------------- readout
 
+def gate_transform(a_bits: np.ndarray, b_bits: np.ndarray, a_log, dt_bias) -> tuple[np.ndarray, np.ndarray]:
+    """Gated-DeltaNet gate transform in float64 (ref: src/decider/unpack_gate_transform_kernel.py:69-88;
+    eager form ref: src/decider/packed_conv.py:49-53): g = -exp(a_log) * softplus(a + dt_bias) with
+    softplus(x) = x if x > 20 else log1p(exp(x)), and beta = sigmoid(b) (before its bf16 rounding).
+    a, b: bf16 bits [..., H]; a_log, dt_bias: float [H] (bf16 parameters already widened)."""
+    # the eager sum a.float() + dt_bias is one fp32 addition; the rest is exact here
+    x = (bf16_to_f32(a_bits) + np.asarray(dt_bias, np.float32)).astype(np.float64)
+    sp = np.where(x > 20, x, np.log1p(np.exp(np.minimum(x, 20.0))))
+    g = -np.exp(np.asarray(a_log, np.float64)) * sp
+    beta = 1.0 / (1.0 + np.exp(-bf16_to_f32(b_bits).astype(np.float64)))
+    return g, beta
+
+
 def decide(logits: np.ndarray, nopts) -> tuple[np.ndarray, np.ndarray]:
     """Masked softmax over the first nopts[i] letters of each slot, then argmax.
 

@@ -18,7 +18,10 @@ repository's oracle or kernels:
   ``use_qk_l2norm_in_kernel=True`` on bf16 q/k, as the decider's layers call it,
   ref: src/decider/packed_conv.py:55-59), per request for varlen, q/k heads
   expanded by ``repeat_interleave`` as ``Qwen3_5GatedDeltaNet.forward`` does,
-  and transformers' ``l2norm`` on bf16 rows.
+  and transformers' ``l2norm`` on bf16 rows;
+* gate transform: the eager expressions ``-A_log.float().exp() * F.softplus(a.float()
+  + dt_bias)`` and ``b.sigmoid()`` (ref: src/decider/packed_conv.py:49-53) on bf16
+  a, b and bf16 / fp32 parameters.
 
 bf16 arrays are stored as uint16 bit patterns.  Each fixture is small (< 1 MB).
 """
@@ -218,8 +221,24 @@ def make_gated_delta(g: torch.Generator) -> dict:
     return out
 
 
+def make_gates(g: torch.Generator) -> dict:
+    H = 16
+    a = (torch.randn((1, 300, H), generator=g) * 4).to(torch.bfloat16)
+    b = (torch.randn((1, 300, H), generator=g) * 4).to(torch.bfloat16)
+    a[0, :4] = torch.tensor([19.5, 20.0, 20.5, 40.0]).to(torch.bfloat16)[:, None]  # around softplus's threshold
+    a_log = torch.log(torch.empty(H).uniform_(1, 16, generator=g))
+    dt_bias = torch.ones(H) + 0.1 * torch.randn(H, generator=g)
+    out = dict(a=bits(a), b=bits(b))
+    for tag, dt in (("bf16", torch.bfloat16), ("f32", torch.float32)):
+        al, db = a_log.to(dt), dt_bias.to(dt)
+        gg = -al.float().exp() * F.softplus(a.float() + db)
+        out.update({f"{tag}_a_log": al.float().numpy(), f"{tag}_dt_bias": db.float().numpy(), f"{tag}_g": gg.numpy()})
+    out["beta"] = bits(b.sigmoid())
+    return out
+
+
 FIXTURES = (("conv", make_conv), ("rmsnorm", make_rms), ("gqa", make_gqa), ("readout", make_readout),
-            ("gated_delta", make_gated_delta))
+            ("gated_delta", make_gated_delta), ("gates", make_gates))
 
 
 def main(names=None) -> None:

@@ -21,7 +21,8 @@ def declared_functions() -> set[str]:
 
 def test_header_declares_the_expected_entry_points():
     assert declared_functions() == {"fd_abi_version", "fd_last_error", "fd_gqa_fwd", "fd_packed_conv_fwd",
-                                    "fd_add_rmsnorm_fwd", "fd_gated_delta_workspace_bytes", "fd_gated_delta_fwd"}
+                                    "fd_add_rmsnorm_fwd", "fd_gated_delta_workspace_bytes", "fd_gated_delta_fwd",
+                                    "fd_gate_transform_fwd"}
 
 
 def test_library_exports_every_declared_symbol_and_nothing_else():
@@ -134,6 +135,22 @@ def test_gated_delta_argument_errors():
     assert call(scale=0.0) == _lib.FD_ERR_INVALID_ARGUMENT
     assert call(work=None) == _lib.FD_ERR_INVALID_ARGUMENT
     assert call(B=0, ws=0) == _lib.FD_OK  # empty batch: nothing to launch
+
+
+def test_gate_transform_argument_errors():
+    from fastdecisions_amd import _lib
+    lib = _lib.lib()
+    f = 1 << 20
+
+    def call(a=f, sa=32, sb=32, ld=0, bd=1, rows=2048, heads=16):
+        return lib.fd_gate_transform_fwd(a, f + 32, sa, sb, f, ld, f, bd, f, f, rows, heads, None)
+
+    assert call(a=None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert call(heads=0) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert call(sa=8) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert call(ld=3) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert "dtypes" in _err(lib)
+    assert call(rows=0) == _lib.FD_OK
 
 
 def test_python_wrappers_keep_the_reference_errors_on_cpu_tensors():

@@ -402,3 +402,44 @@ def test_planted_gated_delta_slips_fail_the_golden(oracle, gd, golden):
 
     for slip in ("no_decay", "decay_after", "beta_outside", "sign", "output_before_write"):
         assert not _close_to_bf16_golden(oracle, slipped(slip), want), slip
+
+
+# ------------------------------------------------------------------ gate transform
+
+def _f32_ulps(got, want):
+    want = np.asarray(want, np.float64)
+    return np.abs(np.asarray(got, np.float64) - want) / np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+
+
+@pytest.mark.parametrize("tag", ["bf16", "f32"])
+def test_gate_transform_matches_eager_golden(oracle, golden, tag):
+    d = golden("gates")
+    g, beta = oracle.gate_transform(d["a"], d["b"], d[f"{tag}_a_log"], d[f"{tag}_dt_bias"])
+    assert _f32_ulps(g, d[f"{tag}_g"]).max() < 4
+    assert np.array_equal(oracle.f32_to_bf16(beta.astype(np.float32)), d["beta"])
+
+
+def test_gate_transform_closed_forms(oracle):
+    a = oracle.f32_to_bf16(np.array([[25.0, 0.0, -30.0]], np.float32))
+    b = oracle.f32_to_bf16(np.array([[0.0, 80.0, -80.0]], np.float32))
+    g, beta = oracle.gate_transform(a, b, np.zeros(3), np.zeros(3))
+    # above the threshold softplus is the identity; softplus(0) = ln 2; softplus(-30) = e^-30 to 1e-13
+    assert g[0, 0] == -25.0 and np.isclose(g[0, 1], -np.log(2.0)) and np.isclose(g[0, 2], -np.exp(-30.0))
+    assert beta[0, 0] == 0.5 and beta[0, 1] == 1.0 and beta[0, 2] < 1e-34
+    # the decay scales with exp(a_log)
+    g2, _ = oracle.gate_transform(a, b, np.full(3, np.log(4.0)), np.zeros(3))
+    assert np.allclose(g2, 4 * g)
+
+
+def test_planted_gate_slips_fail_the_golden(oracle, golden):
+    d = golden("gates")
+    want = d["f32_g"]
+    a_log, bias = d["f32_a_log"], d["f32_dt_bias"]
+    good, _ = oracle.gate_transform(d["a"], d["b"], a_log, bias)
+    assert _f32_ulps(good, want).max() < 4
+    x = oracle.bf16_to_f32(d["a"]).astype(np.float64) + bias
+    sp = np.where(x > 20, x, np.log1p(np.exp(np.minimum(x, 20.0))))
+    for slip in (-a_log * sp,                        # log-space decay without the exp
+                 -np.exp(a_log) * np.log1p(np.exp(np.minimum(oracle.bf16_to_f32(d["a"]), 20.0))),  # bias dropped
+                 np.exp(a_log) * sp):                 # sign
+        assert _f32_ulps(slip, want).max() > 100
