@@ -62,6 +62,8 @@ struct GqaArgs {
   const uint16_t* v;
   uint16_t* o;
   int64_t qs[4], ks[4], vs[4], os[4];
+  const uint16_t* gate;  // output gate (fd_gqa_gated_fwd) or null
+  int64_t gs[4];
   int q_heads, kv_heads, seq_len;
   float scale_log2;
   const int32_t* cu;
@@ -438,6 +440,7 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
   const float inv = 1.0f / l_tot;
   if (qvalid) {
     uint16_t* orow = obase + qpos * a.os[2];
+    const uint16_t* grow = a.gate ? a.gate + bidx * a.gs[0] + qhead * a.gs[1] + qpos * a.gs[2] : nullptr;
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
@@ -445,7 +448,21 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
         const int d = db * 32 + r4 * 8 + half * 4;
         f32x4_t v4 = {o[db][r4 * 4 + 0] * inv, o[db][r4 * 4 + 1] * inv, o[db][r4 * 4 + 2] * inv,
                       o[db][r4 * 4 + 3] * inv};
-        *reinterpret_cast<bf16x4_t*>(orow + d) = __builtin_convertvector(v4, bf16x4_t);
+        bf16x4_t ob = __builtin_convertvector(v4, bf16x4_t);
+        if (grow != nullptr) {
+          // output gate: bf16(o) * bf16(sigmoid(gate)), each product rounded to bf16 as the eager ops do
+          const bf16x4_t gb = *reinterpret_cast<const bf16x4_t*>(grow + d);
+          const f32x4_t gf = __builtin_convertvector(gb, f32x4_t);
+          const f32x4_t of = __builtin_convertvector(ob, f32x4_t);
+          f32x4_t sg, pr;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sg[e] = 1.0f / (1.0f + expf(-gf[e]));
+          const f32x4_t sgr = __builtin_convertvector(__builtin_convertvector(sg, bf16x4_t), f32x4_t);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) pr[e] = of[e] * sgr[e];
+          ob = __builtin_convertvector(pr, bf16x4_t);
+        }
+        *reinterpret_cast<bf16x4_t*>(orow + d) = ob;
       }
     }
   }
@@ -467,12 +484,10 @@ bool stride_ok(const int64_t s[4]) {
   return true;
 }
 
-}  // namespace
-
-extern "C" int fd_gqa_fwd(const void* q, const void* k, const void* v, void* out, const int64_t q_strides[4],
-                          const int64_t k_strides[4], const int64_t v_strides[4], const int64_t out_strides[4],
-                          int batch, int q_heads, int kv_heads, int seq_len, int head_dim, float scale,
-                          const int32_t* cu_seqlens, int n_seqs, int max_seqlen, void* stream) {
+int gqa_launch(const void* q, const void* k, const void* v, void* out, const int64_t q_strides[4],
+               const int64_t k_strides[4], const int64_t v_strides[4], const int64_t out_strides[4],
+               const void* gate, const int64_t gate_strides[4], int batch, int q_heads, int kv_heads, int seq_len,
+               int head_dim, float scale, const int32_t* cu_seqlens, int n_seqs, int max_seqlen, void* stream) {
   FD_REQUIRE(q && k && v && out && q_strides && k_strides && v_strides && out_strides, FD_ERR_INVALID_ARGUMENT,
              "fd_gqa_fwd: tensor and stride pointers must be non-null");
   FD_REQUIRE(batch >= 0 && seq_len >= 0 && q_heads >= 1 && kv_heads >= 1, FD_ERR_INVALID_ARGUMENT,
@@ -511,6 +526,8 @@ extern "C" int fd_gqa_fwd(const void* q, const void* k, const void* v, void* out
   a.k = static_cast<const uint16_t*>(k);
   a.v = static_cast<const uint16_t*>(v);
   a.o = static_cast<uint16_t*>(out);
+  a.gate = static_cast<const uint16_t*>(gate);
+  for (int i = 0; i < 4; ++i) a.gs[i] = gate ? gate_strides[i] : 0;
   for (int i = 0; i < 4; ++i) {
     a.qs[i] = q_strides[i];
     a.ks[i] = k_strides[i];
@@ -545,4 +562,27 @@ extern "C" int fd_gqa_fwd(const void* q, const void* k, const void* v, void* out
       break;
   }
   return fd_check_launch("fd_gqa_fwd");
+}
+
+}  // namespace
+
+extern "C" int fd_gqa_fwd(const void* q, const void* k, const void* v, void* out, const int64_t q_strides[4],
+                          const int64_t k_strides[4], const int64_t v_strides[4], const int64_t out_strides[4],
+                          int batch, int q_heads, int kv_heads, int seq_len, int head_dim, float scale,
+                          const int32_t* cu_seqlens, int n_seqs, int max_seqlen, void* stream) {
+  return gqa_launch(q, k, v, out, q_strides, k_strides, v_strides, out_strides, nullptr, nullptr, batch, q_heads,
+                    kv_heads, seq_len, head_dim, scale, cu_seqlens, n_seqs, max_seqlen, stream);
+}
+
+extern "C" int fd_gqa_gated_fwd(const void* q, const void* k, const void* v, const void* gate, void* out,
+                                const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4],
+                                const int64_t gate_strides[4], const int64_t out_strides[4], int batch,
+                                int q_heads, int kv_heads, int seq_len, int head_dim, float scale,
+                                const int32_t* cu_seqlens, int n_seqs, int max_seqlen, void* stream) {
+  FD_REQUIRE(gate && gate_strides, FD_ERR_INVALID_ARGUMENT, "fd_gqa_gated_fwd: gate and its strides must be non-null");
+  FD_REQUIRE(fd_aligned16(gate) && gate_strides[3] == 1 && gate_strides[0] % 8 == 0 && gate_strides[1] % 8 == 0 &&
+                 gate_strides[2] % 8 == 0,
+             FD_ERR_ALIGNMENT, "fd_gqa_gated_fwd: gate must keep 16-byte rows with a unit innermost stride");
+  return gqa_launch(q, k, v, out, q_strides, k_strides, v_strides, out_strides, gate, gate_strides, batch, q_heads,
+                    kv_heads, seq_len, head_dim, scale, cu_seqlens, n_seqs, max_seqlen, stream);
 }

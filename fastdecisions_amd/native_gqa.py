@@ -13,7 +13,12 @@ here they are part of the package:
   ``Qwen3_5Attention`` of a model and returns the count.  Unsupported calls
   (KV cache, training, grad, non-CUDA, non-bf16) fall back to the original
   forward, as the other install patches of the reference do
-  (ref: src/decider/packed_conv.py:27-38).
+  (ref: src/decider/packed_conv.py:27-38);
+* ``attn_prologue`` / ``native_gqa_gated`` — the attention layer's prologue
+  (q/k RMSNorm + partial RoPE, one kernel) and the attention with its sigmoid
+  output gate applied in the store; ``install_attention_fusions(core)``
+  switches ``candidate_forward`` to them (q/k/v projections and o_proj stay
+  library GEMMs).
 """
 from __future__ import annotations
 
@@ -21,6 +26,9 @@ from types import MethodType
 
 import torch
 
+from typing import Optional
+
+from .attention_prologue_kernel import attention_prologue
 from .native_gqa_kernel import native_gqa_attention
 
 
@@ -47,6 +55,55 @@ def _native_gqa_varlen_fake(q, k, v, cu_seqlens, max_seqlen):
     return q.new_empty((b, t, h, d)).permute(0, 2, 1, 3)
 
 
+@torch.library.custom_op("fastdecisions::attn_prologue", mutates_args=(), device_types="cuda")
+def attn_prologue(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
+                  cos: torch.Tensor, sin: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    return attention_prologue(q, k, q_weight, k_weight, cos, sin, eps)
+
+
+@attn_prologue.register_fake
+def _attn_prologue_fake(q, k, q_weight, k_weight, cos, sin, eps):
+    return q.new_empty(q.shape), k.new_empty(k.shape)
+
+
+@torch.library.custom_op("fastdecisions::native_gqa_gated", mutates_args=(), device_types="cuda")
+def native_gqa_gated(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gate: torch.Tensor,
+                     cu_seqlens: Optional[torch.Tensor], max_seqlen: int) -> torch.Tensor:
+    if cu_seqlens is None:
+        return native_gqa_attention(q, k, v, gate=gate)
+    return native_gqa_attention(q, k, v, gate=gate, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen)
+
+
+@native_gqa_gated.register_fake
+def _native_gqa_gated_fake(q, k, v, gate, cu_seqlens, max_seqlen):
+    b, h, t, d = q.shape
+    return q.new_empty((b, t, h, d)).permute(0, 2, 1, 3)
+
+
+def _fusable(self, position_embeddings) -> bool:
+    cos, sin = position_embeddings
+    return (self.head_dim == 128 and self.q_norm.eps == self.k_norm.eps
+            and self.q_norm.weight.dtype == self.k_norm.weight.dtype
+            and self.q_norm.weight.dtype in (torch.bfloat16, torch.float32)
+            and cos.dtype == torch.bfloat16 and sin.dtype == torch.bfloat16 and cos.ndim == 3
+            and cos.shape[-1] in (16, 32, 64, 128))
+
+
+def _fused_forward(self, hidden_states, position_embeddings, cu_seqlens, max_seqlen):
+    """The attention layer with its prologue and output gate in HIP kernels."""
+    shape = hidden_states.shape[:-1]
+    d = self.head_dim
+    qg = self.q_proj(hidden_states).view(*shape, -1, 2 * d)   # per head: query | gate
+    kp = self.k_proj(hidden_states).view(*shape, -1, d)
+    v = self.v_proj(hidden_states).view(*shape, -1, d).transpose(1, 2)
+    cos, sin = position_embeddings
+    q, k = attn_prologue(qg[..., :d], kp, self.q_norm.weight, self.k_norm.weight, cos.contiguous(),
+                         sin.contiguous(), float(self.q_norm.eps))
+    out = native_gqa_gated(q.transpose(1, 2), k.transpose(1, 2), v, qg[..., d:].transpose(1, 2), cu_seqlens,
+                           int(max_seqlen))
+    return self.o_proj(out.transpose(1, 2).reshape(*shape, -1)), None
+
+
 def candidate_forward(self, hidden_states, position_embeddings, attention_mask=None, past_key_values=None,
                       **kwargs):
     """Qwen3_5Attention.forward with the attention itself on the HIP kernel
@@ -58,6 +115,10 @@ def candidate_forward(self, hidden_states, position_embeddings, attention_mask=N
             or self.head_dim not in (64, 128, 256)):
         return self._native_gqa_original_forward(hidden_states, position_embeddings, attention_mask,
                                                  past_key_values=past_key_values, **kwargs)
+    cu_seqlens = kwargs.get("cu_seq_lens_q")
+    if getattr(self, "_fd_attn_fused", False) and _fusable(self, position_embeddings):
+        max_len = kwargs["max_length_q"] if cu_seqlens is not None else hidden_states.shape[1]
+        return _fused_forward(self, hidden_states, position_embeddings, cu_seqlens, max_len)
     from transformers.models.qwen3_5.modeling_qwen3_5 import apply_rotary_pos_emb
     shape = hidden_states.shape[:-1]
     heads_shape = (*shape, -1, self.head_dim)
@@ -67,7 +128,6 @@ def candidate_forward(self, hidden_states, position_embeddings, attention_mask=N
     k = self.k_norm(self.k_proj(hidden_states).view(heads_shape)).transpose(1, 2)
     v = self.v_proj(hidden_states).view(heads_shape).transpose(1, 2)
     q, k = apply_rotary_pos_emb(q, k, *position_embeddings)
-    cu_seqlens = kwargs.get("cu_seq_lens_q")
     if cu_seqlens is not None:
         out = native_gqa_varlen(q, k, v, cu_seqlens, int(kwargs["max_length_q"]))
     else:
@@ -85,5 +145,18 @@ def install_native_gqa(core) -> int:
             if not hasattr(module, "_native_gqa_original_forward"):
                 module._native_gqa_original_forward = module.forward
                 module.forward = MethodType(candidate_forward, module)
+            count += 1
+    return count
+
+
+def install_attention_fusions(core) -> int:
+    """Run every attention layer's prologue and output gate in HIP kernels; return the count.
+    Installs ``candidate_forward`` where it is not there yet."""
+    install_native_gqa(core)
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5Attention
+    count = 0
+    for module in core.modules():
+        if isinstance(module, Qwen3_5Attention):
+            module._fd_attn_fused = True
             count += 1
     return count

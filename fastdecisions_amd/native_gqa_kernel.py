@@ -9,8 +9,11 @@ current stream without synchronisation.
 
 Differences, all widenings: head_dim 64/128/256 (the reference accepts only
 256, ref: :132-133), an optional ``scale`` (default ``D**-0.5`` as ref: :168),
-and packed variable-length batches through ``cu_seqlens``/``max_seqlen``
-(B == 1, T = total tokens), with causal masking inside each request.
+packed variable-length batches through ``cu_seqlens``/``max_seqlen``
+(B == 1, T = total tokens), with causal masking inside each request, and an
+optional output ``gate`` (logical ``[B, Hq, T, D]`` like the output): the
+attention layer's ``output * sigmoid(gate)`` applied in the kernel's store
+(``fd_gqa_gated_fwd``; ref: experiments/native_gqa/bench_native_gqa_model.py:54-55).
 """
 from __future__ import annotations
 
@@ -29,6 +32,7 @@ def native_gqa_attention(
     scale: float | None = None,
     cu_seqlens: torch.Tensor | None = None,
     max_seqlen: int | None = None,
+    gate: torch.Tensor | None = None,
 ) -> torch.Tensor:
     # Logical shapes: Q [B, Hq, T, D], K/V [B, Hkv, T, D] (ref: :120).
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
@@ -56,6 +60,12 @@ def native_gqa_attention(
         if tensor.data_ptr() % 16 or any(s % 8 for s in tensor.stride()[:3]):
             raise ValueError("Q, K and V rows must be 16-byte aligned")
 
+    if gate is not None:
+        if gate.shape != q.shape or gate.dtype != torch.bfloat16 or gate.device != q.device:
+            raise ValueError("gate must be a BF16 tensor shaped like Q on Q's device")
+        if gate.stride(-1) != 1 or gate.data_ptr() % 16 or any(s % 8 for s in gate.stride()[:3]):
+            raise ValueError("gate rows must be contiguous and 16-byte aligned")
+
     n_seqs = 0
     cu_ptr = None
     if cu_seqlens is not None:
@@ -82,9 +92,16 @@ def native_gqa_attention(
             (batch, seq_len, q_heads, head_dim), device=q.device, dtype=q.dtype
         ).permute(0, 2, 1, 3)
         lib = _lib.lib()
-        _lib.check("fd_gqa_fwd", lib.fd_gqa_fwd(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), output.data_ptr(),
-            _lib.strides4(q), _lib.strides4(k), _lib.strides4(v), _lib.strides4(output),
-            batch, q_heads, kv_heads, seq_len, head_dim, float(scale),
-            cu_ptr, n_seqs, int(max_seqlen), _lib.stream_handle(q.device)))
+        if gate is None:
+            _lib.check("fd_gqa_fwd", lib.fd_gqa_fwd(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), output.data_ptr(),
+                _lib.strides4(q), _lib.strides4(k), _lib.strides4(v), _lib.strides4(output),
+                batch, q_heads, kv_heads, seq_len, head_dim, float(scale),
+                cu_ptr, n_seqs, int(max_seqlen), _lib.stream_handle(q.device)))
+        else:
+            _lib.check("fd_gqa_gated_fwd", lib.fd_gqa_gated_fwd(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), gate.data_ptr(), output.data_ptr(),
+                _lib.strides4(q), _lib.strides4(k), _lib.strides4(v), _lib.strides4(gate), _lib.strides4(output),
+                batch, q_heads, kv_heads, seq_len, head_dim, float(scale),
+                cu_ptr, n_seqs, int(max_seqlen), _lib.stream_handle(q.device)))
     return output

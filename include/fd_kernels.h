@@ -17,6 +17,10 @@
  *   fd_gated_delta_fwd  chunked gated delta rule of the Gated-DeltaNet layers
  *                       replaces the torch_chunk_gated_delta_rule call
  *                       (ref: src/decider/packed_conv.py:55-59)
+ *   fd_gqa_gated_fwd    fd_gqa_fwd with the attention layer's sigmoid output gate applied in the store
+ *   fd_attn_prologue_fwd   q/k RMSNorm over head_dim + partial rotary embedding of the attention layers
+ *                       replaces the eager prologue of the patched attention forward
+ *                       (ref: experiments/native_gqa/bench_native_gqa_model.py:47-53)
  *   fd_gate_transform_fwd  gate transform (decay g and beta) of the Gated-DeltaNet layers
  *                       replaces unpack_gate(combined, a_log, dt_bias)
  *                       (ref: src/decider/unpack_gate_transform_kernel.py:94-133, kernel :51-91)
@@ -45,7 +49,7 @@ extern "C" {
 #define FD_API
 #endif
 
-#define FD_ABI_VERSION 3
+#define FD_ABI_VERSION 4
 
 #define FD_OK 0
 #define FD_ERR_INVALID_ARGUMENT (-1) /* shape, size, stride or flag out of range */
@@ -91,6 +95,50 @@ FD_API int fd_gqa_fwd(const void* q, const void* k, const void* v, void* out,
                int batch, int q_heads, int kv_heads, int seq_len, int head_dim,
                float scale, const int32_t* cu_seqlens, int n_seqs, int max_seqlen,
                void* stream);
+
+/*
+ * fd_gqa_fwd followed by the attention layer's output gate, applied before the
+ * store (ref: experiments/native_gqa/bench_native_gqa_model.py:54-55,
+ * `output * torch.sigmoid(gate)`):
+ *   out = bf16(bf16(attn) * bf16(1 / (1 + exp(-gate))))
+ * gate has the logical layout of out, [batch, q_heads, seq_len, head_dim]
+ * (gate_strides = {b, h, t, d}, innermost 1, 16-byte rows).  Other arguments
+ * and limits as fd_gqa_fwd.
+ */
+FD_API int fd_gqa_gated_fwd(const void* q, const void* k, const void* v, const void* gate, void* out,
+                            const int64_t q_strides[4], const int64_t k_strides[4],
+                            const int64_t v_strides[4], const int64_t gate_strides[4],
+                            const int64_t out_strides[4], int batch, int q_heads, int kv_heads,
+                            int seq_len, int head_dim, float scale, const int32_t* cu_seqlens,
+                            int n_seqs, int max_seqlen, void* stream);
+
+/*
+ * Attention prologue: per-head RMSNorm of q and k over head_dim, then the
+ * rotary embedding of the first rotary_dim features, replacing the eager
+ * q_norm / k_norm / apply_rotary_pos_emb of the patched attention forward
+ * (ref: experiments/native_gqa/bench_native_gqa_model.py:47-53; transformers
+ * Qwen3_5RMSNorm and apply_rotary_pos_emb):
+ *   y   = bf16((x * (1 / sqrt(mean(x^2) + eps))) * g),  g = 1 + w (gain_offset) or w
+ *   out = bf16(bf16(y_i * cos_i) + bf16(rot_i * sin_i)) for i < rotary_dim,
+ *         rot = (-y[R/2:R], y[0:R/2]);  out_i = y_i for i >= rotary_dim
+ * fp32 arithmetic, fixed reduction order, correctly rounded sqrt and division.
+ *
+ *   q_in  token t, head h at q_in + t*q_token_stride + h*q_head_stride (bf16, 128 contiguous)
+ *         (e.g. the query half of the q_proj output [tokens, q_heads, 2*head_dim])
+ *   k_in  likewise with k_token_stride, k_head_stride
+ *   q_weight, k_weight  [head_dim] of weight_dtype (FD_DTYPE_BF16 or FD_DTYPE_F32)
+ *   cos, sin  [tokens, rotary_dim] bf16 contiguous (NULL when rotary_dim == 0)
+ *   q_out [tokens, q_heads, head_dim], k_out [tokens, kv_heads, head_dim] bf16 contiguous
+ *
+ * Limits: head_dim == 128; rotary_dim in {0, 16, 32, 64, 128}; 16-byte aligned
+ * pointers and strides that are multiples of 8 elements.
+ */
+FD_API int fd_attn_prologue_fwd(const void* q_in, int64_t q_token_stride, int64_t q_head_stride,
+                                const void* k_in, int64_t k_token_stride, int64_t k_head_stride,
+                                const void* q_weight, const void* k_weight, int weight_dtype,
+                                int gain_offset, float eps, const void* cos, const void* sin,
+                                int rotary_dim, void* q_out, void* k_out, int64_t tokens, int q_heads,
+                                int kv_heads, int head_dim, void* stream);
 
 /*
  * Packed causal depthwise conv1d + activation with a head-split store.

@@ -30,6 +30,9 @@ def _lib() -> ctypes.CDLL:
         lib.fd_oracle_f32_to_bf16.argtypes = [ctypes.c_float]
         lib.fd_oracle_packed_conv.restype = ctypes.c_int
         lib.fd_oracle_packed_conv.argtypes = [p, p, p, p, p, p] + [ctypes.c_int] * 5 + [p, ctypes.c_int, ctypes.c_int]
+        lib.fd_oracle_attn_prologue.restype = ctypes.c_int
+        lib.fd_oracle_attn_prologue.argtypes = [p, ctypes.c_int64, ctypes.c_int, p, ctypes.c_int, ctypes.c_int,
+                                                ctypes.c_float, p, p, ctypes.c_int, p]
         lib.fd_oracle_add_rmsnorm.restype = ctypes.c_int
         lib.fd_oracle_add_rmsnorm.argtypes = [p, p, p, p, p, ctypes.c_int64, ctypes.c_int, ctypes.c_float,
                                               ctypes.c_int, ctypes.c_int]
@@ -230,6 +233,48 @@ def gqa_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, *, scale: float |
 
 
 # ---------------------------------------------------------------- readout
+
+def attn_prologue(x_bits: np.ndarray, weight, cos_bits: np.ndarray | None, sin_bits: np.ndarray | None,
+                  eps: float = 1e-6, gain_offset: bool = True) -> np.ndarray:
+    """Per-head RMSNorm + partial rotary embedding of x [B, T, H, 128] (bf16 bits), bit-exact
+    restatement of the GPU kernel (C oracle); weight [128] (uint16 bf16 bits or float32),
+    cos / sin [B, T, R] bf16 bits or None.  Returns bf16 bits shaped like x."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    B, T, H, D = x.shape
+    if D != 128:
+        raise ValueError("head_dim must be 128")
+    w = np.ascontiguousarray(weight)
+    w_dtype = 1 if w.dtype == np.float32 else 0
+    if w_dtype == 0:
+        w = w.astype(np.uint16)
+    rot = 0 if cos_bits is None else cos_bits.shape[-1]
+    c = None if cos_bits is None else np.ascontiguousarray(cos_bits, dtype=np.uint16)
+    s = None if sin_bits is None else np.ascontiguousarray(sin_bits, dtype=np.uint16)
+    out = np.empty_like(x)
+    rc = _lib().fd_oracle_attn_prologue(_ptr(x), B * T * H, H, _ptr(w), w_dtype, int(gain_offset), eps,
+                                        _ptr(c), _ptr(s), rot, _ptr(out))
+    if rc:
+        raise ValueError("fd_oracle_attn_prologue rejected its arguments")
+    return out
+
+
+def attn_prologue_f64(x_bits: np.ndarray, weight, cos_bits=None, sin_bits=None, eps: float = 1e-6,
+                      gain_offset: bool = True) -> np.ndarray:
+    """The same prologue in float64 without intermediate roundings (closed form)."""
+    x = bf16_to_f32(x_bits).astype(np.float64)
+    w = np.asarray(weight, np.float64) if np.asarray(weight).dtype != np.uint16 else \
+        bf16_to_f32(weight).astype(np.float64)
+    g = 1.0 + w if gain_offset else w
+    y = x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * g
+    if cos_bits is not None:
+        R = cos_bits.shape[-1]
+        c = bf16_to_f32(cos_bits).astype(np.float64)[:, :, None, :]
+        s = bf16_to_f32(sin_bits).astype(np.float64)[:, :, None, :]
+        yr = y[..., :R]
+        rh = np.concatenate([-yr[..., R // 2:], yr[..., :R // 2]], axis=-1)
+        y = np.concatenate([yr * c + rh * s, y[..., R:]], axis=-1)
+    return y
+
 
 def gate_transform(a_bits: np.ndarray, b_bits: np.ndarray, a_log, dt_bias) -> tuple[np.ndarray, np.ndarray]:
     """Gated-DeltaNet gate transform in float64 (ref: src/decider/unpack_gate_transform_kernel.py:69-88;

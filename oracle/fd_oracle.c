@@ -9,6 +9,8 @@
  *     (ref: src/decider/packed_conv_kernel.py:128-191: tap order :139-177,
  *      zero taps before the sequence start :128-176, SiLU :178-182,
  *      q/k/v split :184-191);
+ *   - the attention prologue (per-head RMSNorm of q / k, partial rotary
+ *     embedding; ref: experiments/native_gqa/bench_native_gqa_model.py:47-53);
  *   - the fused residual add + RMSNorm (ref: src/decider/residual_rms_baseline.py:48-85
  *     for eps placement, ref: src/decider/persistent_residual_rms_kernel.py:59-72 for
  *     the (w + 1) gain; the residual is rounded to bf16 before it is normalised as in
@@ -166,6 +168,62 @@ int fd_oracle_add_rmsnorm(const uint16_t* x, const uint16_t* residual, const voi
       if (gain_offset) g = 1.0f + g;
       const float y = (h[i] * inv) * g;
       out[base + i] = fd_oracle_f32_to_bf16(y);
+    }
+  }
+  return 0;
+}
+
+/* Attention prologue on rows of 128 bf16 features (row r belongs to token r / heads):
+ * RMSNorm with the GPU kernel's summation order (16 lanes of 8 features: per-lane
+ * sum in feature order, then an xor butterfly over the 16 lanes), gain (1 + w) or w,
+ * one bf16 rounding; then the rotary embedding of the first `rot` features with
+ * every bf16 product and sum rounded (transformers apply_rotary_pos_emb on bf16;
+ * ref: experiments/native_gqa/bench_native_gqa_model.py:47-53).
+ * weight_dtype 0: bf16, 1: fp32.  cos / sin: [rows / heads][rot] bf16.  Returns 0 or -1. */
+static float r16(float x) { return bf16_to_f32(fd_oracle_f32_to_bf16(x)); }
+
+int fd_oracle_attn_prologue(const uint16_t* x, int64_t rows, int heads, const void* weight, int weight_dtype,
+                            int gain_offset, float eps, const uint16_t* cos, const uint16_t* sin, int rot,
+                            uint16_t* out) {
+  if (rows < 0 || heads < 1 || rot < 0 || rot > 128 || (rot % 16)) return -1;
+  for (int64_t r = 0; r < rows; ++r) {
+    const uint16_t* xr = x + (size_t)r * 128;
+    float v[128], y[128];
+    for (int i = 0; i < 128; ++i) v[i] = bf16_to_f32(xr[i]);
+    float lane[16];
+    for (int l = 0; l < 16; ++l) {
+      float s = 0.0f;
+      for (int e = 0; e < 8; ++e) {
+        const float sq = v[8 * l + e] * v[8 * l + e];
+        s = s + sq;
+      }
+      lane[l] = s;
+    }
+    for (int off = 8; off >= 1; off >>= 1) {
+      float next[16];
+      for (int l = 0; l < 16; ++l) next[l] = lane[l] + lane[l ^ off];
+      memcpy(lane, next, sizeof(next));
+    }
+    const float mean = lane[0] / 128.0f;
+    const float inv = 1.0f / sqrtf(mean + eps);
+    for (int i = 0; i < 128; ++i) {
+      float g = weight_dtype == 1 ? ((const float*)weight)[i] : bf16_to_f32(((const uint16_t*)weight)[i]);
+      if (gain_offset) g = 1.0f + g;
+      const float t = v[i] * inv;
+      y[i] = r16(t * g);
+    }
+    const int64_t tok = r / heads;
+    uint16_t* o = out + (size_t)r * 128;
+    for (int i = 0; i < 128; ++i) {
+      float res = y[i];
+      if (i < rot) {
+        const int h = rot / 2;
+        const float rh = i < h ? -y[i + h] : y[i - h];
+        const float c = bf16_to_f32(cos[(size_t)tok * rot + i]);
+        const float s = bf16_to_f32(sin[(size_t)tok * rot + i]);
+        res = r16(r16(y[i] * c) + r16(rh * s));
+      }
+      o[i] = fd_oracle_f32_to_bf16(res);
     }
   }
   return 0;

@@ -19,6 +19,9 @@ repository's oracle or kernels:
   ref: src/decider/packed_conv.py:55-59), per request for varlen, q/k heads
   expanded by ``repeat_interleave`` as ``Qwen3_5GatedDeltaNet.forward`` does,
   and transformers' ``l2norm`` on bf16 rows;
+* attention prologue: transformers' ``Qwen3_5RMSNorm`` (q_norm / k_norm over
+  head_dim) and ``apply_rotary_pos_emb`` on bf16, with cos / sin from the
+  decider shape's ``Qwen3_5TextRotaryEmbedding`` (partial rotary factor 0.25);
 * gate transform: the eager expressions ``-A_log.float().exp() * F.softplus(a.float()
   + dt_bias)`` and ``b.sigmoid()`` (ref: src/decider/packed_conv.py:49-53) on bf16
   a, b and bf16 / fp32 parameters.
@@ -27,6 +30,7 @@ bf16 arrays are stored as uint16 bit patterns.  Each fixture is small (< 1 MB).
 """
 from __future__ import annotations
 
+import sys
 from pathlib import Path
 
 import numpy as np
@@ -34,6 +38,7 @@ import torch
 import torch.nn.functional as F
 
 HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE.parents[1]))  # the repository root, for the decider shape of the rotary table
 
 
 def bits(t: torch.Tensor) -> np.ndarray:
@@ -237,8 +242,30 @@ def make_gates(g: torch.Generator) -> dict:
     return out
 
 
+def make_prologue(g: torch.Generator) -> dict:
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as mq
+    from fastdecisions_amd.model import DECIDER_2B_SHAPED, make_config
+    cfg = make_config(DECIDER_2B_SHAPED)
+    rope = mq.Qwen3_5TextRotaryEmbedding(cfg)
+    T = 40
+    q = torch.randn((1, T, 4, 128), generator=g).to(torch.bfloat16) * 3
+    k = torch.randn((1, T, 2, 128), generator=g).to(torch.bfloat16)
+    pos = torch.arange(100, 100 + T)[None]
+    cos, sin = rope(q, pos)
+    qn = mq.Qwen3_5RMSNorm(128, eps=1e-6)
+    kn = mq.Qwen3_5RMSNorm(128, eps=1e-6)
+    with torch.no_grad():
+        qn.weight.copy_(torch.randn(128, generator=g) * 0.1)
+        kn.weight.copy_(torch.randn(128, generator=g) * 0.1)
+    qn, kn = qn.to(torch.bfloat16), kn.to(torch.bfloat16)
+    with torch.no_grad():
+        qe, ke = mq.apply_rotary_pos_emb(qn(q).transpose(1, 2), kn(k).transpose(1, 2), cos, sin)
+    return dict(q=bits(q), k=bits(k), q_w=bits(qn.weight.data), k_w=bits(kn.weight.data), cos=bits(cos),
+                sin=bits(sin), q_out=bits(qe.transpose(1, 2)), k_out=bits(ke.transpose(1, 2)))
+
+
 FIXTURES = (("conv", make_conv), ("rmsnorm", make_rms), ("gqa", make_gqa), ("readout", make_readout),
-            ("gated_delta", make_gated_delta), ("gates", make_gates))
+            ("gated_delta", make_gated_delta), ("gates", make_gates), ("prologue", make_prologue))
 
 
 def main(names=None) -> None:

@@ -443,3 +443,52 @@ def test_planted_gate_slips_fail_the_golden(oracle, golden):
                  -np.exp(a_log) * np.log1p(np.exp(np.minimum(oracle.bf16_to_f32(d["a"]), 20.0))),  # bias dropped
                  np.exp(a_log) * sp):                 # sign
         assert _f32_ulps(slip, want).max() > 100
+
+
+# ------------------------------------------------------------------ attention prologue
+
+def test_attn_prologue_matches_eager_golden(oracle, golden):
+    d = golden("prologue")
+    for n in ("q", "k"):
+        got = oracle.attn_prologue(d[n], d[f"{n}_w"], d["cos"], d["sin"])
+        from helpers import ulp_diff
+        ulps = ulp_diff(got, d[f"{n}_out"])
+        assert ulps.max() <= 1 and (ulps > 0).mean() < 1e-3, n
+
+
+def test_attn_prologue_vs_f64_and_special_cases(oracle, golden):
+    d = golden("prologue")
+    got = oracle.bf16_to_f32(oracle.attn_prologue(d["q"], d["q_w"], d["cos"], d["sin"])).astype(np.float64)
+    ref = oracle.attn_prologue_f64(d["q"], d["q_w"], d["cos"], d["sin"])
+    # each bf16 rounding is within 2^-9 of what it rounds: the normalised value y,
+    # the products y*cos and rot*sin, and their sum
+    y = oracle.attn_prologue_f64(d["q"], d["q_w"])
+    R = d["cos"].shape[-1]
+    c = np.abs(oracle.bf16_to_f32(d["cos"]))[:, :, None, :]
+    sn = np.abs(oracle.bf16_to_f32(d["sin"]))[:, :, None, :]
+    scale = np.abs(y).copy()
+    yr = np.abs(y[..., :R])
+    scale[..., :R] = yr * c + np.concatenate([yr[..., R // 2:], yr[..., :R // 2]], axis=-1) * sn + np.abs(ref[..., :R])
+    assert (np.abs(got - ref) <= 2.0 ** -7 * scale + 1e-6).all()
+    # cos = 1, sin = 0 leaves the normalised row unchanged; rotary_dim 0 is the plain RMSNorm
+    one = oracle.f32_to_bf16(np.ones(d["cos"].shape, np.float32))
+    zero = oracle.f32_to_bf16(np.zeros(d["sin"].shape, np.float32))
+    plain = oracle.attn_prologue(d["q"], d["q_w"], None, None)
+    assert np.array_equal(oracle.attn_prologue(d["q"], d["q_w"], one, zero), plain)
+    # the plain RMSNorm agrees with the add+RMSNorm oracle (no residual) to one bf16 ulp
+    from helpers import ulp_diff
+    x = d["q"].reshape(-1, 128)
+    w = d["q_w"]
+    other, _ = oracle.add_rmsnorm(x, None, w)
+    assert ulp_diff(plain.reshape(-1, 128), other).max() <= 1
+
+
+def test_planted_prologue_slips_fail_the_golden(oracle, golden):
+    d = golden("prologue")
+    want = oracle.bf16_to_f32(d["q_out"]).astype(np.float64)
+    q, w, c, s = d["q"], d["q_w"], d["cos"], d["sin"]
+    sin_neg = oracle.f32_to_bf16(-oracle.bf16_to_f32(s))
+    for slip in (oracle.attn_prologue(q, w, c, sin_neg),                       # rotation the wrong way
+                 oracle.attn_prologue(q, w, c, s, gain_offset=False),           # w instead of 1 + w
+                 oracle.attn_prologue(q, w, s, c)):                             # cos and sin swapped
+        assert np.abs(oracle.bf16_to_f32(slip) - want).max() > 0.05
