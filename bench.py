@@ -352,10 +352,23 @@ def bench_forward(args) -> dict:
         e.record()
     torch.cuda.synchronize()
     eager_ms = [s.elapsed_time(e) for s, e in events]
+    # the slot-only forward (final norm + letter projection + softmax at the 4 slots only,
+    # ref: src/decider/slot_projection.py), reported beside the metric, outside the timed region
+    lg_slots, p_slots = hip_engine.slot_probs(ids, rows, req.slots, req.nopts)
+    d_slots = p_slots.argmax(-1).tolist()
+    skey = ("slots", *ids.shape, len(req.slots))
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for s, e in events:
+        s.record()
+        hip_engine.replay(skey)
+        e.record()
+    torch.cuda.synchronize()
+    slot_ms = [s.elapsed_time(e) for s, e in events]
     return dict(
         median_ms=statistics.median(hip_ms), min_ms=min(hip_ms), wall_ms_per_step=total_hip / args.steps,
         eager_median_ms=statistics.median(eager_ms), speedup_vs_eager=statistics.median(eager_ms) / statistics.median(hip_ms),
-        decisions_eager=d_ref, decisions_hip=d_got, decisions_identical=d_ref == d_got,
+        slot_only_median_ms=statistics.median(slot_ms), decisions_slot_only=d_slots,
+        decisions_eager=d_ref, decisions_hip=d_got, decisions_identical=d_ref == d_got == d_slots,
         slot_margins=[round(m, 4) for m in margins(ref, rows, req.slots, req.nopts)],
         max_abs_logit_diff=float((got - ref).abs().max()), patched=counts)
 

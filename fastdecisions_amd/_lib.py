@@ -67,6 +67,12 @@ SIGNATURES = {
         ctypes.c_int64,
         [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int],
     ),
+    "fd_slot_readout_fwd": (
+        ctypes.c_int,
+        [_c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+         _c_void_p, ctypes.c_int, _c_void_p, _c_void_p, _c_void_p, ctypes.c_int, ctypes.c_float, _c_void_p,
+         _c_void_p, _c_void_p],
+    ),
     "fd_gate_transform_fwd": (
         ctypes.c_int,
         [_c_void_p, _c_void_p, ctypes.c_int64, ctypes.c_int64, _c_void_p, ctypes.c_int, _c_void_p, ctypes.c_int,

@@ -58,8 +58,41 @@ class Engine:
         graph.replay()
         return s_out
 
-    def replay(self, key: tuple[int, int]) -> torch.Tensor:
-        """Replay the captured graph of shape ``key`` on its current static input."""
+    @torch.no_grad()
+    def slot_probs(self, ids: torch.Tensor, rows, slots, nopts):
+        """Slot-only forward (the final norm, the letter projection and the masked
+        softmax at the slots, ref: src/decider/slot_projection.py:6-21), replayed from
+        a graph per (B, T, N) with the slot indices in fixed device buffers.
+        Returns (logits [N, K], probabilities [N, K]) on the device (graph outputs)."""
+        dev = ids.device
+        idx = torch.tensor([list(rows), list(slots), list(nopts)], dtype=torch.int32).to(dev)
+        if not self.use_graphs:
+            return self.model.slot_logits(ids, idx[0], idx[1], idx[2])
+        key = ("slots", *ids.shape, idx.shape[1])
+        if key not in self.graphs:
+            s_ids = torch.zeros_like(ids)
+            s_idx = torch.zeros_like(idx)
+            side = torch.cuda.Stream(device=dev)
+            side.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    self.model.slot_logits(s_ids, s_idx[0], s_idx[1], s_idx[2])
+            torch.cuda.current_stream(dev).wait_stream(side)
+            torch.cuda.synchronize(dev)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, pool=self.pool):
+                s_out = self.model.slot_logits(s_ids, s_idx[0], s_idx[1], s_idx[2])
+            self.stats["graph_captures"] += 1
+            self.graphs[key] = ((s_ids, s_idx), s_out, graph)
+        (s_ids, s_idx), s_out, graph = self.graphs[key]
+        s_ids.copy_(ids)
+        s_idx.copy_(idx)
+        graph.replay()
+        return s_out
+
+    def replay(self, key: tuple) -> torch.Tensor:
+        """Replay the captured graph of ``key`` (a ``(B, T)`` shape, or the slot-only
+        forward's ``("slots", B, T, N)``) on its current static input."""
         s_ids, s_out, graph = self.graphs[key]
         graph.replay()
         return s_out

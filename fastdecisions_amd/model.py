@@ -90,8 +90,10 @@ class DeciderModel(nn.Module):
         self.letters = nn.Parameter(torch.empty(shape.n_letters, shape.hidden_size))
 
     def hidden(self, ids: torch.Tensor, *, cu_seqlens: torch.Tensor | None = None,
-               segments: list[tuple[int, int]] | None = None, max_seqlen: int | None = None) -> torch.Tensor:
-        """Final normed hidden states [B, T, H].  For packed requests pass ``cu_seqlens``
+               segments: list[tuple[int, int]] | None = None, max_seqlen: int | None = None,
+               final_norm: bool = True) -> torch.Tensor:
+        """Final normed hidden states [B, T, H] (the residual stream before the final
+        norm with ``final_norm=False``).  For packed requests pass ``cu_seqlens``
         (device int32), ``segments`` (host (start, end) pairs) and ``max_seqlen``."""
         core = self.core
         h = core.embed_tokens(ids)
@@ -109,10 +111,20 @@ class DeciderModel(nn.Module):
         for layer in core.layers[: self.config.num_hidden_layers]:
             h = layer(h, position_embeddings=pe, attention_mask=None, position_ids=pos, past_key_values=None,
                       **kwargs)
-        return core.norm(h)
+        return core.norm(h) if final_norm else h
 
     def forward(self, ids: torch.Tensor, **kw) -> torch.Tensor:
         return F.linear(self.hidden(ids, **kw), self.letters).float()
+
+    def slot_logits(self, ids: torch.Tensor, slot_rows: torch.Tensor, slot_positions: torch.Tensor,
+                    nopts: torch.Tensor | None = None, temperature: float = 1.0, **kw):
+        """Letter logits [N, K] (fp32) and masked probabilities at the slots only: the
+        layers run on every token, the final norm and the projection only at the
+        slots (fd_slot_readout_fwd; ref: src/decider/slot_projection.py:6-21)."""
+        from .slot_projection import slot_readout
+        h = self.hidden(ids, final_norm=False, **kw)
+        return slot_readout(h.contiguous(), self.core.norm.weight, self.letters, slot_rows, slot_positions, nopts,
+                            eps=self.core.norm.eps, temperature=temperature)
 
 
 def _init_value(name: str, shape, gen: torch.Generator, device) -> torch.Tensor:

@@ -21,6 +21,9 @@
  *   fd_attn_prologue_fwd   q/k RMSNorm over head_dim + partial rotary embedding of the attention layers
  *                       replaces the eager prologue of the patched attention forward
  *                       (ref: experiments/native_gqa/bench_native_gqa_model.py:47-53)
+ *   fd_slot_readout_fwd final RMSNorm + option-letter projection + masked softmax at the slots only
+ *                       replaces SlotProjectionForward and read_slots
+ *                       (ref: src/decider/slot_projection.py:6-21, src/decider/engine.py:48-56)
  *   fd_gate_transform_fwd  gate transform (decay g and beta) of the Gated-DeltaNet layers
  *                       replaces unpack_gate(combined, a_log, dt_bias)
  *                       (ref: src/decider/unpack_gate_transform_kernel.py:94-133, kernel :51-91)
@@ -49,7 +52,7 @@ extern "C" {
 #define FD_API
 #endif
 
-#define FD_ABI_VERSION 4
+#define FD_ABI_VERSION 5
 
 #define FD_OK 0
 #define FD_ERR_INVALID_ARGUMENT (-1) /* shape, size, stride or flag out of range */
@@ -246,6 +249,29 @@ FD_API int fd_gate_transform_fwd(const void* a, const void* b, int64_t a_row_str
                                  int64_t b_row_stride, const void* a_log, int a_log_dtype,
                                  const void* dt_bias, int dt_bias_dtype, float* g, void* beta,
                                  int64_t rows, int heads, void* stream);
+
+/*
+ * Slot-only readout: for each slot n (hidden row slot_rows[n], position
+ * slot_positions[n]) the model's final RMSNorm, the option-letter projection
+ * and the masked softmax at temperature (ref: src/decider/slot_projection.py:6-21,
+ * src/decider/engine.py:48-56, src/decider/temperature.py:136-144):
+ *   y         = bf16((x * (1 / sqrt(mean(x^2) + eps))) * g),  g = 1 + w (gain_offset) or w
+ *   logits[n] = bf16(y . letters[k]) for every letter k           (F.linear on bf16)
+ *   probs[n]  = softmax(logits[n, :nopts[n]] / temperature), 0 for k >= nopts[n]
+ * fp32 arithmetic; slots outside [0, batch) x [0, seq_len) read row 0, position 0.
+ *
+ *   hidden   [batch, seq_len, width] bf16 contiguous (the residual stream before the final norm)
+ *   norm_weight [width] of weight_dtype;  letters [n_letters, width] bf16 contiguous
+ *   slot_rows, slot_positions [n_slots] int32 (device);  nopts [n_slots] int32 or NULL (all letters)
+ *   logits   [n_slots, n_letters] fp32;  probs [n_slots, n_letters] fp32 or NULL
+ *
+ * Limits: width a multiple of 8 in [8, 8192]; n_letters in [1, 1024].
+ */
+FD_API int fd_slot_readout_fwd(const void* hidden, int batch, int seq_len, int width,
+                               const void* norm_weight, int weight_dtype, int gain_offset, float eps,
+                               const void* letters, int n_letters, const int32_t* slot_rows,
+                               const int32_t* slot_positions, const int32_t* nopts, int n_slots,
+                               float temperature, float* logits, float* probs, void* stream);
 
 #ifdef __cplusplus
 }

@@ -276,6 +276,26 @@ def attn_prologue_f64(x_bits: np.ndarray, weight, cos_bits=None, sin_bits=None, 
     return y
 
 
+def slot_readout(hidden_bits: np.ndarray, norm_weight, letters_bits: np.ndarray, rows, positions, nopts=None,
+                 eps: float = 1e-6, temperature: float = 1.0, gain_offset: bool = True):
+    """Slot-only readout in float64 (ref: src/decider/slot_projection.py:6-21 with the model's final
+    Qwen3_5RMSNorm, then src/decider/engine.py:48-56): y = bf16(x / sqrt(mean(x^2) + eps) * (1 + w)) at
+    each slot, logits = bf16(y . letters), probs = softmax(logits[:nopts] / temperature).
+    hidden [B, T, H] and letters [K, H] bf16 bits; norm_weight float [H].  Returns (logits, probs)."""
+    x = bf16_to_f32(hidden_bits[np.asarray(rows), np.asarray(positions)]).astype(np.float64)   # [N, H]
+    w = np.asarray(norm_weight, np.float64)
+    g = 1.0 + w if gain_offset else w
+    y = x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * g
+    y = bf16_to_f32(_f64_to_bf16(y)).astype(np.float64)
+    lg = y @ bf16_to_f32(letters_bits).astype(np.float64).T
+    lg = bf16_to_f32(_f64_to_bf16(lg)).astype(np.float64)
+    K = lg.shape[1]
+    n = np.full(lg.shape[0], K) if nopts is None else np.asarray(nopts)
+    z = np.where(np.arange(K)[None, :] < n[:, None], lg / temperature, -np.inf)
+    p = np.exp(z - z.max(axis=1, keepdims=True))
+    return lg, p / p.sum(axis=1, keepdims=True)
+
+
 def gate_transform(a_bits: np.ndarray, b_bits: np.ndarray, a_log, dt_bias) -> tuple[np.ndarray, np.ndarray]:
     """Gated-DeltaNet gate transform in float64 (ref: src/decider/unpack_gate_transform_kernel.py:69-88;
     eager form ref: src/decider/packed_conv.py:49-53): g = -exp(a_log) * softplus(a + dt_bias) with

@@ -22,6 +22,9 @@ repository's oracle or kernels:
 * attention prologue: transformers' ``Qwen3_5RMSNorm`` (q_norm / k_norm over
   head_dim) and ``apply_rotary_pos_emb`` on bf16, with cos / sin from the
   decider shape's ``Qwen3_5TextRotaryEmbedding`` (partial rotary factor 0.25);
+* slot readout: the model's final ``Qwen3_5RMSNorm`` on bf16 hidden states, the
+  gather at the slots, ``F.linear`` with the bf16 letter rows, ``.float()`` and
+  the masked softmax of the reference readout (ref: src/decider/engine.py:48-56);
 * gate transform: the eager expressions ``-A_log.float().exp() * F.softplus(a.float()
   + dt_bias)`` and ``b.sigmoid()`` (ref: src/decider/packed_conv.py:49-53) on bf16
   a, b and bf16 / fp32 parameters.
@@ -264,8 +267,30 @@ def make_prologue(g: torch.Generator) -> dict:
                 sin=bits(sin), q_out=bits(qe.transpose(1, 2)), k_out=bits(ke.transpose(1, 2)))
 
 
+def make_readout_slots(g: torch.Generator) -> dict:
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as mq
+    H, K = 2048, 10
+    hidden = (torch.randn((2, 50, H), generator=g) * 2).to(torch.bfloat16)
+    norm = mq.Qwen3_5RMSNorm(H, eps=1e-6)
+    with torch.no_grad():
+        norm.weight.copy_(torch.randn(H, generator=g) * 0.02)
+    norm = norm.to(torch.bfloat16)
+    letters = (torch.randn((K, H), generator=g) * 0.02).to(torch.bfloat16)
+    rows = torch.tensor([0, 0, 1, 1, 1, 0])
+    pos = torch.tensor([49, 3, 0, 25, 49, 17])
+    nopts = torch.tensor([4, 10, 2, 7, 10, 3])
+    with torch.no_grad():
+        lg = F.linear(norm(hidden)[rows, pos], letters).float()
+    masked = lg.masked_fill(torch.arange(K)[None, :] >= nopts[:, None], float("-inf"))
+    return dict(hidden=bits(hidden), norm_w=norm.weight.data.float().numpy(), letters=bits(letters),
+                rows=rows.numpy().astype(np.int32), pos=pos.numpy().astype(np.int32),
+                nopts=nopts.numpy().astype(np.int32), logits=lg.numpy(), probs=torch.softmax(masked, -1).numpy(),
+                probs_t2=torch.softmax(masked / 2.0, -1).numpy())
+
+
 FIXTURES = (("conv", make_conv), ("rmsnorm", make_rms), ("gqa", make_gqa), ("readout", make_readout),
-            ("gated_delta", make_gated_delta), ("gates", make_gates), ("prologue", make_prologue))
+            ("gated_delta", make_gated_delta), ("gates", make_gates), ("prologue", make_prologue),
+            ("readout_slots", make_readout_slots))
 
 
 def main(names=None) -> None:

@@ -492,3 +492,33 @@ def test_planted_prologue_slips_fail_the_golden(oracle, golden):
                  oracle.attn_prologue(q, w, c, s, gain_offset=False),           # w instead of 1 + w
                  oracle.attn_prologue(q, w, s, c)):                             # cos and sin swapped
         assert np.abs(oracle.bf16_to_f32(slip) - want).max() > 0.05
+
+
+# ------------------------------------------------------------------ slot readout
+
+def test_slot_readout_matches_eager_golden(oracle, golden):
+    d = golden("readout_slots")
+    lg, p = oracle.slot_readout(d["hidden"], d["norm_w"], d["letters"], d["rows"], d["pos"], d["nopts"])
+    # bf16 logits: the fp64 restatement and the eager fp32 path round to the same or a neighbouring bf16
+    assert np.abs(lg - d["logits"]).max() <= 2.0 ** -8 * np.abs(d["logits"]).max()
+    assert np.abs(p - d["probs"]).max() < 1e-2
+    assert np.array_equal(p.argmax(1), d["probs"].argmax(1))
+    _, p2 = oracle.slot_readout(d["hidden"], d["norm_w"], d["letters"], d["rows"], d["pos"], d["nopts"],
+                                temperature=2.0)
+    assert np.abs(p2 - d["probs_t2"]).max() < 1e-2
+    assert all((p[i, n:] == 0).all() for i, n in enumerate(d["nopts"]))
+
+
+def test_slot_readout_closed_forms_and_slips(oracle, golden):
+    d = golden("readout_slots")
+    lg, p = oracle.slot_readout(d["hidden"], d["norm_w"], d["letters"], d["rows"], d["pos"], d["nopts"])
+    # one allowed letter: probability 1; softmax rows sum to 1
+    _, p1 = oracle.slot_readout(d["hidden"], d["norm_w"], d["letters"], d["rows"], d["pos"], np.ones(6, np.int32))
+    assert np.allclose(p1[:, 0], 1.0) and np.allclose(p.sum(1), 1.0)
+    # slips: the norm's gain without the +1, the wrong slot, a transposed gather
+    assert np.abs(oracle.slot_readout(d["hidden"], d["norm_w"], d["letters"], d["rows"], d["pos"], d["nopts"],
+                                      gain_offset=False)[0] - d["logits"]).max() > 0.05
+    assert np.abs(oracle.slot_readout(d["hidden"], d["norm_w"], d["letters"], d["rows"], d["pos"] - 1,
+                                      d["nopts"])[0] - d["logits"]).max() > 0.05
+    assert np.abs(oracle.slot_readout(d["hidden"], d["norm_w"], d["letters"], 1 - d["rows"], d["pos"],
+                                      d["nopts"])[0] - d["logits"]).max() > 0.05
