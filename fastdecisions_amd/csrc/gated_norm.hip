@@ -1,0 +1,149 @@
+// Gated RMSNorm of the Gated-DeltaNet layers and the MLP's SiLU gate, for gfx950.
+//
+// fd_gated_rmsnorm_fwd replaces transformers' Qwen3_5RMSNormGated applied to the
+// delta rule's output (the call after ref: src/decider/packed_conv.py:55-59:
+// ``self.norm(core_attn_out, z)``), evaluated exactly as the eager ops round:
+//   y  = bf16(x * (1 / sqrt(mean(x^2) + eps)))      (x.to(input dtype))
+//   y2 = bf16(w * y)                                (bf16 weight times bf16 row)
+//   out = bf16(y2 * silu(z)),  silu(z) = z / (1 + exp(-z)) in fp32 on the bf16 gate
+// (with an fp32 weight the product w * y stays fp32, as the eager promotion does).
+// A 16-lane group owns one row of 128 (8 features per lane, 16-byte accesses);
+// rows of 64 or 256 use 8 or 32 lanes.
+//
+// fd_silu_mul_fwd replaces the MLP's ``act_fn(gate_proj(x)) * up_proj(x)``
+// (transformers Qwen3_5MLP) on a combined [rows, 2*width] gate|up projection:
+//   out = bf16(bf16(silu(gate)) * up)
+// HBM-bound, 16-byte loads and stores, one thread per 8 features.
+#include "fd_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float bf16r(float x) { return fd_bf16_to_f32(fd_f32_to_bf16(x)); }
+
+__device__ __forceinline__ void unpack8(uint4 raw, float* x) {
+  const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = fd_lo(wd[i]);
+    x[2 * i + 1] = fd_hi(wd[i]);
+  }
+}
+
+__device__ __forceinline__ uint4 pack8(const float* x) {
+  uint4 r;
+  r.x = fd_f32_to_bf16(x[0]) | (fd_f32_to_bf16(x[1]) << 16);
+  r.y = fd_f32_to_bf16(x[2]) | (fd_f32_to_bf16(x[3]) << 16);
+  r.z = fd_f32_to_bf16(x[4]) | (fd_f32_to_bf16(x[5]) << 16);
+  r.w = fd_f32_to_bf16(x[6]) | (fd_f32_to_bf16(x[7]) << 16);
+  return r;
+}
+
+// LANES lanes per row (LANES * 8 == width)
+template <int LANES, bool W_F32>
+__global__ __launch_bounds__(kThreads) void gated_rmsnorm_kernel(const uint16_t* __restrict__ x,
+                                                                 const uint16_t* __restrict__ z, int64_t z_stride,
+                                                                 const void* __restrict__ w,
+                                                                 uint16_t* __restrict__ out, int64_t rows,
+                                                                 float eps) {
+  constexpr int kWidth = LANES * 8;
+  const int64_t row = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) / LANES;
+  const int ln = threadIdx.x % LANES;
+  const bool valid = row < rows;  // uniform over the lanes of a row
+  const int64_t r = valid ? row : 0;
+  float xv[8], zv[8];
+  unpack8(*reinterpret_cast<const uint4*>(x + r * kWidth + ln * 8), xv);
+  unpack8(*reinterpret_cast<const uint4*>(z + r * z_stride + ln * 8), zv);
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s = s + xv[e] * xv[e];
+#pragma unroll
+  for (int off = LANES / 2; off >= 1; off >>= 1) s = s + __shfl_xor(s, off);
+  const float inv = 1.0f / __builtin_sqrtf(s / static_cast<float>(kWidth) + eps);
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float yn = bf16r(xv[e] * inv);
+    float g;
+    if constexpr (W_F32) {
+      g = static_cast<const float*>(w)[ln * 8 + e] * yn;
+    } else {
+      g = bf16r(fd_bf16_to_f32(static_cast<const uint16_t*>(w)[ln * 8 + e]) * yn);
+    }
+    const float act = zv[e] / (1.0f + expf(-zv[e]));
+    y[e] = g * act;
+  }
+  if (valid) *reinterpret_cast<uint4*>(out + r * kWidth + ln * 8) = pack8(y);
+}
+
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __restrict__ gu, int64_t gu_stride,
+                                                            uint16_t* __restrict__ out, int64_t rows, int width) {
+  const int chunks = width / 8;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= rows * chunks) return;
+  const int64_t r = i / chunks;
+  const int c = static_cast<int>(i - r * chunks);
+  float g[8], u[8], y[8];
+  unpack8(*reinterpret_cast<const uint4*>(gu + r * gu_stride + c * 8), g);
+  unpack8(*reinterpret_cast<const uint4*>(gu + r * gu_stride + width + c * 8), u);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = bf16r(g[e] / (1.0f + expf(-g[e]))) * u[e];
+  *reinterpret_cast<uint4*>(out + r * width + c * 8) = pack8(y);
+}
+
+}  // namespace
+
+extern "C" FD_API int fd_gated_rmsnorm_fwd(const void* x, const void* gate, int64_t gate_row_stride,
+                                           const void* weight, int weight_dtype, void* out, int64_t rows, int width,
+                                           float eps, void* stream) {
+  FD_REQUIRE(x && gate && weight && out, FD_ERR_INVALID_ARGUMENT, "fd_gated_rmsnorm_fwd: pointers must be non-null");
+  FD_REQUIRE(width == 64 || width == 128 || width == 256, FD_ERR_UNSUPPORTED,
+             "fd_gated_rmsnorm_fwd: width must be 64, 128 or 256 (got %d)", width);
+  FD_REQUIRE(rows >= 0 && gate_row_stride >= width && gate_row_stride % 8 == 0, FD_ERR_INVALID_ARGUMENT,
+             "fd_gated_rmsnorm_fwd: rows >= 0 and gate_row_stride a multiple of 8 >= width");
+  FD_REQUIRE(weight_dtype == FD_DTYPE_BF16 || weight_dtype == FD_DTYPE_F32, FD_ERR_INVALID_ARGUMENT,
+             "fd_gated_rmsnorm_fwd: weight_dtype must be FD_DTYPE_BF16 or FD_DTYPE_F32");
+  FD_REQUIRE(eps >= 0.0f, FD_ERR_INVALID_ARGUMENT, "fd_gated_rmsnorm_fwd: eps must be >= 0");
+  FD_REQUIRE(fd_aligned16(x) && fd_aligned16(gate) && fd_aligned16(out), FD_ERR_ALIGNMENT,
+             "fd_gated_rmsnorm_fwd: x, gate and out must be 16-byte aligned");
+  if (rows == 0) return FD_OK;
+  const int lanes = width / 8;
+  const int64_t blocks = (rows * lanes + kThreads - 1) / kThreads;
+  FD_REQUIRE(blocks < (1LL << 31), FD_ERR_INVALID_ARGUMENT, "fd_gated_rmsnorm_fwd: problem too large");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* zp = static_cast<const uint16_t*>(gate);
+  uint16_t* op = static_cast<uint16_t*>(out);
+  const dim3 grid(static_cast<unsigned>(blocks));
+#define FD_GN(L)                                                                                              \
+  do {                                                                                                        \
+    if (weight_dtype == FD_DTYPE_F32)                                                                         \
+      hipLaunchKernelGGL((gated_rmsnorm_kernel<L, true>), grid, dim3(kThreads), 0, s, xp, zp, gate_row_stride, \
+                         weight, op, rows, eps);                                                              \
+    else                                                                                                      \
+      hipLaunchKernelGGL((gated_rmsnorm_kernel<L, false>), grid, dim3(kThreads), 0, s, xp, zp,                \
+                         gate_row_stride, weight, op, rows, eps);                                             \
+  } while (0)
+  if (lanes == 8) FD_GN(8); else if (lanes == 16) FD_GN(16); else FD_GN(32);
+#undef FD_GN
+  return fd_check_launch("fd_gated_rmsnorm_fwd");
+}
+
+extern "C" FD_API int fd_silu_mul_fwd(const void* gate_up, int64_t row_stride, void* out, int64_t rows, int width,
+                                      void* stream) {
+  FD_REQUIRE(gate_up && out, FD_ERR_INVALID_ARGUMENT, "fd_silu_mul_fwd: pointers must be non-null");
+  FD_REQUIRE(rows >= 0 && width > 0 && width % 8 == 0 && row_stride >= 2LL * width && row_stride % 8 == 0,
+             FD_ERR_INVALID_ARGUMENT,
+             "fd_silu_mul_fwd: width a positive multiple of 8 and row_stride a multiple of 8 >= 2*width");
+  FD_REQUIRE(fd_aligned16(gate_up) && fd_aligned16(out), FD_ERR_ALIGNMENT,
+             "fd_silu_mul_fwd: gate_up and out must be 16-byte aligned");
+  const int64_t n = rows * (width / 8);
+  if (n == 0) return FD_OK;
+  const int64_t blocks = (n + kThreads - 1) / kThreads;
+  FD_REQUIRE(blocks < (1LL << 31), FD_ERR_INVALID_ARGUMENT, "fd_silu_mul_fwd: problem too large");
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gate_up), row_stride,
+                     static_cast<uint16_t*>(out), rows, width);
+  return fd_check_launch("fd_silu_mul_fwd");
+}

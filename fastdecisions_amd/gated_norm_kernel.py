@@ -1,0 +1,54 @@
+"""Gated RMSNorm and the MLP's SiLU gate on the gfx950 HIP kernels
+``fd_gated_rmsnorm_fwd`` / ``fd_silu_mul_fwd``.
+
+* ``gated_rms_norm(x, gate, weight, eps)`` — transformers' ``Qwen3_5RMSNormGated``
+  (the norm after the delta rule, ref: src/decider/packed_conv.py:60-61) with the
+  eager rounding; x / gate ``[..., D]`` bf16, D in {64, 128, 256};
+* ``silu_mul(gate_up)`` — ``silu(gate) * up`` of transformers' ``Qwen3_5MLP`` on one
+  combined ``[..., 2I]`` gate|up projection output, returning ``[..., I]``.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_W_DTYPES = {torch.bfloat16: _lib.FD_DTYPE_BF16, torch.float32: _lib.FD_DTYPE_F32}
+
+
+def gated_rms_norm(x: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    if not x.is_cuda or x.dtype != torch.bfloat16 or gate.dtype != torch.bfloat16 or gate.device != x.device:
+        raise ValueError("x and gate must be CUDA BF16 on one device")
+    D = x.shape[-1]
+    if gate.shape != x.shape or D not in (64, 128, 256):
+        raise ValueError("x and gate must share a shape [..., D] with D in {64, 128, 256}")
+    if not x.is_contiguous():
+        raise ValueError("x must be contiguous")
+    g2 = gate.reshape(-1, D)
+    if g2.stride(1) != 1 or g2.data_ptr() % 16 or g2.stride(0) % 8:
+        raise ValueError("gate rows must be contiguous and 16-byte aligned")
+    if weight.shape != (D,) or weight.dtype not in _W_DTYPES or weight.device != x.device or not weight.is_contiguous():
+        raise ValueError(f"weight must be a contiguous BF16 or FP32 vector [{D}] on x's device")
+    if x.data_ptr() % 16:
+        raise ValueError("x must be 16-byte aligned")
+    rows = x.numel() // D
+    with torch.cuda.device(x.device):
+        out = torch.empty_like(x)
+        _lib.check("fd_gated_rmsnorm_fwd", _lib.lib().fd_gated_rmsnorm_fwd(
+            x.data_ptr(), g2.data_ptr(), g2.stride(0), weight.data_ptr(), _W_DTYPES[weight.dtype], out.data_ptr(),
+            rows, D, float(eps), _lib.stream_handle(x.device)))
+    return out
+
+
+def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
+    if not gate_up.is_cuda or gate_up.dtype != torch.bfloat16 or gate_up.shape[-1] % 16:
+        raise ValueError("gate_up must be CUDA BF16 [..., 2I] with I a multiple of 8")
+    if not gate_up.is_contiguous() or gate_up.data_ptr() % 16:
+        raise ValueError("gate_up must be contiguous and 16-byte aligned")
+    width = gate_up.shape[-1] // 2
+    rows = gate_up.numel() // gate_up.shape[-1]
+    with torch.cuda.device(gate_up.device):
+        out = torch.empty((*gate_up.shape[:-1], width), device=gate_up.device, dtype=torch.bfloat16)
+        _lib.check("fd_silu_mul_fwd", _lib.lib().fd_silu_mul_fwd(
+            gate_up.data_ptr(), gate_up.shape[-1], out.data_ptr(), rows, width, _lib.stream_handle(gate_up.device)))
+    return out

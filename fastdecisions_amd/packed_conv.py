@@ -110,7 +110,12 @@ def _forward(self, hidden_states, cache_params=None, attention_mask=None, **kwar
                     initial_state=None, output_final_state=False, use_qk_l2norm_in_kernel=True)
                 parts.append(out)
         core_attn_out = torch.cat(parts, dim=1)
-    core_attn_out = self.norm(core_attn_out.reshape(-1, self.head_v_dim), z.reshape(-1, self.head_v_dim))
+    if getattr(self, "_fd_gated_norm", False):
+        from .layer_fusions import gated_rms_norm_op
+        core_attn_out = gated_rms_norm_op(core_attn_out.reshape(-1, self.head_v_dim), z.reshape(-1, self.head_v_dim),
+                                          self.norm.weight, float(self.norm.variance_epsilon))
+    else:
+        core_attn_out = self.norm(core_attn_out.reshape(-1, self.head_v_dim), z.reshape(-1, self.head_v_dim))
     return self.out_proj(core_attn_out.reshape(batch, seq, -1))
 
 

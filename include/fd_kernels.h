@@ -24,6 +24,8 @@
  *   fd_slot_readout_fwd final RMSNorm + option-letter projection + masked softmax at the slots only
  *                       replaces SlotProjectionForward and read_slots
  *                       (ref: src/decider/slot_projection.py:6-21, src/decider/engine.py:48-56)
+ *   fd_gated_rmsnorm_fwd   gated RMSNorm of the delta rule's output (transformers Qwen3_5RMSNormGated)
+ *   fd_silu_mul_fwd     the MLP's silu(gate) * up on a combined gate|up projection
  *   fd_gate_transform_fwd  gate transform (decay g and beta) of the Gated-DeltaNet layers
  *                       replaces unpack_gate(combined, a_log, dt_bias)
  *                       (ref: src/decider/unpack_gate_transform_kernel.py:94-133, kernel :51-91)
@@ -52,7 +54,7 @@ extern "C" {
 #define FD_API
 #endif
 
-#define FD_ABI_VERSION 5
+#define FD_ABI_VERSION 6
 
 #define FD_OK 0
 #define FD_ERR_INVALID_ARGUMENT (-1) /* shape, size, stride or flag out of range */
@@ -272,6 +274,28 @@ FD_API int fd_slot_readout_fwd(const void* hidden, int batch, int seq_len, int w
                                const void* letters, int n_letters, const int32_t* slot_rows,
                                const int32_t* slot_positions, const int32_t* nopts, int n_slots,
                                float temperature, float* logits, float* probs, void* stream);
+
+/*
+ * Gated RMSNorm of the Gated-DeltaNet output (transformers Qwen3_5RMSNormGated,
+ * called after the delta rule, ref: src/decider/packed_conv.py:60-61), eager rounding:
+ *   y = bf16(x / sqrt(mean(x^2) + eps));  y2 = bf16(w * y) (fp32 for an fp32 weight);
+ *   out = bf16(y2 * z / (1 + exp(-z)))
+ * x, out [rows, width] bf16 contiguous; gate z [rows, width] bf16 with row stride
+ * gate_row_stride (elements); weight [width] of weight_dtype.
+ * Limits: width in {64, 128, 256}; 16-byte aligned pointers.
+ */
+FD_API int fd_gated_rmsnorm_fwd(const void* x, const void* gate, int64_t gate_row_stride,
+                                const void* weight, int weight_dtype, void* out, int64_t rows,
+                                int width, float eps, void* stream);
+
+/*
+ * The MLP's activation (transformers Qwen3_5MLP: act_fn(gate_proj(x)) * up_proj(x)) on a
+ * combined projection gate_up [rows, row_stride] holding gate in columns [0, width)
+ * and up in [width, 2*width):  out = bf16(bf16(silu(gate)) * up), out [rows, width].
+ * Limits: width a multiple of 8; 16-byte aligned pointers and row_stride a multiple of 8.
+ */
+FD_API int fd_silu_mul_fwd(const void* gate_up, int64_t row_stride, void* out, int64_t rows, int width,
+                           void* stream);
 
 #ifdef __cplusplus
 }

@@ -296,6 +296,30 @@ def slot_readout(hidden_bits: np.ndarray, norm_weight, letters_bits: np.ndarray,
     return lg, p / p.sum(axis=1, keepdims=True)
 
 
+def gated_rmsnorm(x_bits: np.ndarray, z_bits: np.ndarray, weight, eps: float = 1e-6) -> np.ndarray:
+    """transformers' Qwen3_5RMSNormGated on bf16 rows in float64 with its bf16 roundings
+    (y = bf16(x / sqrt(mean(x^2) + eps)); y2 = bf16(w * y) for a bf16 weight, w * y for fp32;
+    out = y2 * silu(z)); returns the value before its final bf16 rounding."""
+    x = bf16_to_f32(x_bits).astype(np.float64)
+    z = bf16_to_f32(z_bits).astype(np.float64)
+    y = bf16_to_f32(_f64_to_bf16(x / np.sqrt((x * x).mean(-1, keepdims=True) + eps))).astype(np.float64)
+    w = np.asarray(weight)
+    if w.dtype == np.uint16:
+        y2 = bf16_to_f32(_f64_to_bf16(bf16_to_f32(w).astype(np.float64) * y)).astype(np.float64)
+    else:
+        y2 = w.astype(np.float64) * y
+    return y2 * (z / (1.0 + np.exp(-z)))
+
+
+def silu_mul(gate_up_bits: np.ndarray) -> np.ndarray:
+    """The MLP's silu(gate) * up on a combined [..., 2I] bf16 projection: bf16(silu(g)) * u in
+    float64 (before the final bf16 rounding)."""
+    gu = bf16_to_f32(gate_up_bits).astype(np.float64)
+    I = gu.shape[-1] // 2
+    g, u = gu[..., :I], gu[..., I:]
+    return bf16_to_f32(_f64_to_bf16(g / (1.0 + np.exp(-g)))).astype(np.float64) * u
+
+
 def gate_transform(a_bits: np.ndarray, b_bits: np.ndarray, a_log, dt_bias) -> tuple[np.ndarray, np.ndarray]:
     """Gated-DeltaNet gate transform in float64 (ref: src/decider/unpack_gate_transform_kernel.py:69-88;
     eager form ref: src/decider/packed_conv.py:49-53): g = -exp(a_log) * softplus(a + dt_bias) with

@@ -25,6 +25,8 @@ repository's oracle or kernels:
 * slot readout: the model's final ``Qwen3_5RMSNorm`` on bf16 hidden states, the
   gather at the slots, ``F.linear`` with the bf16 letter rows, ``.float()`` and
   the masked softmax of the reference readout (ref: src/decider/engine.py:48-56);
+* gated norm and MLP gate: transformers' ``Qwen3_5RMSNormGated`` (bf16 weight and
+  fp32 weight) and ``act_fn(gate) * up`` of ``Qwen3_5MLP`` on bf16 tensors;
 * gate transform: the eager expressions ``-A_log.float().exp() * F.softplus(a.float()
   + dt_bias)`` and ``b.sigmoid()`` (ref: src/decider/packed_conv.py:49-53) on bf16
   a, b and bf16 / fp32 parameters.
@@ -288,9 +290,29 @@ def make_readout_slots(g: torch.Generator) -> dict:
                 probs_t2=torch.softmax(masked / 2.0, -1).numpy())
 
 
+def make_fusions(g: torch.Generator) -> dict:
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as mq
+    x = (torch.randn((300, 128), generator=g) * 0.3).to(torch.bfloat16)
+    z = (torch.randn((300, 128), generator=g) * 2).to(torch.bfloat16)
+    w = 1.0 + 0.02 * torch.randn(128, generator=g)
+    out = dict(x=bits(x), z=bits(z), w_f32=w.numpy())
+    for tag, dt in (("bf16", torch.bfloat16), ("f32", torch.float32)):
+        norm = mq.Qwen3_5RMSNormGated(128, eps=1e-6)
+        with torch.no_grad():
+            norm.weight.copy_(w)
+        norm = norm.to(dt)
+        with torch.no_grad():
+            out[f"y_{tag}"] = bits(norm(x, z))
+    out["w_bf16"] = bits(w.to(torch.bfloat16))
+    gu = (torch.randn((64, 2 * 512), generator=g) * 3).to(torch.bfloat16)
+    act = torch.nn.SiLU()
+    out.update(gu=bits(gu), mlp=bits(act(gu[:, :512]) * gu[:, 512:]))
+    return out
+
+
 FIXTURES = (("conv", make_conv), ("rmsnorm", make_rms), ("gqa", make_gqa), ("readout", make_readout),
             ("gated_delta", make_gated_delta), ("gates", make_gates), ("prologue", make_prologue),
-            ("readout_slots", make_readout_slots))
+            ("readout_slots", make_readout_slots), ("fusions", make_fusions))
 
 
 def main(names=None) -> None:

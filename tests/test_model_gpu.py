@@ -37,13 +37,19 @@ def _uninstall(model):
             del m._buffers["_combined_gate_weight"]
         if hasattr(m, "_fd_attn_fused"):
             delattr(m, "_fd_attn_fused")
+        if hasattr(m, "_fd_gated_norm"):
+            delattr(m, "_fd_gated_norm")
+        if hasattr(m, "_fd_mlp_original_forward"):
+            m.forward = m._fd_mlp_original_forward
+            delattr(m, "_fd_mlp_original_forward")
+            del m._buffers["_fd_gate_up_weight"]
 
 
 def test_install_counts_and_fallback(full_model):
     from fastdecisions_amd.model import install_hip_kernels
     counts = install_hip_kernels(full_model)
     try:
-        assert counts == dict(packed_conv=21, native_gqa=7, residual_rms=28, gated_delta=21, combined_gates=21, attention_fusions=7)
+        assert counts == dict(packed_conv=21, native_gqa=7, residual_rms=28, gated_delta=21, combined_gates=21, attention_fusions=7, gated_norm=21, mlp_fusion=28)
         # guarded fallbacks: grad mode goes to the original eager methods
         ids = torch.randint(0, 100, (1, 64), device="cuda")
         with torch.enable_grad():

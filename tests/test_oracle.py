@@ -522,3 +522,32 @@ def test_slot_readout_closed_forms_and_slips(oracle, golden):
                                       d["nopts"])[0] - d["logits"]).max() > 0.05
     assert np.abs(oracle.slot_readout(d["hidden"], d["norm_w"], d["letters"], 1 - d["rows"], d["pos"],
                                       d["nopts"])[0] - d["logits"]).max() > 0.05
+
+
+# ------------------------------------------------------------------ gated norm and MLP gate
+
+def test_gated_rmsnorm_and_silu_mul_match_eager_golden(oracle, golden):
+    from helpers import ulp_diff
+    d = golden("fusions")
+    for tag in ("bf16", "f32"):
+        y = oracle.gated_rmsnorm(d["x"], d["z"], d[f"w_{tag}"])
+        u = ulp_diff(oracle.f32_to_bf16(y.astype(np.float32)), d[f"y_{tag}"])
+        assert u.max() <= 1 and (u > 0).mean() < 1e-2, tag
+    m = oracle.silu_mul(d["gu"])
+    u = ulp_diff(oracle.f32_to_bf16(m.astype(np.float32)), d["mlp"])
+    assert u.max() <= 1 and (u > 0).mean() < 1e-2
+
+
+def test_planted_fusion_slips_fail_the_golden(oracle, golden):
+    d = golden("fusions")
+    want = oracle.bf16_to_f32(d["y_bf16"]).astype(np.float64)
+    x, z = oracle.bf16_to_f32(d["x"]).astype(np.float64), oracle.bf16_to_f32(d["z"]).astype(np.float64)
+    y = x / np.sqrt((x * x).mean(-1, keepdims=True) + 1e-6)
+    w = oracle.bf16_to_f32(d["w_bf16"])
+    for slip in (y * w * z / (1 + np.exp(z)),          # silu sign
+                 y * w * (1.0 / (1 + np.exp(-z))),      # sigmoid instead of silu
+                 (y * (1 + w)) * z / (1 + np.exp(-z))):  # offset gain
+        assert np.abs(slip - want).max() > 0.05
+    gu = oracle.bf16_to_f32(d["gu"]).astype(np.float64)
+    wrong = gu[:, 512:] / (1 + np.exp(-gu[:, 512:])) * gu[:, :512]    # gate and up swapped
+    assert np.abs(wrong - oracle.bf16_to_f32(d["mlp"])).max() > 0.05
