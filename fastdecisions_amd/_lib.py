@@ -75,8 +75,14 @@ SIGNATURES = {
     ),
     "fd_gated_rmsnorm_fwd": (
         ctypes.c_int,
-        [_c_void_p, _c_void_p, ctypes.c_int64, _c_void_p, ctypes.c_int, _c_void_p, ctypes.c_int64, ctypes.c_int,
-         ctypes.c_float, _c_void_p],
+        [_c_void_p, _c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, _c_void_p, ctypes.c_int, _c_void_p,
+         ctypes.c_int64, ctypes.c_int, ctypes.c_float, _c_void_p],
+    ),
+    "fd_packed_conv_strided_fwd": (
+        ctypes.c_int,
+        [_c_void_p, ctypes.c_int64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+         _c_void_p, ctypes.c_int, ctypes.c_int, _c_void_p],
     ),
     "fd_silu_mul_fwd": (
         ctypes.c_int,

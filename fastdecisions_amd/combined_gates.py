@@ -8,12 +8,28 @@ packed Gated-DeltaNet forward computes both gate projections with one GEMM and
 the transform with one kernel (``fastdecisions_amd.packed_conv._forward``).
 Reinvoke after changing the projection weights.  Any head count works (the
 reference requires two bias-free [16, 2048] projections).
+
+``install_combined_projections(core)`` goes further: all four input
+projections of a Gated-DeltaNet layer (q|k|v, z, a, b) become one GEMM whose
+output the packed conv, the gated norm and the gate transform read as strided
+views (``fastdecisions::gate_transform`` takes a and b as separate views).
 """
 from __future__ import annotations
 
 import torch
 
-from .unpack_gate_transform_kernel import unpack_gate
+from .unpack_gate_transform_kernel import gate_transform, unpack_gate
+
+
+@torch.library.custom_op("fastdecisions::gate_transform", mutates_args=(), device_types="cuda")
+def gate_transform_op(a: torch.Tensor, b: torch.Tensor, a_log: torch.Tensor,
+                      dt_bias: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    return gate_transform(a, b, a_log, dt_bias)
+
+
+@gate_transform_op.register_fake
+def _gate_transform_fake(a, b, a_log, dt_bias):
+    return (a.new_empty(a.shape, dtype=torch.float32), a.new_empty(a.shape, dtype=torch.bfloat16))
 
 
 @torch.library.custom_op("fastdecisions::unpack_gate", mutates_args=(), device_types="cuda")
@@ -47,5 +63,30 @@ def install_combined_gates(core) -> int:
                 module._combined_gate_weight = weight
             else:
                 module.register_buffer("_combined_gate_weight", weight, persistent=False)
+            count += 1
+    return count
+
+
+def install_combined_projections(core) -> int:
+    """One GEMM for in_proj_qkv | in_proj_z | in_proj_a | in_proj_b of every
+    Gated-DeltaNet layer (a non-persistent buffer; reinvoke after changing weights)."""
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5GatedDeltaNet
+    from .packed_conv import install_packed_conv
+    install_packed_conv(core)
+    count = 0
+    for module in core.modules():
+        if isinstance(module, Qwen3_5GatedDeltaNet):
+            projs = (module.in_proj_qkv, module.in_proj_z, module.in_proj_a, module.in_proj_b)
+            if any(p.bias is not None for p in projs):
+                continue
+            with torch.no_grad():
+                weight = torch.cat([p.weight for p in projs], dim=0).detach()
+                pad = -weight.shape[0] % 8  # zero rows keep the output's row stride a multiple of 8
+                if pad:
+                    weight = torch.cat([weight, weight.new_zeros((pad, weight.shape[1]))], dim=0)
+            if "_fd_in_proj_weight" in module._buffers:
+                module._fd_in_proj_weight = weight
+            else:
+                module.register_buffer("_fd_in_proj_weight", weight, persistent=False)
             count += 1
     return count

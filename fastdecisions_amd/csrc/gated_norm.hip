@@ -43,7 +43,8 @@ __device__ __forceinline__ uint4 pack8(const float* x) {
 // LANES lanes per row (LANES * 8 == width)
 template <int LANES, bool W_F32>
 __global__ __launch_bounds__(kThreads) void gated_rmsnorm_kernel(const uint16_t* __restrict__ x,
-                                                                 const uint16_t* __restrict__ z, int64_t z_stride,
+                                                                 const uint16_t* __restrict__ z, int64_t z_ts,
+                                                                 int64_t z_hs, int heads,
                                                                  const void* __restrict__ w,
                                                                  uint16_t* __restrict__ out, int64_t rows,
                                                                  float eps) {
@@ -54,7 +55,8 @@ __global__ __launch_bounds__(kThreads) void gated_rmsnorm_kernel(const uint16_t*
   const int64_t r = valid ? row : 0;
   float xv[8], zv[8];
   unpack8(*reinterpret_cast<const uint4*>(x + r * kWidth + ln * 8), xv);
-  unpack8(*reinterpret_cast<const uint4*>(z + r * z_stride + ln * 8), zv);
+  const int64_t tok = r / heads;
+  unpack8(*reinterpret_cast<const uint4*>(z + tok * z_ts + (r - tok * heads) * z_hs + ln * 8), zv);
   float s = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) s = s + xv[e] * xv[e];
@@ -94,14 +96,17 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __re
 
 }  // namespace
 
-extern "C" FD_API int fd_gated_rmsnorm_fwd(const void* x, const void* gate, int64_t gate_row_stride,
-                                           const void* weight, int weight_dtype, void* out, int64_t rows, int width,
-                                           float eps, void* stream) {
+extern "C" FD_API int fd_gated_rmsnorm_fwd(const void* x, const void* gate, int64_t gate_token_stride,
+                                           int64_t gate_head_stride, int heads, const void* weight, int weight_dtype,
+                                           void* out, int64_t rows, int width, float eps, void* stream) {
   FD_REQUIRE(x && gate && weight && out, FD_ERR_INVALID_ARGUMENT, "fd_gated_rmsnorm_fwd: pointers must be non-null");
   FD_REQUIRE(width == 64 || width == 128 || width == 256, FD_ERR_UNSUPPORTED,
              "fd_gated_rmsnorm_fwd: width must be 64, 128 or 256 (got %d)", width);
-  FD_REQUIRE(rows >= 0 && gate_row_stride >= width && gate_row_stride % 8 == 0, FD_ERR_INVALID_ARGUMENT,
-             "fd_gated_rmsnorm_fwd: rows >= 0 and gate_row_stride a multiple of 8 >= width");
+  FD_REQUIRE(rows >= 0 && heads >= 1 && rows % heads == 0, FD_ERR_INVALID_ARGUMENT,
+             "fd_gated_rmsnorm_fwd: rows must be a non-negative multiple of heads >= 1");
+  FD_REQUIRE(gate_token_stride % 8 == 0 && gate_head_stride % 8 == 0 && gate_head_stride >= width &&
+                 gate_token_stride >= static_cast<int64_t>(heads) * gate_head_stride,
+             FD_ERR_ALIGNMENT, "fd_gated_rmsnorm_fwd: gate strides must be multiples of 8 covering [heads, width]");
   FD_REQUIRE(weight_dtype == FD_DTYPE_BF16 || weight_dtype == FD_DTYPE_F32, FD_ERR_INVALID_ARGUMENT,
              "fd_gated_rmsnorm_fwd: weight_dtype must be FD_DTYPE_BF16 or FD_DTYPE_F32");
   FD_REQUIRE(eps >= 0.0f, FD_ERR_INVALID_ARGUMENT, "fd_gated_rmsnorm_fwd: eps must be >= 0");
@@ -119,11 +124,11 @@ extern "C" FD_API int fd_gated_rmsnorm_fwd(const void* x, const void* gate, int6
 #define FD_GN(L)                                                                                              \
   do {                                                                                                        \
     if (weight_dtype == FD_DTYPE_F32)                                                                         \
-      hipLaunchKernelGGL((gated_rmsnorm_kernel<L, true>), grid, dim3(kThreads), 0, s, xp, zp, gate_row_stride, \
-                         weight, op, rows, eps);                                                              \
+      hipLaunchKernelGGL((gated_rmsnorm_kernel<L, true>), grid, dim3(kThreads), 0, s, xp, zp,                 \
+                         gate_token_stride, gate_head_stride, heads, weight, op, rows, eps);                  \
     else                                                                                                      \
       hipLaunchKernelGGL((gated_rmsnorm_kernel<L, false>), grid, dim3(kThreads), 0, s, xp, zp,                \
-                         gate_row_stride, weight, op, rows, eps);                                             \
+                         gate_token_stride, gate_head_stride, heads, weight, op, rows, eps);                  \
   } while (0)
   if (lanes == 8) FD_GN(8); else if (lanes == 16) FD_GN(16); else FD_GN(32);
 #undef FD_GN

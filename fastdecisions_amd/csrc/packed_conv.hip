@@ -53,8 +53,9 @@ __device__ __forceinline__ uint4 load16(const uint16_t* p) { return *reinterpret
 template <int WIDTH, int RUN, bool SILU, bool HAS_BIAS>
 __global__ __launch_bounds__(kThreads) void packed_conv_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias,
-    uint16_t* __restrict__ q, uint16_t* __restrict__ k, uint16_t* __restrict__ v, int total_rows, int seq_len,
-    int key_dim, int value_dim, const int32_t* __restrict__ cu_seqlens, int n_seqs, int n_runs, int n_col) {
+    uint16_t* __restrict__ q, uint16_t* __restrict__ k, uint16_t* __restrict__ v, int64_t x_row, int total_rows,
+    int seq_len, int key_dim, int value_dim, const int32_t* __restrict__ cu_seqlens, int n_seqs, int n_runs,
+    int n_col) {
   const int C = 2 * key_dim + value_dim;
   const int nblocks = gridDim.x;
   const int lin = blockIdx.x;
@@ -112,13 +113,13 @@ __global__ __launch_bounds__(kThreads) void packed_conv_kernel(
 #pragma unroll
   for (int j = 0; j < WIDTH - 1; ++j) {
     const int r = r0 - (WIDTH - 1) + j;
-    halo[j] = (r >= seg_start && r >= 0) ? load16(x + static_cast<int64_t>(r) * C + c0) : zero;
+    halo[j] = (r >= seg_start && r >= 0) ? load16(x + static_cast<int64_t>(r) * x_row + c0) : zero;
   }
   uint4 cur[RUN];
 #pragma unroll
   for (int i = 0; i < RUN; ++i) {
     const int r = r0 + i;
-    cur[i] = (r < r_end) ? load16(x + static_cast<int64_t>(r) * C + c0) : zero;
+    cur[i] = (r < r_end) ? load16(x + static_cast<int64_t>(r) * x_row + c0) : zero;
   }
 
   uint16_t* dst;
@@ -175,8 +176,8 @@ __global__ __launch_bounds__(kThreads) void packed_conv_kernel(
 }
 
 template <int WIDTH, int RUN>
-int launch_run(const void* x, const void* w, const void* bias, void* q, void* k, void* v, int total_rows,
-               int seq_len, int key_dim, int value_dim, const int32_t* cu, int n_seqs, int act,
+int launch_run(const void* x, int64_t x_row, const void* w, const void* bias, void* q, void* k, void* v,
+               int total_rows, int seq_len, int key_dim, int value_dim, const int32_t* cu, int n_seqs, int act,
                hipStream_t stream) {
   const int C = 2 * key_dim + value_dim;
   const int chunks = C / 8;
@@ -194,7 +195,7 @@ int launch_run(const void* x, const void* w, const void* bias, void* q, void* k,
   auto vs = static_cast<uint16_t*>(v);
 #define FD_CONV_LAUNCH(SILU, BIAS)                                                                         \
   hipLaunchKernelGGL((packed_conv_kernel<WIDTH, RUN, SILU, BIAS>), grid, block, 0, stream, xs, ws, bsp, qs, ks, vs, \
-                     total_rows, seq_len, key_dim, value_dim, cu, n_seqs, n_runs, n_col)
+                     x_row, total_rows, seq_len, key_dim, value_dim, cu, n_seqs, n_runs, n_col)
   const bool silu = act == FD_ACT_SILU;
   if (silu && bsp == nullptr) FD_CONV_LAUNCH(true, false);
   else if (silu) FD_CONV_LAUNCH(true, true);
@@ -212,11 +213,9 @@ int launch_run(const void* x, const void* w, const void* bias, void* q, void* k,
 // so occupancy matters more than the 3/4 halo re-read, which hits L2).
 constexpr int kRun = FD_CONV_RUN;
 
-}  // namespace
-
-extern "C" int fd_packed_conv_fwd(const void* x, const void* weight, const void* bias, void* q, void* k, void* v,
-                                  int batch, int seq_len, int key_dim, int value_dim, int width,
-                                  const int32_t* cu_seqlens, int n_seqs, int activation, void* stream) {
+int packed_conv_entry(const void* x, int64_t x_row_stride, const void* weight, const void* bias, void* q, void* k,
+                      void* v, int batch, int seq_len, int key_dim, int value_dim, int width,
+                      const int32_t* cu_seqlens, int n_seqs, int activation, void* stream) {
   FD_REQUIRE(x != nullptr && weight != nullptr && q != nullptr && k != nullptr && v != nullptr,
              FD_ERR_INVALID_ARGUMENT, "fd_packed_conv_fwd: x, weight, q, k and v must be non-null");
   FD_REQUIRE(batch >= 0 && seq_len >= 0, FD_ERR_INVALID_ARGUMENT,
@@ -230,7 +229,9 @@ extern "C" int fd_packed_conv_fwd(const void* x, const void* weight, const void*
              "fd_packed_conv_fwd: activation must be FD_ACT_NONE or FD_ACT_SILU (got %d)", activation);
   const int64_t total = static_cast<int64_t>(batch) * seq_len;
   const int64_t C = 2 * static_cast<int64_t>(key_dim) + value_dim;
-  FD_REQUIRE(total * C < (static_cast<int64_t>(1) << 40) && total < 2147483647LL && C <= 1048576,
+  FD_REQUIRE(x_row_stride >= C && x_row_stride % 8 == 0, FD_ERR_ALIGNMENT,
+             "fd_packed_conv_fwd: the row stride of x must be a multiple of 8 and >= C");
+  FD_REQUIRE(total * x_row_stride < (static_cast<int64_t>(1) << 40) && total < 2147483647LL && C <= 1048576,
              FD_ERR_INVALID_ARGUMENT, "fd_packed_conv_fwd: problem too large");
   if (cu_seqlens != nullptr) {
     FD_REQUIRE(batch == 1, FD_ERR_INVALID_ARGUMENT,
@@ -244,9 +245,26 @@ extern "C" int fd_packed_conv_fwd(const void* x, const void* weight, const void*
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int rows = static_cast<int>(total);
   switch (width) {
-    case 1: return launch_run<1, kRun>(x, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, s);
-    case 2: return launch_run<2, kRun>(x, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, s);
-    case 3: return launch_run<3, kRun>(x, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, s);
-    default: return launch_run<4, kRun>(x, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, s);
+    case 1: return launch_run<1, kRun>(x, x_row_stride, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, s);
+    case 2: return launch_run<2, kRun>(x, x_row_stride, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, s);
+    case 3: return launch_run<3, kRun>(x, x_row_stride, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, s);
+    default: return launch_run<4, kRun>(x, x_row_stride, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, s);
   }
+}
+
+}  // namespace
+
+extern "C" int fd_packed_conv_fwd(const void* x, const void* weight, const void* bias, void* q, void* k, void* v,
+                                  int batch, int seq_len, int key_dim, int value_dim, int width,
+                                  const int32_t* cu_seqlens, int n_seqs, int activation, void* stream) {
+  return packed_conv_entry(x, 2 * static_cast<int64_t>(key_dim) + value_dim, weight, bias, q, k, v, batch, seq_len,
+                           key_dim, value_dim, width, cu_seqlens, n_seqs, activation, stream);
+}
+
+extern "C" int fd_packed_conv_strided_fwd(const void* x, int64_t x_row_stride, const void* weight, const void* bias,
+                                          void* q, void* k, void* v, int batch, int seq_len, int key_dim,
+                                          int value_dim, int width, const int32_t* cu_seqlens, int n_seqs,
+                                          int activation, void* stream) {
+  return packed_conv_entry(x, x_row_stride, weight, bias, q, k, v, batch, seq_len, key_dim, value_dim, width,
+                           cu_seqlens, n_seqs, activation, stream);
 }

@@ -17,26 +17,37 @@ _W_DTYPES = {torch.bfloat16: _lib.FD_DTYPE_BF16, torch.float32: _lib.FD_DTYPE_F3
 
 
 def gated_rms_norm(x: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """x: contiguous [..., D]; gate: [..., heads, D] view with the same number of rows, a unit
+    feature stride and uniformly strided tokens (e.g. part of a combined projection output)."""
     if not x.is_cuda or x.dtype != torch.bfloat16 or gate.dtype != torch.bfloat16 or gate.device != x.device:
         raise ValueError("x and gate must be CUDA BF16 on one device")
     D = x.shape[-1]
-    if gate.shape != x.shape or D not in (64, 128, 256):
-        raise ValueError("x and gate must share a shape [..., D] with D in {64, 128, 256}")
-    if not x.is_contiguous():
-        raise ValueError("x must be contiguous")
-    g2 = gate.reshape(-1, D)
-    if g2.stride(1) != 1 or g2.data_ptr() % 16 or g2.stride(0) % 8:
+    if D not in (64, 128, 256) or gate.shape[-1] != D or gate.numel() != x.numel() or gate.ndim < 2:
+        raise ValueError("x [..., D] and gate [..., heads, D] must hold the same rows, D in {64, 128, 256}")
+    if not x.is_contiguous() or x.data_ptr() % 16:
+        raise ValueError("x must be contiguous and 16-byte aligned")
+    heads = gate.shape[-2]
+    hs = gate.stride(-2)
+    if gate.ndim == 2:
+        ts = heads * hs
+    else:
+        ts = gate.stride(-3)
+        dims, strides = gate.shape[:-3], gate.stride()[:-3]
+        expect = ts * gate.shape[-3]
+        for size, stride in zip(reversed(dims), reversed(strides)):
+            if size != 1 and stride != expect:
+                raise ValueError("gate tokens must be uniformly strided")
+            expect *= size
+    if gate.stride(-1) != 1 or gate.data_ptr() % 16 or hs % 8 or ts % 8:
         raise ValueError("gate rows must be contiguous and 16-byte aligned")
     if weight.shape != (D,) or weight.dtype not in _W_DTYPES or weight.device != x.device or not weight.is_contiguous():
         raise ValueError(f"weight must be a contiguous BF16 or FP32 vector [{D}] on x's device")
-    if x.data_ptr() % 16:
-        raise ValueError("x must be 16-byte aligned")
     rows = x.numel() // D
     with torch.cuda.device(x.device):
         out = torch.empty_like(x)
         _lib.check("fd_gated_rmsnorm_fwd", _lib.lib().fd_gated_rmsnorm_fwd(
-            x.data_ptr(), g2.data_ptr(), g2.stride(0), weight.data_ptr(), _W_DTYPES[weight.dtype], out.data_ptr(),
-            rows, D, float(eps), _lib.stream_handle(x.device)))
+            x.data_ptr(), gate.data_ptr(), ts, hs, heads, weight.data_ptr(), _W_DTYPES[weight.dtype],
+            out.data_ptr(), rows, D, float(eps), _lib.stream_handle(x.device)))
     return out
 
 

@@ -160,7 +160,7 @@ def build_decider(shape: DeciderShape = DECIDER_2B_SHAPED, seed: int = 0, device
 
 def install_hip_kernels(model: DeciderModel) -> dict:
     """Route the hot ops of every layer to the HIP kernels; returns per-op patch counts."""
-    from .combined_gates import install_combined_gates
+    from .combined_gates import install_combined_gates, install_combined_projections
     from .gated_delta import install_gated_delta_rule
     from .layer_fusions import install_gated_norm, install_mlp_fusion
     from .native_gqa import install_attention_fusions, install_native_gqa
@@ -169,6 +169,7 @@ def install_hip_kernels(model: DeciderModel) -> dict:
     return dict(packed_conv=install_packed_conv(model.core), native_gqa=install_native_gqa(model.core),
                 residual_rms=install_persistent_residual_rms(model.core, all_layers=True),
                 gated_delta=install_gated_delta_rule(model.core), combined_gates=install_combined_gates(model.core),
+                combined_projections=install_combined_projections(model.core),
                 attention_fusions=install_attention_fusions(model.core), gated_norm=install_gated_norm(model.core),
                 mlp_fusion=install_mlp_fusion(model.core))
 

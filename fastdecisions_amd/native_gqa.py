@@ -25,6 +25,7 @@ from __future__ import annotations
 from types import MethodType
 
 import torch
+import torch.nn.functional as F
 
 from typing import Optional
 
@@ -93,9 +94,18 @@ def _fused_forward(self, hidden_states, position_embeddings, cu_seqlens, max_seq
     """The attention layer with its prologue and output gate in HIP kernels."""
     shape = hidden_states.shape[:-1]
     d = self.head_dim
-    qg = self.q_proj(hidden_states).view(*shape, -1, 2 * d)   # per head: query | gate
-    kp = self.k_proj(hidden_states).view(*shape, -1, d)
-    v = self.v_proj(hidden_states).view(*shape, -1, d).transpose(1, 2)
+    if hasattr(self, "_fd_qkv_weight"):
+        # q|gate, k, v from one GEMM, read as strided views
+        proj = F.linear(hidden_states, self._fd_qkv_weight)
+        nq = self.q_proj.weight.shape[0]
+        nk = self.k_proj.weight.shape[0]
+        qg = proj[..., :nq].view(*shape, -1, 2 * d)
+        kp = proj[..., nq:nq + nk].view(*shape, -1, d)
+        v = proj[..., nq + nk:].view(*shape, -1, d).transpose(1, 2)
+    else:
+        qg = self.q_proj(hidden_states).view(*shape, -1, 2 * d)   # per head: query | gate
+        kp = self.k_proj(hidden_states).view(*shape, -1, d)
+        v = self.v_proj(hidden_states).view(*shape, -1, d).transpose(1, 2)
     cos, sin = position_embeddings
     q, k = attn_prologue(qg[..., :d], kp, self.q_norm.weight, self.k_norm.weight, cos.contiguous(),
                          sin.contiguous(), float(self.q_norm.eps))
@@ -150,13 +160,23 @@ def install_native_gqa(core) -> int:
 
 
 def install_attention_fusions(core) -> int:
-    """Run every attention layer's prologue and output gate in HIP kernels; return the count.
-    Installs ``candidate_forward`` where it is not there yet."""
+    """Run every attention layer's prologue and output gate in HIP kernels, with q|gate,
+    k and v from one GEMM on the concatenated weight (a non-persistent buffer; reinvoke
+    after changing weights); return the count.  Installs ``candidate_forward`` where it is
+    not there yet."""
     install_native_gqa(core)
     from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5Attention
     count = 0
     for module in core.modules():
         if isinstance(module, Qwen3_5Attention):
             module._fd_attn_fused = True
+            projs = (module.q_proj, module.k_proj, module.v_proj)
+            if all(p.bias is None for p in projs):
+                with torch.no_grad():
+                    weight = torch.cat([p.weight for p in projs], dim=0).detach()
+                if "_fd_qkv_weight" in module._buffers:
+                    module._fd_qkv_weight = weight
+                else:
+                    module.register_buffer("_fd_qkv_weight", weight, persistent=False)
             count += 1
     return count

@@ -76,19 +76,33 @@ def _forward(self, hidden_states, cache_params=None, attention_mask=None, **kwar
     from transformers.models.qwen3_5 import modeling_qwen3_5 as mq
     hidden_states = mq.apply_mask_to_padding_states(hidden_states, attention_mask)
     batch, seq, _ = hidden_states.shape
-    mixed = self.in_proj_qkv(hidden_states)
+    combined = hasattr(self, "_fd_in_proj_weight")
+    if combined:
+        # q|k|v, z, a, b from one GEMM, read below as strided views
+        proj = F.linear(hidden_states, self._fd_in_proj_weight)
+        c0 = 2 * self.key_dim + self.value_dim
+        c1 = c0 + self.value_dim
+        mixed = proj[..., :c0]
+    else:
+        mixed = self.in_proj_qkv(hidden_states)
     cu_seqlens = kwargs.get("cu_seq_lens_q")
     if cu_seqlens is not None:
         query, key, value = packed_conv_varlen(mixed, self.conv1d.weight, cu_seqlens)
     else:
         query, key, value = packed_conv(mixed, self.conv1d.weight)
-    z = self.in_proj_z(hidden_states).reshape(batch, seq, -1, self.head_v_dim)
-    if hasattr(self, "_combined_gate_weight"):
+    if combined:
+        from .combined_gates import gate_transform_op
+        z = proj[..., c0:c1].view(batch, seq, -1, self.head_v_dim)
+        h = self.num_v_heads
+        g, beta = gate_transform_op(proj[..., c1:c1 + h], proj[..., c1 + h:c1 + 2 * h], self.A_log, self.dt_bias)
+    elif hasattr(self, "_combined_gate_weight"):
+        z = self.in_proj_z(hidden_states).reshape(batch, seq, -1, self.head_v_dim)
         # one GEMM for both gate projections, one kernel for both transforms (ref: :45-48)
         from .combined_gates import unpack_gate_op
-        combined = F.linear(hidden_states, self._combined_gate_weight)
-        g, beta = unpack_gate_op(combined, self.A_log, self.dt_bias)
+        ab = F.linear(hidden_states, self._combined_gate_weight)
+        g, beta = unpack_gate_op(ab, self.A_log, self.dt_bias)
     else:
+        z = self.in_proj_z(hidden_states).reshape(batch, seq, -1, self.head_v_dim)
         b = self.in_proj_b(hidden_states)
         a = self.in_proj_a(hidden_states)
         beta = b.sigmoid()
@@ -112,10 +126,11 @@ def _forward(self, hidden_states, cache_params=None, attention_mask=None, **kwar
         core_attn_out = torch.cat(parts, dim=1)
     if getattr(self, "_fd_gated_norm", False):
         from .layer_fusions import gated_rms_norm_op
-        core_attn_out = gated_rms_norm_op(core_attn_out.reshape(-1, self.head_v_dim), z.reshape(-1, self.head_v_dim),
-                                          self.norm.weight, float(self.norm.variance_epsilon))
+        core_attn_out = gated_rms_norm_op(core_attn_out.reshape(-1, self.head_v_dim), z, self.norm.weight,
+                                          float(self.norm.variance_epsilon))
     else:
-        core_attn_out = self.norm(core_attn_out.reshape(-1, self.head_v_dim), z.reshape(-1, self.head_v_dim))
+        core_attn_out = self.norm(core_attn_out.reshape(-1, self.head_v_dim),
+                                  z.reshape(-1, self.head_v_dim))
     return self.out_proj(core_attn_out.reshape(batch, seq, -1))
 
 

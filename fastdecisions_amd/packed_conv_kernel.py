@@ -5,7 +5,8 @@ Drop-in for the reference's ``prep_qkv(input_qkv, weight)``
 contiguous token-major, depthwise weight ``[6144, 4]`` or ``[6144, 1, 4]``,
 outputs q, k, v ``[B, T, 16, 128]`` bf16 contiguous, launched on the current
 stream.  Validation and messages follow the reference; the fixed
-``T == 2048`` (ref: :200-201) is lifted to any ``T >= 1``.
+``T == 2048`` (ref: :200-201) is lifted to any ``T >= 1``, and the input may be
+a view of the first C columns of a wider projection output (uniform row stride).
 
 Keyword extensions (defaults reproduce the reference exactly): ``bias``,
 ``head_k_dim``/``head_v_dim`` and ``key_dim``/``value_dim`` for other head
@@ -50,7 +51,11 @@ def prep_qkv(
         raise ValueError("Expected input_qkv shape [B, T, 2*key_dim + value_dim], B >= 1, T >= 1")
     if key_dim % head_k_dim or value_dim % head_v_dim or head_k_dim % 8 or head_v_dim % 8:
         raise ValueError("key_dim/value_dim must be multiples of head dims that are multiples of 8")
-    if input_qkv.dtype != torch.bfloat16 or not input_qkv.is_contiguous():
+    # a view of the first C columns of a wider projection output is accepted too (rows
+    # stride(1) elements apart); the reference requires a contiguous tensor
+    row_stride = input_qkv.stride(1)
+    if (input_qkv.dtype != torch.bfloat16 or input_qkv.stride(2) != 1 or row_stride < C or row_stride % 8
+            or (B > 1 and input_qkv.stride(0) != T * row_stride)):
         raise ValueError("input_qkv must be contiguous BF16")
     if weight.device != input_qkv.device:
         raise ValueError("weight and input_qkv must share a device")
@@ -92,8 +97,8 @@ def prep_qkv(
         k = torch.empty_like(q)
         v = torch.empty((B, T, value_dim // head_v_dim, head_v_dim), device=input_qkv.device, dtype=input_qkv.dtype)
         lib = _lib.lib()
-        _lib.check("fd_packed_conv_fwd", lib.fd_packed_conv_fwd(
-            input_qkv.data_ptr(), weight.data_ptr(), _lib.ptr(bias), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-            B, T, key_dim, value_dim, width, cu_ptr, n_seqs, _ACTIVATIONS[activation],
+        _lib.check("fd_packed_conv_strided_fwd", lib.fd_packed_conv_strided_fwd(
+            input_qkv.data_ptr(), row_stride, weight.data_ptr(), _lib.ptr(bias), q.data_ptr(), k.data_ptr(),
+            v.data_ptr(), B, T, key_dim, value_dim, width, cu_ptr, n_seqs, _ACTIVATIONS[activation],
             _lib.stream_handle(input_qkv.device)))
     return q, k, v

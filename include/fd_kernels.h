@@ -54,7 +54,7 @@ extern "C" {
 #define FD_API
 #endif
 
-#define FD_ABI_VERSION 6
+#define FD_ABI_VERSION 7
 
 #define FD_OK 0
 #define FD_ERR_INVALID_ARGUMENT (-1) /* shape, size, stride or flag out of range */
@@ -173,6 +173,17 @@ FD_API int fd_packed_conv_fwd(const void* x, const void* weight, const void* bia
                        int activation, void* stream);
 
 /*
+ * fd_packed_conv_fwd on x rows x_row_stride elements apart (a multiple of 8, >= C):
+ * the q|k|v channels may be the first C columns of a wider combined projection
+ * output.  Other arguments and limits as fd_packed_conv_fwd.
+ */
+FD_API int fd_packed_conv_strided_fwd(const void* x, int64_t x_row_stride, const void* weight,
+                                      const void* bias, void* q, void* k, void* v, int batch,
+                                      int seq_len, int key_dim, int value_dim, int width,
+                                      const int32_t* cu_seqlens, int n_seqs, int activation,
+                                      void* stream);
+
+/*
  * Fused residual add + RMSNorm over rows of `width` features.
  *
  *   h            = bf16(x + residual)            (residual == NULL: h = x)
@@ -280,13 +291,15 @@ FD_API int fd_slot_readout_fwd(const void* hidden, int batch, int seq_len, int w
  * called after the delta rule, ref: src/decider/packed_conv.py:60-61), eager rounding:
  *   y = bf16(x / sqrt(mean(x^2) + eps));  y2 = bf16(w * y) (fp32 for an fp32 weight);
  *   out = bf16(y2 * z / (1 + exp(-z)))
- * x, out [rows, width] bf16 contiguous; gate z [rows, width] bf16 with row stride
- * gate_row_stride (elements); weight [width] of weight_dtype.
- * Limits: width in {64, 128, 256}; 16-byte aligned pointers.
+ * x, out [rows, width] bf16 contiguous, rows = tokens * heads (row r = token r / heads,
+ * head r % heads); gate z of row r at gate + token*gate_token_stride + head*gate_head_stride
+ * (elements: a [tokens, heads, width] view, e.g. part of a combined projection output);
+ * weight [width] of weight_dtype.
+ * Limits: width in {64, 128, 256}; 16-byte aligned pointers, strides multiples of 8.
  */
-FD_API int fd_gated_rmsnorm_fwd(const void* x, const void* gate, int64_t gate_row_stride,
-                                const void* weight, int weight_dtype, void* out, int64_t rows,
-                                int width, float eps, void* stream);
+FD_API int fd_gated_rmsnorm_fwd(const void* x, const void* gate, int64_t gate_token_stride,
+                                int64_t gate_head_stride, int heads, const void* weight, int weight_dtype,
+                                void* out, int64_t rows, int width, float eps, void* stream);
 
 /*
  * The MLP's activation (transformers Qwen3_5MLP: act_fn(gate_proj(x)) * up_proj(x)) on a

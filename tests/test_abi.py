@@ -23,7 +23,8 @@ def test_header_declares_the_expected_entry_points():
     assert declared_functions() == {"fd_abi_version", "fd_last_error", "fd_gqa_fwd", "fd_packed_conv_fwd",
                                     "fd_add_rmsnorm_fwd", "fd_gated_delta_workspace_bytes", "fd_gated_delta_fwd",
                                     "fd_gate_transform_fwd", "fd_gqa_gated_fwd", "fd_attn_prologue_fwd",
-                                    "fd_slot_readout_fwd", "fd_gated_rmsnorm_fwd", "fd_silu_mul_fwd"}
+                                    "fd_slot_readout_fwd", "fd_gated_rmsnorm_fwd", "fd_silu_mul_fwd",
+                                    "fd_packed_conv_strided_fwd"}
 
 
 def test_library_exports_every_declared_symbol_and_nothing_else():

@@ -198,3 +198,17 @@ def test_wrapper_rejects_bad_inputs():
     with pytest.raises(ValueError, match="batch size 1"):
         prep_qkv(torch.zeros((2, 16, 6144), dtype=torch.bfloat16, device="cuda"), w,
                  cu_seqlens=torch.tensor([0, 16], dtype=torch.int32, device="cuda"))
+
+
+def test_strided_input_from_a_wider_projection(oracle):
+    """The q|k|v columns read as a view of a wider [B, T, 8224] projection output give the
+    bit-identical result of the contiguous input."""
+    from fastdecisions_amd.packed_conv_kernel import prep_qkv
+    g = torch.Generator().manual_seed(44)
+    wide = torch.randn((2, 300, 8224), generator=g).to(torch.bfloat16).cuda()
+    w = (torch.randn((6144, 4), generator=g) * 0.25).to(torch.bfloat16).cuda()
+    announce("conv strided input B=2 T=300 row stride 8224")
+    got = prep_qkv(wide[..., :6144], w)
+    want = prep_qkv(wide[..., :6144].contiguous(), w)
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b) for a, b in zip(got, want))

@@ -47,14 +47,14 @@ def test_decider_sizes_vs_eager_on_gpu():
     gen = torch.Generator().manual_seed(31)
     x = (torch.randn((2048 * 16, 128), generator=gen) * 0.2).to(torch.bfloat16).cuda()
     zfull = (torch.randn((2048, 16, 2 * 128), generator=gen)).to(torch.bfloat16).cuda()
-    z = zfull[..., :128].reshape(-1, 128)   # a strided gate view
+    z = zfull[..., :128]   # a strided [tokens, heads, 128] gate view (no copy)
     norm = mq.Qwen3_5RMSNormGated(128, eps=1e-6).cuda()
     with torch.no_grad():
         norm.weight.copy_(1 + 0.02 * torch.randn(128, generator=gen).cuda())
     norm = norm.to(torch.bfloat16)
     announce("gated rmsnorm rows=32768, silu_mul 2048x6144")
     with torch.no_grad():
-        ours, eager = gated_rms_norm(x, z, norm.weight.data, 1e-6), norm(x, z)
+        ours, eager = gated_rms_norm(x, z, norm.weight.data, 1e-6), norm(x, z.reshape(-1, 128))
         gu = (torch.randn((2048, 2 * 6144), generator=gen) * 2).to(torch.bfloat16).cuda()
         m_ours = silu_mul(gu)
         m_eager = torch.nn.functional.silu(gu[:, :6144]) * gu[:, 6144:]

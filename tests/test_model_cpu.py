@@ -49,7 +49,8 @@ def test_install_patches_fall_back_on_cpu(tiny):
     with torch.no_grad():
         before = tiny(ids)
     counts = install_hip_kernels(tiny)
-    assert counts == dict(packed_conv=3, native_gqa=1, residual_rms=4, gated_delta=3, combined_gates=3, attention_fusions=1, gated_norm=3, mlp_fusion=4)
+    assert counts == dict(packed_conv=3, native_gqa=1, residual_rms=4, gated_delta=3, combined_gates=3, combined_projections=3, attention_fusions=1, gated_norm=3,
+                      mlp_fusion=4)
     assert install_hip_kernels(tiny) == counts  # idempotent
     with torch.no_grad():
         after = tiny(ids)

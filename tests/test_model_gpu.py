@@ -33,8 +33,9 @@ def _uninstall(model):
                 delattr(m, attr)
         if hasattr(m, "_fd_gated_delta"):
             delattr(m, "_fd_gated_delta")
-        if "_combined_gate_weight" in m._buffers:
-            del m._buffers["_combined_gate_weight"]
+        for buf in ("_combined_gate_weight", "_fd_in_proj_weight", "_fd_qkv_weight"):
+            if buf in m._buffers:
+                del m._buffers[buf]
         if hasattr(m, "_fd_attn_fused"):
             delattr(m, "_fd_attn_fused")
         if hasattr(m, "_fd_gated_norm"):
@@ -49,7 +50,8 @@ def test_install_counts_and_fallback(full_model):
     from fastdecisions_amd.model import install_hip_kernels
     counts = install_hip_kernels(full_model)
     try:
-        assert counts == dict(packed_conv=21, native_gqa=7, residual_rms=28, gated_delta=21, combined_gates=21, attention_fusions=7, gated_norm=21, mlp_fusion=28)
+        assert counts == dict(packed_conv=21, native_gqa=7, residual_rms=28, gated_delta=21, combined_gates=21, combined_projections=21,
+                              attention_fusions=7, gated_norm=21, mlp_fusion=28)
         # guarded fallbacks: grad mode goes to the original eager methods
         ids = torch.randint(0, 100, (1, 64), device="cuda")
         with torch.enable_grad():
