@@ -29,9 +29,10 @@
 //      own, so the 128 value columns split over 8 workgroups.  The state slice
 //      lives in registers; every operand of the next chunk is loaded straight
 //      into registers while the current chunk runs; two barriers per chunk.
+//      Its products run on bf16 MFMA over exact bf16 splits of the fp32 operands.
 //   4. gd_out_kernel — one workgroup per (chunk, value head), chunk-parallel:
 //      o = scale e^{gc} (q S_chunk) + A v'.
-// The fp32 products run on v_mfma_f32_16x16x4_f32 (lane l supplies A[l%16][l/16]
+// The output pass's fp32 products run on v_mfma_f32_16x16x4_f32 (lane l supplies A[l%16][l/16]
 // and B[l/16][l%16]; D[4*(l/16)+r][l%16] in register r).  The reduction index k
 // of 16 consecutive MFMAs is assigned as k = 16*(l/16) + s (s = step), so that
 // each lane reads its operands as contiguous runs.
@@ -61,10 +62,10 @@ struct GdArgs {
   int32_t* row0;     // [nc]  first packed row of each chunk
   int32_t* len;      // [nc]  valid rows of each chunk (0 = unused)
   int32_t* first;    // [N+1] first chunk of each request
-  float* gc;         // [Hv, nc, 64]
+  float* gc;         // [Hv, nc, 3, 64]: e^{gc_t}, e^{gl - gc_t}, then e^{gl} (gl = gc of the last row)
   uint16_t* qn;      // [Hv, nc, 64, 128] bf16
   uint16_t* kn;      // [Hv, nc, 128 (dk), 64 (t)] bf16, transposed
-  float* w;          // [Hv, nc, 64, 128]
+  uint16_t* w;       // [Hv, nc, 3, 64, 128] bf16: w split exactly into hi + mid + lo planes
   float* u;          // [Hv, nc, 64, 128]
   float* vn;         // [Hv, nc, 128 (dv), 64 (t)]  v' transposed
   float* aq;         // [Hv, nc, 64, 64]
@@ -80,6 +81,33 @@ __device__ __forceinline__ f32x4_t mfma4(float a, float b, f32x4_t c) {
 }
 
 __device__ __forceinline__ float bf16r(float x) { return fd_bf16_to_f32(fd_f32_to_bf16(x)); }
+
+__device__ __forceinline__ f32x4_t mfma_bf16(uint4 a, uint4 b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                 c, 0, 0, 0);
+}
+
+// x == hi + mid + lo exactly (each a bf16; the two differences are exact in fp32),
+// so a product with a bf16 value is three exact bf16 products accumulated in fp32.
+// The conversions are v_cvt_pk_bf16_f32 (round to nearest even).
+__device__ __forceinline__ void split3(float x, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
+  hi = fd_pack2(x, 0.0f) & 0xffffu;
+  const float r1 = x - fd_bf16_to_f32(hi);
+  mid = fd_pack2(r1, 0.0f) & 0xffffu;
+  lo = fd_pack2(r1 - fd_bf16_to_f32(mid), 0.0f) & 0xffffu;
+}
+
+// four fp32 values -> three planes of four bf16 each (8 bytes per plane)
+__device__ __forceinline__ void split3x4(const float* x, uint2& hi, uint2& mid, uint2& lo) {
+  const uint32_t h01 = fd_pack2(x[0], x[1]), h23 = fd_pack2(x[2], x[3]);
+  const float r[4] = {x[0] - fd_lo(h01), x[1] - fd_hi(h01), x[2] - fd_lo(h23), x[3] - fd_hi(h23)};
+  const uint32_t m01 = fd_pack2(r[0], r[1]), m23 = fd_pack2(r[2], r[3]);
+  const uint32_t l01 = fd_pack2(r[0] - fd_lo(m01), r[1] - fd_hi(m01));
+  const uint32_t l23 = fd_pack2(r[2] - fd_lo(m23), r[3] - fd_hi(m23));
+  hi = make_uint2(h01, h23);
+  mid = make_uint2(m01, m23);
+  lo = make_uint2(l01, l23);
+}
 
 __device__ __forceinline__ void unpack8(uint4 raw, float* x) {
   const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
@@ -271,8 +299,13 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
     }
     sG[l] = gv;
     sB[l] = bv;
-    sBG[l] = bv * expf(gv);
-    a.gc[hc * kC + l] = gv;
+    const float eg = expf(gv);
+    sBG[l] = bv * eg;
+    const float gl = __shfl(gv, kC - 1);
+    float* gx = a.gc + hc * 3 * kC;
+    gx[l] = eg;
+    gx[kC + l] = expf(gl - gv);
+    if (l == 0) gx[2 * kC] = expf(gl);
   }
   __syncthreads();
 
@@ -337,9 +370,22 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
     for (int m = i & ~3; m < i; ++m) a0 = fmaf(sL[i * kRowF + m], x[m], a0);
     x[i] = x[i] - ((a0 + a1) + (a2 + a3));
   }
-  float* dst = (is_w ? a.w : a.u) + hc * kC * kD + j;
+  if (is_w) {
+    // w as three exact bf16 planes for the state pass's bf16 MFMAs
+    uint16_t* dst = a.w + hc * 3 * kC * kD + j;
 #pragma unroll
-  for (int i = 0; i < kC; ++i) dst[i * kD] = x[i];
+    for (int i = 0; i < kC; ++i) {
+      uint32_t hi, mid, lo;
+      split3(x[i], hi, mid, lo);
+      dst[i * kD] = static_cast<uint16_t>(hi);
+      dst[kC * kD + i * kD] = static_cast<uint16_t>(mid);
+      dst[2 * kC * kD + i * kD] = static_cast<uint16_t>(lo);
+    }
+  } else {
+    float* dst = a.u + hc * kC * kD + j;
+#pragma unroll
+    for (int i = 0; i < kC; ++i) dst[i * kD] = x[i];
+  }
   if (is_w) {
     // normalised k, transposed ([dk][t]), for the state pass's k^T v' product
     uint4* kt = reinterpret_cast<uint4*>(a.kn + hc * kC * kD + static_cast<size_t>(j) * kC);
@@ -351,8 +397,16 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
 
 // ---------------------------------------------------------------------------
 // 3. sequential state pass over the chunks of one request
-constexpr int kRowS = kD + 4;    // fp32 row stride of the transposed state slice
-constexpr int kRowV = kC + 4;    // fp32 row stride of the transposed v' slice
+//
+// Both products of a chunk run on v_mfma_f32_16x16x32_bf16 with the fp32
+// operands split exactly into bf16 planes (x = hi + mid + lo): w S keeps six of
+// the nine plane products (hi.hi, hi.mid, mid.hi, hi.lo, mid.mid, lo.hi; the
+// rest are below 2^-24 relative), k^T v' (k is a bf16 value) keeps all three.
+// The lane layout is that of the fp32 MFMA (A[l%16][k], B[k][l%16],
+// D[4(l/16)+r][l%16]) with the 8 consecutive reduction indices 8(l/16)..+7 of
+// each 32-step in a lane.
+constexpr int kRowSB = kD + 8;   // bf16 row stride of a transposed state plane (272 B)
+constexpr int kRowVB = kC + 8;   // bf16 row stride of a transposed v' plane (144 B)
 
 __global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
   // XCD-aware order: block b runs on XCD b % 8; the logical index below gives
@@ -366,8 +420,8 @@ __global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
   int first, last;
   request_chunks(a, sq, &first, &last);
 
-  __shared__ __attribute__((aligned(16))) float sSt[kSlice * kRowS];
-  __shared__ __attribute__((aligned(16))) float sVd[kSlice * kRowV];
+  __shared__ __attribute__((aligned(16))) uint16_t sS[3][kSlice * kRowSB];   // state planes [col][dk]
+  __shared__ __attribute__((aligned(16))) uint16_t sVd[3][kSlice * kRowVB];  // e^{gl - gc} v' planes [col][t]
 
   const int tid = threadIdx.x;
   const int wv = tid >> 6;
@@ -376,7 +430,7 @@ __global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
   const int c16 = l & 15;
   const int col = kSlice * js + c16;  // value column owned in the C layout
 
-  // state slice in the C layout: S[m][r] = S[dk = 32wv + 16m + 4g4 + r][col]
+  // state slice in the C layout (fp32): S[m][r] = S[dk = 32wv + 16m + 4g4 + r][col]
   float S[2][4];
   const size_t state_base = (static_cast<size_t>(sq) * a.hv + h) * kD * kD;
 #pragma unroll
@@ -385,111 +439,124 @@ __global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
     for (int r = 0; r < 4; ++r)
       S[m][r] = a.s0 ? a.s0[state_base + static_cast<size_t>(32 * wv + 16 * m + 4 * g4 + r) * kD + col] : 0.0f;
 
-  // operands of one chunk, loaded straight into registers one chunk ahead
-  f32x4_t pw[8];   // w[16wv + c16][32g4 .. 32g4 + 31]       (A of w S)
-  float pu[4];     // u[16wv + 4g4 + r][col]                 (C layout)
-  uint4 pk[2][2];  // k^T[32wv + 16m + c16][16g4 .. +15]     (A of k^T v')
-  f32x4_t pgc;     // gc[16wv + 4g4 .. +3]
-  float pgl;       // gc[63]
-  auto prefetch = [&](int c) {
+  // operands of one chunk, loaded straight into registers one chunk ahead; two
+  // register sets alternate (the loop body is unrolled by two) and every load is
+  // issued unconditionally (past the last chunk it re-reads the last one)
+  struct ChunkRegs {
+    uint4 w[3][4];  // plane x, step s: w_x[16wv + c16][32s + 8g4 .. +7]      (A of w S)
+    uint4 k[2][2];  // tile m, step s: k^T[32wv + 16m + c16][32s + 8g4 .. +7]  (A of k^T v')
+    float u[4];     // u[16wv + 4g4 + r][col]                                 (C layout)
+    f32x4_t dec;    // e^{gl - gc_t}, t = 16wv + 4g4 .. +3
+    float egl;      // e^{gl}
+  };
+  auto load_chunk = [&](ChunkRegs& R, int c) {
+    c = min(c, last - 1);
     const size_t hc = static_cast<size_t>(h) * a.nc + c;
-    const float* w = a.w + hc * kC * kD + (16 * wv + c16) * kD + 32 * g4;
+    const uint16_t* w = a.w + hc * 3 * kC * kD + (16 * wv + c16) * kD + 8 * g4;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) pw[i] = *reinterpret_cast<const f32x4_t*>(w + 4 * i);
+    for (int x = 0; x < 3; ++x)
+#pragma unroll
+      for (int st = 0; st < 4; ++st) R.w[x][st] = *reinterpret_cast<const uint4*>(w + x * kC * kD + 32 * st);
+    const uint16_t* kt = a.kn + hc * kC * kD + 8 * g4;
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+        R.k[m][st] = *reinterpret_cast<const uint4*>(kt + (32 * wv + 16 * m + c16) * kC + 32 * st);
     const float* u = a.u + hc * kC * kD + col;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) pu[r] = u[(16 * wv + 4 * g4 + r) * kD];
-    const uint16_t* kt = a.kn + hc * kC * kD + 16 * g4;
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const uint16_t* row = kt + (32 * wv + 16 * m + c16) * kC;
-      pk[m][0] = *reinterpret_cast<const uint4*>(row);
-      pk[m][1] = *reinterpret_cast<const uint4*>(row + 8);
-    }
-    pgc = *reinterpret_cast<const f32x4_t*>(a.gc + hc * kC + 16 * wv + 4 * g4);
-    pgl = a.gc[hc * kC + kC - 1];
+    for (int r = 0; r < 4; ++r) R.u[r] = u[(16 * wv + 4 * g4 + r) * kD];
+    const float* gx = a.gc + hc * 3 * kC;
+    R.dec = *reinterpret_cast<const f32x4_t*>(gx + kC + 16 * wv + 4 * g4);
+    R.egl = gx[2 * kC];
   };
-  if (first < last) prefetch(first);
 
-  for (int c = first; c < last; ++c) {
+  auto step = [&](const ChunkRegs& R, int c) {
     const size_t hc = static_cast<size_t>(h) * a.nc + c;
-    float cw[32];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) cw[4 * i + e] = pw[i][e];
-    float cu[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) cu[r] = pu[r];
-    float ak[2][16];
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      unpack8(pk[m][0], ak[m]);
-      unpack8(pk[m][1], ak[m] + 8);
-    }
-    const f32x4_t gct = pgc;
-    const float gl = pgl;
-    if (c + 1 < last) prefetch(c + 1);
-
-    // state at the chunk start: to LDS (transposed, for w S) and to the workspace (for the output pass)
+    // state at the chunk start: bf16 planes to LDS (B of w S), fp32 to the workspace (output pass)
     float* sc = a.sc + hc * kD * kD + static_cast<size_t>(col) * kD;
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-      const f32x4_t sv = {S[m][0], S[m][1], S[m][2], S[m][3]};
       const int dk = 32 * wv + 16 * m + 4 * g4;
-      *reinterpret_cast<f32x4_t*>(sSt + c16 * kRowS + dk) = sv;
-      *reinterpret_cast<f32x4_t*>(sc + dk) = sv;
+      uint2 ph, pm, pl;
+      split3x4(S[m], ph, pm, pl);
+      *reinterpret_cast<uint2*>(sS[0] + c16 * kRowSB + dk) = ph;
+      *reinterpret_cast<uint2*>(sS[1] + c16 * kRowSB + dk) = pm;
+      *reinterpret_cast<uint2*>(sS[2] + c16 * kRowSB + dk) = pl;
+      *reinterpret_cast<f32x4_t*>(sc + dk) = f32x4_t{S[m][0], S[m][1], S[m][2], S[m][3]};
     }
     __syncthreads();
 
-    // v' = u - w S for rows 16wv..16wv+15 of this slice (two independent MFMA chains)
-    float bS[32];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const f32x4_t sv = *reinterpret_cast<const f32x4_t*>(sSt + c16 * kRowS + 32 * g4 + 4 * i);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) bS[4 * i + e] = sv[e];
-    }
+    // v' = u - w S for rows 16wv..16wv+15 of this slice
     f32x4_t acc0 = {};
     f32x4_t acc1 = {};
 #pragma unroll
-    for (int s = 0; s < 16; ++s) {
-      acc0 = mfma4(cw[s], bS[s], acc0);
-      acc1 = mfma4(cw[16 + s], bS[16 + s], acc1);
+    for (int st = 0; st < 4; ++st) {
+      const int off = c16 * kRowSB + 32 * st + 8 * g4;
+      const uint4 sh = *reinterpret_cast<const uint4*>(sS[0] + off);
+      const uint4 sm = *reinterpret_cast<const uint4*>(sS[1] + off);
+      const uint4 sl = *reinterpret_cast<const uint4*>(sS[2] + off);
+      acc0 = mfma_bf16(R.w[0][st], sh, acc0);
+      acc1 = mfma_bf16(R.w[0][st], sm, acc1);
+      acc0 = mfma_bf16(R.w[1][st], sh, acc0);
+      acc1 = mfma_bf16(R.w[0][st], sl, acc1);
+      acc0 = mfma_bf16(R.w[1][st], sm, acc0);
+      acc1 = mfma_bf16(R.w[2][st], sh, acc1);
     }
-    f32x4_t vnew, vdec;
+    f32x4_t vnew;
+    float vdec[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      vnew[r] = cu[r] - (acc0[r] + acc1[r]);
-      vdec[r] = vnew[r] * expf(gl - gct[r]);
+      vnew[r] = R.u[r] - (acc0[r] + acc1[r]);
+      vdec[r] = vnew[r] * R.dec[r];
     }
     *reinterpret_cast<f32x4_t*>(a.vn + hc * kD * kC + static_cast<size_t>(col) * kC + 16 * wv + 4 * g4) = vnew;
-    *reinterpret_cast<f32x4_t*>(sVd + c16 * kRowV + 16 * wv + 4 * g4) = vdec;
+    {
+      const int off = c16 * kRowVB + 16 * wv + 4 * g4;
+      uint2 ph, pm, pl;
+      split3x4(vdec, ph, pm, pl);
+      *reinterpret_cast<uint2*>(sVd[0] + off) = ph;
+      *reinterpret_cast<uint2*>(sVd[1] + off) = pm;
+      *reinterpret_cast<uint2*>(sVd[2] + off) = pl;
+    }
     __syncthreads();
 
     // S <- e^{gl} S + k^T (e^{gl - gc} v'), dk rows 32wv..32wv+31
-    float bV[16];
+    f32x4_t st0 = {S[0][0] * R.egl, S[0][1] * R.egl, S[0][2] * R.egl, S[0][3] * R.egl};
+    f32x4_t st1 = {S[1][0] * R.egl, S[1][1] * R.egl, S[1][2] * R.egl, S[1][3] * R.egl};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const f32x4_t vv = *reinterpret_cast<const f32x4_t*>(sVd + c16 * kRowV + 16 * g4 + 4 * i);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) bV[4 * i + e] = vv[e];
-    }
-    const float egl = expf(gl);
-    f32x4_t st0 = {S[0][0] * egl, S[0][1] * egl, S[0][2] * egl, S[0][3] * egl};
-    f32x4_t st1 = {S[1][0] * egl, S[1][1] * egl, S[1][2] * egl, S[1][3] * egl};
-#pragma unroll
-    for (int s = 0; s < 16; ++s) {
-      st0 = mfma4(ak[0][s], bV[s], st0);
-      st1 = mfma4(ak[1][s], bV[s], st1);
+    for (int st = 0; st < 2; ++st) {
+      const int off = c16 * kRowVB + 32 * st + 8 * g4;
+      const uint4 dh = *reinterpret_cast<const uint4*>(sVd[0] + off);
+      const uint4 dm = *reinterpret_cast<const uint4*>(sVd[1] + off);
+      const uint4 dl = *reinterpret_cast<const uint4*>(sVd[2] + off);
+      st0 = mfma_bf16(R.k[0][st], dh, st0);
+      st1 = mfma_bf16(R.k[1][st], dh, st1);
+      st0 = mfma_bf16(R.k[0][st], dm, st0);
+      st1 = mfma_bf16(R.k[1][st], dm, st1);
+      st0 = mfma_bf16(R.k[0][st], dl, st0);
+      st1 = mfma_bf16(R.k[1][st], dl, st1);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       S[0][r] = st0[r];
       S[1][r] = st1[r];
     }
-    // no third barrier: the next writes of sSt follow this iteration's second
-    // barrier, and the next writes of sVd follow the next iteration's first
+    // no third barrier: the next writes of sS follow this step's second barrier,
+    // and the next writes of sVd follow the next step's first
+  };
+
+  if (first < last) {
+    ChunkRegs A, B;
+    load_chunk(A, first);
+    for (int c = first; c < last; c += 2) {
+      load_chunk(B, c + 1);
+      step(A, c);
+      if (c + 1 < last) {
+        load_chunk(A, c + 2);
+        step(B, c + 1);
+      }
+    }
   }
 
   if (a.sN != nullptr) {
@@ -531,7 +598,7 @@ __global__ __launch_bounds__(kThreads) void gd_out_kernel(GdArgs a) {
     const int idx = 4 * tid + 1024 * i;
     *reinterpret_cast<f32x4_t*>(sA + (idx >> 6) * kRowF + (idx & 63)) = *reinterpret_cast<const f32x4_t*>(gaq + idx);
   }
-  if (wv == 0) sG[l] = a.gc[hc * kC + l];
+  if (wv == 0) sG[l] = a.gc[hc * 3 * kC + l];  // e^{gc_t}
   __syncthreads();
 
   const size_t o_row = static_cast<size_t>(a.hv) * kD;
@@ -575,7 +642,7 @@ __global__ __launch_bounds__(kThreads) void gd_out_kernel(GdArgs a) {
       for (int r = 0; r < 4; ++r) {
         const int t = 16 * rt + 4 * g4 + r;
         if (t < L) {
-          const float val = (a.scale * expf(sG[t])) * acc1[r] + acc2[r];
+          const float val = (a.scale * sG[t]) * acc1[r] + acc2[r];
           a.o[static_cast<size_t>(r0 + t) * o_row + h * kD + 16 * n + c16] = static_cast<uint16_t>(fd_f32_to_bf16(val));
         }
       }
@@ -599,13 +666,13 @@ GdLayout gd_layout(int64_t nc, int64_t hv, int64_t nseq) {
   L.first = off;
   off = al(off + static_cast<size_t>(nseq + 1) * 4);
   L.gc = off;
-  off = al(off + hc * kC * 4);
+  off = al(off + hc * 3 * kC * 4);
   L.qn = off;
   off = al(off + hc * kC * kD * 2);
   L.kn = off;
   off = al(off + hc * kC * kD * 2);
   L.w = off;
-  off = al(off + hc * kC * kD * 4);
+  off = al(off + hc * 3 * kC * kD * 2);
   L.u = off;
   off = al(off + hc * kC * kD * 4);
   L.vn = off;
@@ -697,7 +764,7 @@ extern "C" FD_API int fd_gated_delta_fwd(const void* q, const void* k, const voi
   a.gc = reinterpret_cast<float*>(ws + lay.gc);
   a.qn = reinterpret_cast<uint16_t*>(ws + lay.qn);
   a.kn = reinterpret_cast<uint16_t*>(ws + lay.kn);
-  a.w = reinterpret_cast<float*>(ws + lay.w);
+  a.w = reinterpret_cast<uint16_t*>(ws + lay.w);
   a.u = reinterpret_cast<float*>(ws + lay.u);
   a.vn = reinterpret_cast<float*>(ws + lay.vn);
   a.aq = reinterpret_cast<float*>(ws + lay.aq);
