@@ -72,6 +72,9 @@ def parse_args():
     p.add_argument("--only-kernel", choices=["gqa", "conv", "rmsnorm", "gdr", "copy"], default=None,
                    help="profiling aid: run just this kernel's HIP timing loop ('copy' is the plain device "
                         "copy used to calibrate HBM byte counters)")
+    p.add_argument("--only-forward", action="store_true",
+                   help="profiling aid: capture the HIP-path forward and replay it --steps times, nothing else "
+                        "(a kernel trace then covers every forward kernel in place)")
     return p.parse_args()
 
 
@@ -373,6 +376,30 @@ def bench_forward(args) -> dict:
         max_abs_logit_diff=float((got - ref).abs().max()), patched=counts)
 
 
+def forward_only(args) -> dict:
+    """The HIP-path forward alone: one graph capture, then `steps` replays."""
+    import torch
+    from fastdecisions_amd.engine import Engine
+    from fastdecisions_amd.model import DECIDER_2B_SHAPED, build_decider, install_hip_kernels
+    from fastdecisions_amd.workloads import config4_request
+    model = build_decider(DECIDER_2B_SHAPED, seed=args.seed, device="cuda")
+    ids = config4_request(DECIDER_2B_SHAPED.vocab_size).ids[None].cuda()
+    counts = install_hip_kernels(model)
+    engine = Engine(model)
+    engine.logits_all(ids)
+    key = tuple(ids.shape)
+    torch.cuda.synchronize()
+    ms = []
+    for _ in range(args.steps):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        engine.replay(key)
+        e.record()
+        e.synchronize()
+        ms.append(s.elapsed_time(e))
+    return dict(median_ms=statistics.median(ms), replays=args.steps, patched=counts)
+
+
 # --------------------------------------------------------------------------- CPU baseline
 
 def cpu_baseline() -> dict:
@@ -412,6 +439,9 @@ def main() -> int:
         fn = dict(gqa=bench_gqa, conv=bench_conv, rmsnorm=bench_rmsnorm, gdr=bench_gated_delta,
                   copy=bench_copy)[args.only_kernel]
         print(json.dumps({args.only_kernel: fn(args.kernel_samples, only=True)}), flush=True)
+        return 0
+    if args.only_forward:
+        print(json.dumps({"forward_only": forward_only(args)}), flush=True)
         return 0
 
     kernels = {}

@@ -108,7 +108,18 @@ class DeciderModel(nn.Module):
             kwargs = dict(cu_seq_lens_q=cu_seqlens, cu_seq_lens_k=cu_seqlens, max_length_q=int(max_seqlen),
                           max_length_k=int(max_seqlen), fd_segments=tuple(segments))
         pe = core.rotary_emb(h, pos)
-        for layer in core.layers[: self.config.num_hidden_layers]:
+        layers = core.layers[: self.config.num_hidden_layers]
+        from .persistent_residual_rms import chain_ready, fused_add_rms_norm_op
+        if len(layers) and chain_ready(core, h):
+            # every layer patched: each MLP residual add runs inside the next RMSNorm kernel
+            residual, delta = h, None
+            for layer in layers:
+                residual, delta = layer._fd_chain_step(residual, delta, position_embeddings=pe, attention_mask=None,
+                                                       position_ids=pos, **kwargs)
+            if final_norm:
+                return fused_add_rms_norm_op(delta, residual, core.norm.weight, core.norm.eps)[0]
+            return residual + delta
+        for layer in layers:
             h = layer(h, position_embeddings=pe, attention_mask=None, position_ids=pos, past_key_values=None,
                       **kwargs)
         return core.norm(h) if final_norm else h

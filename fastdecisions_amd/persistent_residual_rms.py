@@ -11,10 +11,16 @@ Mirrors ref: src/decider/persistent_residual_rms.py:
   input RMSNorm on the kernel, the token mixer, then one fused kernel for
   ``residual + mixer`` and the post-attention RMSNorm, whose second output is
   the residual the MLP adds onto (the reference recomputes it in Python, :33);
+* ``_chain_step`` — the same layer with the residual add of the previous
+  layer's MLP still pending: that add goes into this layer's input RMSNorm
+  kernel (``h = bf16(residual + mlp)``, then the norm of h), so a stack of
+  patched layers runs no separate add kernel; the decider's layer loop uses
+  it when every decoder layer is patched;
 * ``install_persistent_residual_rms(core, all_layers=False)`` — patches the
   linear-attention layers as the reference does (ref: :36-49), or every
-  decoder layer with ``all_layers=True``; requires width <= 8192 and the
-  layer's eps (the reference additionally fixes width 2048 and eps 1e-6).
+  decoder layer with ``all_layers=True`` (which also enables the chained
+  residual); requires width <= 8192 and the layer's eps (the reference
+  additionally fixes width 2048 and eps 1e-6).
 """
 from __future__ import annotations
 
@@ -78,6 +84,35 @@ def _forward(self, hidden_states, position_embeddings, attention_mask=None, posi
     return residual + self.mlp(normalized)
 
 
+def _chain_step(self, residual, delta, position_embeddings, attention_mask=None, position_ids=None, **kwargs):
+    """Decoder layer on (residual, delta) with the previous layer's ``residual + delta``
+    not yet formed (``delta`` is None for the first layer); returns this layer's
+    (residual, mlp output).  Same arithmetic as the eager layer: the add is rounded
+    to bf16 (it is the updated residual) before it is normalised."""
+    if delta is None:
+        normalized = rms_norm_op(residual, self.input_layernorm.weight, self.input_layernorm.eps)
+    else:
+        normalized, residual = fused_add_rms_norm_op(delta, residual, self.input_layernorm.weight,
+                                                     self.input_layernorm.eps)
+    if self.block_type == "linear_attention":
+        mixed = self.linear_attn(hidden_states=normalized, cache_params=None, attention_mask=attention_mask,
+                                 **kwargs)
+    else:
+        mixed, _ = self.self_attn(hidden_states=normalized, attention_mask=attention_mask,
+                                  position_ids=position_ids, past_key_values=None,
+                                  position_embeddings=position_embeddings, **kwargs)
+    normalized, residual = fused_add_rms_norm_op(mixed.contiguous(), residual, self.post_attention_layernorm.weight,
+                                                 self.post_attention_layernorm.eps)
+    return residual, self.mlp(normalized)
+
+
+def chain_ready(core, hidden_states) -> bool:
+    """True when every decoder layer of ``core`` runs ``_chain_step`` and the inputs are
+    ones the patched layers accept (inference, CUDA, bf16, contiguous)."""
+    return (getattr(core, "_fd_residual_chain", False) and not torch.is_grad_enabled() and hidden_states.is_cuda
+            and hidden_states.dtype == torch.bfloat16 and hidden_states.is_contiguous())
+
+
 def install_persistent_residual_rms(core, all_layers: bool = False) -> int:
     """Patch linear-attention decoder layers (or all with ``all_layers``); return the count."""
     from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5DecoderLayer
@@ -91,5 +126,8 @@ def install_persistent_residual_rms(core, all_layers: bool = False) -> int:
             if not hasattr(module, "_persistent_original_forward"):
                 module._persistent_original_forward = module.forward
                 module.forward = MethodType(_forward, module)
+                module._fd_chain_step = MethodType(_chain_step, module)
             count += 1
+    if all_layers and count:
+        core._fd_residual_chain = True
     return count

@@ -33,6 +33,9 @@ def _uninstall(model):
                 delattr(m, attr)
         if hasattr(m, "_fd_gated_delta"):
             delattr(m, "_fd_gated_delta")
+        for flag in ("_fd_chain_step", "_fd_residual_chain"):
+            if hasattr(m, flag):
+                delattr(m, flag)
         for buf in ("_combined_gate_weight", "_fd_in_proj_weight", "_fd_qkv_weight"):
             if buf in m._buffers:
                 del m._buffers[buf]
