@@ -266,32 +266,44 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
   const size_t qk_row = static_cast<size_t>(a.hk) * kD;
   const size_t v_row = static_cast<size_t>(a.hv) * kD;
   uint16_t* gq = a.qn + hc * kC * kD;
+  // every load of the block is issued before any is used (rows past the chunk's
+  // end re-read its first row and are zeroed below)
+  uint4 rq[4], rk[4], rv[4];
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int row = it * 16 + wv * 4 + g4;
-    const bool valid = row < L;
-    const size_t grow = static_cast<size_t>(r0 + (valid ? row : 0));
-    const uint4 zero = make_uint4(0, 0, 0, 0);
-    uint4 rq = valid ? *reinterpret_cast<const uint4*>(a.q + grow * qk_row + hk * kD + c16 * 8) : zero;
-    uint4 rk = valid ? *reinterpret_cast<const uint4*>(a.k + grow * qk_row + hk * kD + c16 * 8) : zero;
-    const uint4 rv = valid ? *reinterpret_cast<const uint4*>(a.v + grow * v_row + h * kD + c16 * 8) : zero;
-    if (a.l2norm) {
-      rq = l2norm_row8(rq);
-      rk = l2norm_row8(rk);
-    }
-    *reinterpret_cast<uint4*>(sQ + row * kRowK + c16 * 8) = rq;
-    *reinterpret_cast<uint4*>(sK + row * kRowK + c16 * 8) = rk;
-    *reinterpret_cast<uint4*>(sV + row * kRowK + c16 * 8) = rv;
-    *reinterpret_cast<uint4*>(gq + row * kD + c16 * 8) = rq;
+    const size_t grow = static_cast<size_t>(r0 + (row < L ? row : 0));
+    rq[it] = *reinterpret_cast<const uint4*>(a.q + grow * qk_row + hk * kD + c16 * 8);
+    rk[it] = *reinterpret_cast<const uint4*>(a.k + grow * qk_row + hk * kD + c16 * 8);
+    rv[it] = *reinterpret_cast<const uint4*>(a.v + grow * v_row + h * kD + c16 * 8);
   }
-  // g (inclusive cumsum over the chunk) and beta; padded rows carry g = beta = 0
+  // g and beta of row l (wave 0; padded rows carry g = beta = 0)
+  float gv = 0.0f, bv = 0.0f;
   if (wv == 0) {
-    const bool valid = l < L;
-    const size_t idx = static_cast<size_t>(r0 + (valid ? l : 0)) * a.hv + h;
-    float gv = valid ? a.g[idx] : 0.0f;
-    float bv = 0.0f;
-    if (valid) bv = a.beta_f32 ? static_cast<const float*>(a.beta)[idx]
-                               : fd_bf16_to_f32(static_cast<const uint16_t*>(a.beta)[idx]);
+    const size_t idx = static_cast<size_t>(r0 + (l < L ? l : 0)) * a.hv + h;
+    gv = a.g[idx];
+    bv = a.beta_f32 ? static_cast<const float*>(a.beta)[idx]
+                    : fd_bf16_to_f32(static_cast<const uint16_t*>(a.beta)[idx]);
+    if (l >= L) gv = bv = 0.0f;
+  }
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int row = it * 16 + wv * 4 + g4;
+    const uint4 zero = make_uint4(0, 0, 0, 0);
+    uint4 q4 = row < L ? rq[it] : zero;
+    uint4 k4 = row < L ? rk[it] : zero;
+    const uint4 v4 = row < L ? rv[it] : zero;
+    if (a.l2norm) {
+      q4 = l2norm_row8(q4);
+      k4 = l2norm_row8(k4);
+    }
+    *reinterpret_cast<uint4*>(sQ + row * kRowK + c16 * 8) = q4;
+    *reinterpret_cast<uint4*>(sK + row * kRowK + c16 * 8) = k4;
+    *reinterpret_cast<uint4*>(sV + row * kRowK + c16 * 8) = v4;
+    *reinterpret_cast<uint4*>(gq + row * kD + c16 * 8) = q4;
+  }
+  // g (inclusive cumsum over the chunk) and beta
+  if (wv == 0) {
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const float up = __shfl_up(gv, off);
@@ -331,7 +343,7 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
     for (int r = 0; r < 16; ++r) {
       const int i = 32 * I + (r >> 2) * 8 + (l >> 5) * 4 + (r & 3);
       const float dec = i >= j ? expf(sG[i] - gj) : 0.0f;
-      sL[i * kRowF + j] = i > j ? (sB[i] * accG[r]) * dec : 0.0f;
+      sL[j * kRowF + i] = i > j ? (sB[i] * accG[r]) * dec : 0.0f;  // transposed: sL[j][i] = L[i][j]
       gaq[i * kC + j] = i >= j ? (a.scale * accA[r]) * dec : 0.0f;
     }
   } else {
@@ -340,7 +352,10 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
   }
   __syncthreads();
 
-  // forward substitution (I + L) x = rhs, one column per thread
+  // forward substitution (I + L) x = rhs, one column per thread, right-looking:
+  // once x_m is final, every later row takes its term -L[i][m] x_m (column m of
+  // L is row m of the transposed tile), so one fma per step sits on the
+  // dependent chain and the reads of later columns run ahead
   const bool is_w = tid >= kD;   // waves 2, 3
   const int j = tid & (kD - 1);
   const uint16_t* src = is_w ? sK : sV;
@@ -356,19 +371,15 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
     x[i] = (is_w ? sBG[i] : sB[i]) * fd_bf16_to_f32(bits);
   }
 #pragma unroll
-  for (int i = 1; i < kC; ++i) {
-    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  for (int m = 0; m < kC - 1; ++m) {
+    const float xm = x[m];
 #pragma unroll
-    for (int m = 0; m + 4 <= i; m += 4) {
-      const f32x4_t lv = *reinterpret_cast<const f32x4_t*>(sL + i * kRowF + m);
-      a0 = fmaf(lv[0], x[m], a0);
-      a1 = fmaf(lv[1], x[m + 1], a1);
-      a2 = fmaf(lv[2], x[m + 2], a2);
-      a3 = fmaf(lv[3], x[m + 3], a3);
+    for (int i0 = (m + 1) & ~3; i0 < kC; i0 += 4) {
+      const f32x4_t lv = *reinterpret_cast<const f32x4_t*>(sL + m * kRowF + i0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (i0 + e > m) x[i0 + e] = fmaf(-lv[e], xm, x[i0 + e]);
     }
-#pragma unroll
-    for (int m = i & ~3; m < i; ++m) a0 = fmaf(sL[i * kRowF + m], x[m], a0);
-    x[i] = x[i] - ((a0 + a1) + (a2 + a3));
   }
   if (is_w) {
     // w as three exact bf16 planes for the state pass's bf16 MFMAs
