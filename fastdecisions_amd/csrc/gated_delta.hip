@@ -64,9 +64,12 @@ struct GdArgs {
   int32_t* first;    // [N+1] first chunk of each request
   float* gc;         // [Hv, nc, 3, 64]: e^{gc_t}, e^{gl - gc_t}, then e^{gl} (gl = gc of the last row)
   uint16_t* qn;      // [Hv, nc, 64, 128] bf16
-  uint16_t* kn;      // [Hv, nc, 128 (dk), 64 (t)] bf16, transposed
-  uint16_t* w;       // [Hv, nc, 3, 64, 128] bf16: w split exactly into hi + mid + lo planes
-  float* u;          // [Hv, nc, 64, 128]
+  // w, k^T and u are stored in the state pass's operand order: every load of a
+  // wavefront there reads 1 KiB contiguous (lane = 16 * g4 + c16, see gd_state_kernel)
+  uint16_t* kn;      // [Hv, nc, wv 4, m 2, st 2, lane 64, 8] bf16: k^T[32wv + 16m + c16][32st + 8g4 + e]
+  uint16_t* w;       // [Hv, nc, plane 3, wv 4, st 4, lane 64, 8] bf16: w_x[16wv + c16][32st + 8g4 + e],
+                     // w split exactly into hi + mid + lo planes
+  float* u;          // [Hv, nc, js 8, wv 4, lane 64, r 4]: u[16wv + 4g4 + r][16js + c16]
   float* vn;         // [Hv, nc, 128 (dv), 64 (t)]  v' transposed
   float* aq;         // [Hv, nc, 64, 64]
   float* sc;         // [Hv, nc, 128 (dv), 128 (dk)] state at chunk start, transposed
@@ -233,6 +236,8 @@ constexpr int kPrepG = kPrepL + kC * kRowF * 4;             // fp32 [64]  gc
 constexpr int kPrepB = kPrepG + kC * 4;                     // fp32 [64]  beta
 constexpr int kPrepBG = kPrepB + kC * 4;                    // fp32 [64]  beta e^gc
 constexpr int kPrepBytes = kPrepBG + kC * 4;
+constexpr int kRowT = kD + 4;    // fp32 row stride of the u / w staging tiles (reuse the q/k/v/L area)
+static_assert(2 * kC * kRowT * 4 <= kPrepG, "u and w staging tiles must fit below the g / beta vectors");
 
 // One workgroup per (chunk, value head).  u = T (beta v) and w = T (beta e^gc k)
 // are the solutions of (I + L) x = rhs; thread j < 128 solves for column j of
@@ -381,28 +386,59 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
         if (i0 + e > m) x[i0 + e] = fmaf(-lv[e], xm, x[i0 + e]);
     }
   }
-  if (is_w) {
-    // w as three exact bf16 planes for the state pass's bf16 MFMAs
-    uint16_t* dst = a.w + hc * 3 * kC * kD + j;
+  // u and w through LDS (the q/k/v/L tiles are dead after this barrier), then
+  // out in the state pass's operand order with 16-byte stores
+  __syncthreads();
+  float* tU = reinterpret_cast<float*>(smem);   // [64][kRowT] u
+  float* tW = tU + kC * kRowT;                  // [64][kRowT] w
+  {
+    float* dst = (is_w ? tW : tU) + j;
 #pragma unroll
-    for (int i = 0; i < kC; ++i) {
-      uint32_t hi, mid, lo;
-      split3(x[i], hi, mid, lo);
-      dst[i * kD] = static_cast<uint16_t>(hi);
-      dst[kC * kD + i * kD] = static_cast<uint16_t>(mid);
-      dst[2 * kC * kD + i * kD] = static_cast<uint16_t>(lo);
-    }
-  } else {
-    float* dst = a.u + hc * kC * kD + j;
-#pragma unroll
-    for (int i = 0; i < kC; ++i) dst[i * kD] = x[i];
+    for (int i = 0; i < kC; ++i) dst[i * kRowT] = x[i];
   }
   if (is_w) {
-    // normalised k, transposed ([dk][t]), for the state pass's k^T v' product
-    uint4* kt = reinterpret_cast<uint4*>(a.kn + hc * kC * kD + static_cast<size_t>(j) * kC);
+    // normalised k^T in the state pass's operand order: row dk = j, the 8 tokens
+    // 32st + 8g4 .. +7 of lane 16g4 + (j % 16) (16 lanes write 256 B contiguous)
+    uint16_t* kt = a.kn + hc * kC * kD;
+    const int kwv = j >> 5, km = (j >> 4) & 1, kc16 = j & 15;
 #pragma unroll
-    for (int i = 0; i < kC / 8; ++i)
-      kt[i] = make_uint4(kbits[4 * i], kbits[4 * i + 1], kbits[4 * i + 2], kbits[4 * i + 3]);
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int i = 4 * (4 * st + g);  // kbits index of token 32st + 8g
+        *reinterpret_cast<uint4*>(kt + ((((kwv * 2 + km) * 2 + st) * 64) + 16 * g + kc16) * 8) =
+            make_uint4(kbits[i], kbits[i + 1], kbits[i + 2], kbits[i + 3]);
+      }
+  }
+  __syncthreads();
+  uint16_t* gw = a.w + hc * 3 * kC * kD;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int q = tid + kThreads * it;  // (wv, st, lane) of one 8-value piece
+    const int lane = q & 63;
+    const int row = 16 * (q >> 8) + (lane & 15);
+    const int col = 32 * ((q >> 6) & 3) + 8 * (lane >> 4);
+    const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(tW + row * kRowT + col);
+    const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(tW + row * kRowT + col + 4);
+    const float va[4] = {v0[0], v0[1], v0[2], v0[3]};
+    const float vb[4] = {v1[0], v1[1], v1[2], v1[3]};
+    uint2 ha, ma, la, hb, mb, lb;
+    split3x4(va, ha, ma, la);
+    split3x4(vb, hb, mb, lb);
+    *reinterpret_cast<uint4*>(gw + q * 8) = make_uint4(ha.x, ha.y, hb.x, hb.y);
+    *reinterpret_cast<uint4*>(gw + kC * kD + q * 8) = make_uint4(ma.x, ma.y, mb.x, mb.y);
+    *reinterpret_cast<uint4*>(gw + 2 * kC * kD + q * 8) = make_uint4(la.x, la.y, lb.x, lb.y);
+  }
+  float* gu = a.u + hc * kC * kD;
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int q = tid + kThreads * it;  // (js, wv, lane) of one 4-value piece
+    const int lane = q & 63;
+    const int row = 16 * ((q >> 6) & 3) + 4 * (lane >> 4);
+    const int col = 16 * (q >> 8) + (lane & 15);
+    const f32x4_t v = {tU[row * kRowT + col], tU[(row + 1) * kRowT + col], tU[(row + 2) * kRowT + col],
+                       tU[(row + 3) * kRowT + col]};
+    *reinterpret_cast<f32x4_t*>(gu + q * 4) = v;
   }
 }
 
@@ -463,20 +499,20 @@ __global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
   auto load_chunk = [&](ChunkRegs& R, int c) {
     c = min(c, last - 1);
     const size_t hc = static_cast<size_t>(h) * a.nc + c;
-    const uint16_t* w = a.w + hc * 3 * kC * kD + (16 * wv + c16) * kD + 8 * g4;
+    // operand-ordered tiles: each wavefront load is 1 KiB contiguous (lane l = 16 g4 + c16)
+    const uint16_t* w = a.w + hc * 3 * kC * kD + (wv * 4 * 64 + l) * 8;
 #pragma unroll
     for (int x = 0; x < 3; ++x)
 #pragma unroll
-      for (int st = 0; st < 4; ++st) R.w[x][st] = *reinterpret_cast<const uint4*>(w + x * kC * kD + 32 * st);
-    const uint16_t* kt = a.kn + hc * kC * kD + 8 * g4;
+      for (int st = 0; st < 4; ++st) R.w[x][st] = *reinterpret_cast<const uint4*>(w + x * kC * kD + st * 64 * 8);
+    const uint16_t* kt = a.kn + hc * kC * kD + (wv * 4 * 64 + l) * 8;
 #pragma unroll
     for (int m = 0; m < 2; ++m)
 #pragma unroll
-      for (int st = 0; st < 2; ++st)
-        R.k[m][st] = *reinterpret_cast<const uint4*>(kt + (32 * wv + 16 * m + c16) * kC + 32 * st);
-    const float* u = a.u + hc * kC * kD + col;
+      for (int st = 0; st < 2; ++st) R.k[m][st] = *reinterpret_cast<const uint4*>(kt + (m * 2 + st) * 64 * 8);
+    const f32x4_t u4 = *reinterpret_cast<const f32x4_t*>(a.u + hc * kC * kD + ((js * 4 + wv) * 64 + l) * 4);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) R.u[r] = u[(16 * wv + 4 * g4 + r) * kD];
+    for (int r = 0; r < 4; ++r) R.u[r] = u4[r];
     const float* gx = a.gc + hc * 3 * kC;
     R.dec = *reinterpret_cast<const f32x4_t*>(gx + kC + 16 * wv + 4 * g4);
     R.egl = gx[2 * kC];
