@@ -31,11 +31,11 @@
 //      into registers while the current chunk runs; two barriers per chunk.
 //      Its products run on bf16 MFMA over exact bf16 splits of the fp32 operands.
 //   4. gd_out_kernel — one workgroup per (chunk, value head), chunk-parallel:
-//      o = scale e^{gc} (q S_chunk) + A v'.
-// The output pass's fp32 products run on v_mfma_f32_16x16x4_f32 (lane l supplies A[l%16][l/16]
-// and B[l/16][l%16]; D[4*(l/16)+r][l%16] in register r).  The reduction index k
-// of 16 consecutive MFMAs is assigned as k = 16*(l/16) + s (s = step), so that
-// each lane reads its operands as contiguous runs.
+//      o = scale e^{gc} (q S_chunk) + A v', on bf16 MFMA over the same splits.
+// The intermediates sit in the workspace in the order their consumer's MFMA
+// operands are loaded (one wavefront load = 1-2 KiB contiguous).  The MFMA
+// lane layout (v_mfma_f32_16x16x32_bf16): lane l supplies A[l%16][8(l/16)+j]
+// and B[8(l/16)+j][l%16] for j = 0..7 of each 32-step; D[4(l/16)+r][l%16].
 #include "fd_common.h"
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -70,18 +70,14 @@ struct GdArgs {
   uint16_t* w;       // [Hv, nc, plane 3, wv 4, st 4, lane 64, 8] bf16: w_x[16wv + c16][32st + 8g4 + e],
                      // w split exactly into hi + mid + lo planes
   float* u;          // [Hv, nc, js 8, wv 4, lane 64, r 4]: u[16wv + 4g4 + r][16js + c16]
-  float* vn;         // [Hv, nc, 128 (dv), 64 (t)]  v' transposed
+  float* vn;         // [Hv, nc, n 8, s 2, lane 64, j 8]: v'[32s + 8g4 + j][16n + c16] (output pass B order)
   float* aq;         // [Hv, nc, 64, 64]
-  float* sc;         // [Hv, nc, 128 (dv), 128 (dk)] state at chunk start, transposed
+  float* sc;         // [Hv, nc, n 8, s 4, lane 64, j 8]: chunk-start S[32s + 8g4 + j][16n + c16] (output pass B order)
   int hk, hv, nc, nseq;
   int varlen, seq_len, nct;  // packed requests (table) or a padded batch of nct chunks per sequence
   int beta_f32, l2norm;
   float scale;
 };
-
-__device__ __forceinline__ f32x4_t mfma4(float a, float b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
 
 __device__ __forceinline__ float bf16r(float x) { return fd_bf16_to_f32(fd_f32_to_bf16(x)); }
 
@@ -521,7 +517,9 @@ __global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
   auto step = [&](const ChunkRegs& R, int c) {
     const size_t hc = static_cast<size_t>(h) * a.nc + c;
     // state at the chunk start: bf16 planes to LDS (B of w S), fp32 to the workspace (output pass)
-    float* sc = a.sc + hc * kD * kD + static_cast<size_t>(col) * kD;
+    // (in the output pass's B-operand order: S[dk][col] at step s = dk / 32 of column group
+    // n = js, lane 16 (dk % 32 / 8) + c16, element dk % 8; 64 lanes write 1 KiB contiguous)
+    float* sc = a.sc + hc * kD * kD + static_cast<size_t>(js) * 4 * 64 * 8;
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       const int dk = 32 * wv + 16 * m + 4 * g4;
@@ -530,7 +528,8 @@ __global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
       *reinterpret_cast<uint2*>(sS[0] + c16 * kRowSB + dk) = ph;
       *reinterpret_cast<uint2*>(sS[1] + c16 * kRowSB + dk) = pm;
       *reinterpret_cast<uint2*>(sS[2] + c16 * kRowSB + dk) = pl;
-      *reinterpret_cast<f32x4_t*>(sc + dk) = f32x4_t{S[m][0], S[m][1], S[m][2], S[m][3]};
+      *reinterpret_cast<f32x4_t*>(sc + (wv * 64 + 16 * (2 * m + (g4 >> 1)) + c16) * 8 + 4 * (g4 & 1)) =
+          f32x4_t{S[m][0], S[m][1], S[m][2], S[m][3]};
     }
     __syncthreads();
 
@@ -557,7 +556,10 @@ __global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
       vnew[r] = R.u[r] - (acc0[r] + acc1[r]);
       vdec[r] = vnew[r] * R.dec[r];
     }
-    *reinterpret_cast<f32x4_t*>(a.vn + hc * kD * kC + static_cast<size_t>(col) * kC + 16 * wv + 4 * g4) = vnew;
+    // v'[t][col] in the output pass's B-operand order: step s = t / 32, lane 16 (t % 32 / 8) + c16
+    *reinterpret_cast<f32x4_t*>(a.vn + hc * kD * kC +
+                                ((js * 2 + (wv >> 1)) * 64 + 16 * (2 * (wv & 1) + (g4 >> 1)) + c16) * 8 +
+                                4 * (g4 & 1)) = vnew;
     {
       const int off = c16 * kRowVB + 16 * wv + 4 * g4;
       uint2 ph, pm, pl;
@@ -648,43 +650,56 @@ __global__ __launch_bounds__(kThreads) void gd_out_kernel(GdArgs a) {
   if (wv == 0) sG[l] = a.gc[hc * 3 * kC + l];  // e^{gc_t}
   __syncthreads();
 
+  // bf16 MFMA over exact three-plane splits of the fp32 operands: q S takes the
+  // three products of the bf16 q with S's planes, A v' six of the nine plane products
   const size_t o_row = static_cast<size_t>(a.hv) * kD;
+  auto split8 = [](const float* p, uint4& hi, uint4& mid, uint4& lo) {
+    const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(p);
+    const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(p + 4);
+    const float va[4] = {v0[0], v0[1], v0[2], v0[3]};
+    const float vb[4] = {v1[0], v1[1], v1[2], v1[3]};
+    uint2 ha, ma, la, hb, mb, lb;
+    split3x4(va, ha, ma, la);
+    split3x4(vb, hb, mb, lb);
+    hi = make_uint4(ha.x, ha.y, hb.x, hb.y);
+    mid = make_uint4(ma.x, ma.y, mb.x, mb.y);
+    lo = make_uint4(la.x, la.y, lb.x, lb.y);
+  };
 #pragma unroll 1
   for (int nn = 0; nn < 2; ++nn) {
     const int n = 2 * wv + nn;  // 16 value columns
-    float bS[32], bN[16];
-    const float* sc = a.sc + hc * kD * kD + static_cast<size_t>(16 * n + c16) * kD + 32 * g4;
+    // B operands: S[32s + 8g4 .. +7][16n + c16] and v'[32s + 8g4 .. +7][16n + c16], stored in
+    // this order by the state pass (each lane reads 32 B, a wavefront 2 KiB contiguous)
+    uint4 bS[3][4], bN[3][2];
+    const float* sc = a.sc + hc * kD * kD + (static_cast<size_t>(n) * 4 * 64 + l) * 8;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const f32x4_t sv = *reinterpret_cast<const f32x4_t*>(sc + 4 * i);
+    for (int st = 0; st < 4; ++st) split8(sc + st * 64 * 8, bS[0][st], bS[1][st], bS[2][st]);
+    const float* vn = a.vn + hc * kD * kC + (static_cast<size_t>(n) * 2 * 64 + l) * 8;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) bS[4 * i + e] = sv[e];
-    }
-    const float* vn = a.vn + hc * kD * kC + static_cast<size_t>(16 * n + c16) * kC + 16 * g4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const f32x4_t vv = *reinterpret_cast<const f32x4_t*>(vn + 4 * i);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) bN[4 * i + e] = vv[e];
-    }
+    for (int st = 0; st < 2; ++st) split8(vn + st * 64 * 8, bN[0][st], bN[1][st], bN[2][st]);
 #pragma unroll 1
     for (int rt = 0; rt < 4; ++rt) {
-      float aQ[32], aA[16];
-      const uint16_t* pq = sQ + (16 * rt + c16) * kRowK + 32 * g4;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) unpack8(*reinterpret_cast<const uint4*>(pq + 8 * i), aQ + 8 * i);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const f32x4_t av = *reinterpret_cast<const f32x4_t*>(sA + (16 * rt + c16) * kRowF + 16 * g4 + 4 * i);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) aA[4 * i + e] = av[e];
-      }
+      // A operands: q[16rt + c16][32s + 8g4 .. +7] (bf16) and A[16rt + c16][32s + 8g4 .. +7] (fp32, split)
       f32x4_t acc1 = {};
       f32x4_t acc2 = {};
 #pragma unroll
-      for (int s = 0; s < 32; ++s) acc1 = mfma4(aQ[s], bS[s], acc1);
+      for (int st = 0; st < 4; ++st) {
+        const uint4 aq = *reinterpret_cast<const uint4*>(sQ + (16 * rt + c16) * kRowK + 32 * st + 8 * g4);
+        acc1 = mfma_bf16(aq, bS[0][st], acc1);
+        acc1 = mfma_bf16(aq, bS[1][st], acc1);
+        acc1 = mfma_bf16(aq, bS[2][st], acc1);
+      }
 #pragma unroll
-      for (int s = 0; s < 16; ++s) acc2 = mfma4(aA[s], bN[s], acc2);
+      for (int st = 0; st < 2; ++st) {
+        uint4 ah, am, al;
+        split8(sA + (16 * rt + c16) * kRowF + 32 * st + 8 * g4, ah, am, al);
+        acc2 = mfma_bf16(ah, bN[0][st], acc2);
+        acc2 = mfma_bf16(ah, bN[1][st], acc2);
+        acc2 = mfma_bf16(am, bN[0][st], acc2);
+        acc2 = mfma_bf16(ah, bN[2][st], acc2);
+        acc2 = mfma_bf16(am, bN[1][st], acc2);
+        acc2 = mfma_bf16(al, bN[0][st], acc2);
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = 16 * rt + 4 * g4 + r;
