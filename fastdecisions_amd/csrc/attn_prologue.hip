@@ -39,7 +39,8 @@ struct PrologueArgs {
   float eps;
 };
 
-__device__ __forceinline__ float bf16r(float x) { return fd_bf16_to_f32(fd_f32_to_bf16(x)); }
+// round to bf16 and back (v_cvt_pk_bf16_f32, round to nearest even)
+__device__ __forceinline__ float bf16r(float x) { return fd_lo(fd_pack2(x, 0.0f)); }
 
 __global__ __launch_bounds__(kThreads) void attn_prologue_kernel(PrologueArgs a) {
   const int64_t grp = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) >> 4;
@@ -47,7 +48,7 @@ __global__ __launch_bounds__(kThreads) void attn_prologue_kernel(PrologueArgs a)
   const bool valid = grp < a.rows;   // uniform over the 16 lanes of a group
   const int heads = a.hq + a.hkv;
   const int64_t row = valid ? grp : 0;
-  const int64_t t = row / heads;
+  const int64_t t = static_cast<int>(row) / heads;  // rows < 2^31 (checked by the host)
   const int hh = static_cast<int>(row - t * heads);
   const bool isq = hh < a.hq;
   const uint16_t* src = isq ? a.q_in + t * a.q_ts + hh * a.q_hs : a.k_in + t * a.k_ts + (hh - a.hq) * a.k_hs;
@@ -100,10 +101,10 @@ __global__ __launch_bounds__(kThreads) void attn_prologue_kernel(PrologueArgs a)
   if (valid) {
     uint16_t* dst = isq ? a.q_out + (t * a.hq + hh) * kD : a.k_out + (t * a.hkv + (hh - a.hq)) * kD;
     uint4 out;
-    out.x = fd_f32_to_bf16(y[0]) | (fd_f32_to_bf16(y[1]) << 16);
-    out.y = fd_f32_to_bf16(y[2]) | (fd_f32_to_bf16(y[3]) << 16);
-    out.z = fd_f32_to_bf16(y[4]) | (fd_f32_to_bf16(y[5]) << 16);
-    out.w = fd_f32_to_bf16(y[6]) | (fd_f32_to_bf16(y[7]) << 16);
+    out.x = fd_pack2(y[0], y[1]);
+    out.y = fd_pack2(y[2], y[3]);
+    out.z = fd_pack2(y[4], y[5]);
+    out.w = fd_pack2(y[6], y[7]);
     *reinterpret_cast<uint4*>(dst + ln * 8) = out;
   }
 }
@@ -138,7 +139,8 @@ extern "C" FD_API int fd_attn_prologue_fwd(const void* q_in, int64_t q_token_str
   const int64_t rows = tokens * (q_heads + kv_heads);
   if (rows == 0) return FD_OK;
   const int64_t blocks = (rows * 16 + kThreads - 1) / kThreads;
-  FD_REQUIRE(blocks < (1LL << 31), FD_ERR_INVALID_ARGUMENT, "fd_attn_prologue_fwd: problem too large");
+  FD_REQUIRE(blocks < (1LL << 31) && rows < (1LL << 31), FD_ERR_INVALID_ARGUMENT,
+             "fd_attn_prologue_fwd: problem too large");
   PrologueArgs a;
   a.q_in = static_cast<const uint16_t*>(q_in);
   a.k_in = static_cast<const uint16_t*>(k_in);

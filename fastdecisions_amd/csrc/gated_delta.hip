@@ -79,7 +79,8 @@ struct GdArgs {
   float scale;
 };
 
-__device__ __forceinline__ float bf16r(float x) { return fd_bf16_to_f32(fd_f32_to_bf16(x)); }
+// round to bf16 and back (v_cvt_pk_bf16_f32, round to nearest even)
+__device__ __forceinline__ float bf16r(float x) { return fd_lo(fd_pack2(x, 0.0f)); }
 
 __device__ __forceinline__ f32x4_t mfma_bf16(uint4 a, uint4 b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
@@ -119,10 +120,10 @@ __device__ __forceinline__ void unpack8(uint4 raw, float* x) {
 
 __device__ __forceinline__ uint4 pack8(const float* x) {
   uint4 r;
-  r.x = fd_f32_to_bf16(x[0]) | (fd_f32_to_bf16(x[1]) << 16);
-  r.y = fd_f32_to_bf16(x[2]) | (fd_f32_to_bf16(x[3]) << 16);
-  r.z = fd_f32_to_bf16(x[4]) | (fd_f32_to_bf16(x[5]) << 16);
-  r.w = fd_f32_to_bf16(x[6]) | (fd_f32_to_bf16(x[7]) << 16);
+  r.x = fd_pack2(x[0], x[1]);
+  r.y = fd_pack2(x[2], x[3]);
+  r.z = fd_pack2(x[4], x[5]);
+  r.w = fd_pack2(x[6], x[7]);
   return r;
 }
 

@@ -20,7 +20,8 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ float bf16r(float x) { return fd_bf16_to_f32(fd_f32_to_bf16(x)); }
+// round to bf16 and back (v_cvt_pk_bf16_f32, round to nearest even)
+__device__ __forceinline__ float bf16r(float x) { return fd_lo(fd_pack2(x, 0.0f)); }
 
 __device__ __forceinline__ void unpack8(uint4 raw, float* x) {
   const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
@@ -32,12 +33,7 @@ __device__ __forceinline__ void unpack8(uint4 raw, float* x) {
 }
 
 __device__ __forceinline__ uint4 pack8(const float* x) {
-  uint4 r;
-  r.x = fd_f32_to_bf16(x[0]) | (fd_f32_to_bf16(x[1]) << 16);
-  r.y = fd_f32_to_bf16(x[2]) | (fd_f32_to_bf16(x[3]) << 16);
-  r.z = fd_f32_to_bf16(x[4]) | (fd_f32_to_bf16(x[5]) << 16);
-  r.w = fd_f32_to_bf16(x[6]) | (fd_f32_to_bf16(x[7]) << 16);
-  return r;
+  return make_uint4(fd_pack2(x[0], x[1]), fd_pack2(x[2], x[3]), fd_pack2(x[4], x[5]), fd_pack2(x[6], x[7]));
 }
 
 // LANES lanes per row (LANES * 8 == width)
@@ -55,8 +51,9 @@ __global__ __launch_bounds__(kThreads) void gated_rmsnorm_kernel(const uint16_t*
   const int64_t r = valid ? row : 0;
   float xv[8], zv[8];
   unpack8(*reinterpret_cast<const uint4*>(x + r * kWidth + ln * 8), xv);
-  const int64_t tok = r / heads;
-  unpack8(*reinterpret_cast<const uint4*>(z + tok * z_ts + (r - tok * heads) * z_hs + ln * 8), zv);
+  const int tok = static_cast<int>(r) / heads;  // rows < 2^31 (checked by the host)
+  const int hd = static_cast<int>(r) - tok * heads;
+  unpack8(*reinterpret_cast<const uint4*>(z + tok * z_ts + hd * z_hs + ln * 8), zv);
   float s = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) s = s + xv[e] * xv[e];
@@ -79,18 +76,20 @@ __global__ __launch_bounds__(kThreads) void gated_rmsnorm_kernel(const uint16_t*
   if (valid) *reinterpret_cast<uint4*>(out + r * kWidth + ln * 8) = pack8(y);
 }
 
+// one 8-feature piece per thread; blockIdx.y is the row, so no index division
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __restrict__ gu, int64_t gu_stride,
-                                                            uint16_t* __restrict__ out, int64_t rows, int width) {
-  const int chunks = width / 8;
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  if (i >= rows * chunks) return;
-  const int64_t r = i / chunks;
-  const int c = static_cast<int>(i - r * chunks);
-  float g[8], u[8], y[8];
+                                                            uint16_t* __restrict__ out, int width) {
+  const int c = blockIdx.x * kThreads + threadIdx.x;  // piece within the row
+  if (c * 8 >= width) return;
+  const int64_t r = blockIdx.y;
+  float g[8], u[8], s[8], y[8];
   unpack8(*reinterpret_cast<const uint4*>(gu + r * gu_stride + c * 8), g);
   unpack8(*reinterpret_cast<const uint4*>(gu + r * gu_stride + width + c * 8), u);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = bf16r(g[e] / (1.0f + expf(-g[e]))) * u[e];
+  for (int e = 0; e < 8; ++e) s[e] = g[e] / (1.0f + expf(-g[e]));
+  unpack8(pack8(s), s);  // act_fn's bf16 output
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = s[e] * u[e];
   *reinterpret_cast<uint4*>(out + r * width + c * 8) = pack8(y);
 }
 
@@ -115,7 +114,8 @@ extern "C" FD_API int fd_gated_rmsnorm_fwd(const void* x, const void* gate, int6
   if (rows == 0) return FD_OK;
   const int lanes = width / 8;
   const int64_t blocks = (rows * lanes + kThreads - 1) / kThreads;
-  FD_REQUIRE(blocks < (1LL << 31), FD_ERR_INVALID_ARGUMENT, "fd_gated_rmsnorm_fwd: problem too large");
+  FD_REQUIRE(blocks < (1LL << 31) && rows < (1LL << 31), FD_ERR_INVALID_ARGUMENT,
+             "fd_gated_rmsnorm_fwd: problem too large");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* zp = static_cast<const uint16_t*>(gate);
@@ -143,12 +143,17 @@ extern "C" FD_API int fd_silu_mul_fwd(const void* gate_up, int64_t row_stride, v
              "fd_silu_mul_fwd: width a positive multiple of 8 and row_stride a multiple of 8 >= 2*width");
   FD_REQUIRE(fd_aligned16(gate_up) && fd_aligned16(out), FD_ERR_ALIGNMENT,
              "fd_silu_mul_fwd: gate_up and out must be 16-byte aligned");
-  const int64_t n = rows * (width / 8);
-  if (n == 0) return FD_OK;
-  const int64_t blocks = (n + kThreads - 1) / kThreads;
-  FD_REQUIRE(blocks < (1LL << 31), FD_ERR_INVALID_ARGUMENT, "fd_silu_mul_fwd: problem too large");
-  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gate_up), row_stride,
-                     static_cast<uint16_t*>(out), rows, width);
+  if (rows == 0) return FD_OK;
+  FD_REQUIRE(rows <= 65535 * 1024LL && width <= (1 << 28), FD_ERR_INVALID_ARGUMENT,
+             "fd_silu_mul_fwd: problem too large");
+  const int64_t pieces = width / 8;
+  const unsigned bx = static_cast<unsigned>((pieces + kThreads - 1) / kThreads);
+  // rows beyond the grid's y limit run in slabs of 65535
+  for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
+    const unsigned by = static_cast<unsigned>(rows - r0 < 65535 ? rows - r0 : 65535);
+    hipLaunchKernelGGL(silu_mul_kernel, dim3(bx, by), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(gate_up) + r0 * row_stride, row_stride,
+                       static_cast<uint16_t*>(out) + r0 * width, width);
+  }
   return fd_check_launch("fd_silu_mul_fwd");
 }

@@ -35,7 +35,8 @@ struct SlotArgs {
   float eps, temp;
 };
 
-__device__ __forceinline__ float bf16r(float x) { return fd_bf16_to_f32(fd_f32_to_bf16(x)); }
+// round to bf16 and back (v_cvt_pk_bf16_f32, round to nearest even)
+__device__ __forceinline__ float bf16r(float x) { return fd_lo(fd_pack2(x, 0.0f)); }
 
 __device__ __forceinline__ float wave_sum(float s) {
 #pragma unroll
