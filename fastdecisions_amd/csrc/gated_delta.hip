@@ -82,6 +82,10 @@ struct GdArgs {
 // round to bf16 and back (v_cvt_pk_bf16_f32, round to nearest even)
 __device__ __forceinline__ float bf16r(float x) { return fd_lo(fd_pack2(x, 0.0f)); }
 
+__device__ __forceinline__ f32x4_t mfma_f32(float a, float b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ f32x4_t mfma_bf16(uint4 a, uint4 b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
                                                  c, 0, 0, 0);
@@ -354,10 +358,14 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
   }
   __syncthreads();
 
-  // forward substitution (I + L) x = rhs, one column per thread, right-looking:
-  // once x_m is final, every later row takes its term -L[i][m] x_m (column m of
-  // L is row m of the transposed tile), so one fma per step sits on the
-  // dependent chain and the reads of later columns run ahead
+  // forward substitution (I + L) x = rhs, one column per thread (wave wv owns the 64
+  // columns of its lanes), in four blocks of 16 rows:
+  //  - inside a block, right-looking on the thread's column: once x_m is final every
+  //    later row of the block takes -L[i][m] x_m (column m of L is row m of the
+  //    transposed tile, read as broadcasts);
+  //  - after a block, every remaining row takes -L[rest, block] X_block on fp32 MFMA
+  //    (v_mfma_f32_16x16x4f32), the operands and results passing through a
+  //    wave-private LDS area (the wave's own 64 columns: no barrier).
   const bool is_w = tid >= kD;   // waves 2, 3
   const int j = tid & (kD - 1);
   const uint16_t* src = is_w ? sK : sV;
@@ -372,16 +380,59 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
       kbits[i >> 1] = bits;
     x[i] = (is_w ? sBG[i] : sB[i]) * fd_bf16_to_f32(bits);
   }
+  __syncthreads();  // every wave has read its right-hand sides: the q/k/v tiles are free
+  float* wl = reinterpret_cast<float*>(smem) + wv * (48 * 64);  // 12 KiB per wave
 #pragma unroll
-  for (int m = 0; m < kC - 1; ++m) {
-    const float xm = x[m];
+  for (int b = 0; b < 4; ++b) {
+    const int b0 = 16 * b;
 #pragma unroll
-    for (int i0 = (m + 1) & ~3; i0 < kC; i0 += 4) {
-      const f32x4_t lv = *reinterpret_cast<const f32x4_t*>(sL + m * kRowF + i0);
+    for (int m = b0; m < b0 + 15; ++m) {
+      const float xm = x[m];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (i0 + e > m) x[i0 + e] = fmaf(-lv[e], xm, x[i0 + e]);
+      for (int i0 = (m + 1) & ~3; i0 < b0 + 16; i0 += 4) {
+        const f32x4_t lv = *reinterpret_cast<const f32x4_t*>(sL + m * kRowF + i0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (i0 + e > m) x[i0 + e] = fmaf(-lv[e], xm, x[i0 + e]);
+      }
     }
+    if (b == 3) break;
+    // X_block (16 rows of the wave's 64 columns) -> LDS [16][64]
+#pragma unroll
+    for (int k = 0; k < 16; ++k) wl[k * 64 + l] = x[b0 + k];
+    // C[rest rows][64 columns] = L[rest, block] X_block: rest row tile rt (16 rows), column tile t
+    constexpr int kMaxRt = 3;
+    const int nrt = 3 - b;
+    float bx[4][4];  // B[k = 4s + l/16][n = 16t + l%16]
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int st = 0; st < 4; ++st) bx[t][st] = wl[(4 * st + (l >> 4)) * 64 + 16 * t + (l & 15)];
+    f32x4_t acc[kMaxRt][4];
+#pragma unroll
+    for (int rt = 0; rt < kMaxRt; ++rt) {
+      if (rt >= nrt) break;
+      float al[4];  // A[i = l%16][k = l/16 + 4s] = L[b0 + 16 + 16rt + l%16][b0 + 4s + l/16]
+#pragma unroll
+      for (int st = 0; st < 4; ++st) al[st] = sL[(b0 + 4 * st + (l >> 4)) * kRowF + b0 + 16 + 16 * rt + (l & 15)];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        acc[rt][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) acc[rt][t] = mfma_f32(al[st], bx[t][st], acc[rt][t]);
+      }
+    }
+    // C -> LDS [rest rows][64], then every lane subtracts its own column
+#pragma unroll
+    for (int rt = 0; rt < kMaxRt; ++rt) {
+      if (rt >= nrt) break;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wl[(16 * rt + 4 * (l >> 4) + r) * 64 + 16 * t + (l & 15)] = acc[rt][t][r];
+    }
+#pragma unroll
+    for (int i = b0 + 16; i < kC; ++i) x[i] = x[i] - wl[(i - b0 - 16) * 64 + l];
   }
   // u and w through LDS (the q/k/v/L tiles are dead after this barrier), then
   // out in the state pass's operand order with 16-byte stores
