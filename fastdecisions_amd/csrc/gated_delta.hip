@@ -77,6 +77,13 @@ struct GdArgs {
   int varlen, seq_len, nct;  // packed requests (table) or a padded batch of nct chunks per sequence
   int beta_f32, l2norm;
   float scale;
+  // optional gated RMSNorm epilogue of the output pass (transformers Qwen3_5RMSNormGated):
+  // gate of token row r, head h at z + r * z_ts + h * z_hs; null z = plain output
+  const uint16_t* z;
+  int64_t z_ts, z_hs;
+  const void* nw;  // [128] norm weight, bf16 or fp32 (nw_f32)
+  int nw_f32;
+  float norm_eps;
 };
 
 // round to bf16 and back (v_cvt_pk_bf16_f32, round to nearest even)
@@ -94,13 +101,6 @@ __device__ __forceinline__ f32x4_t mfma_bf16(uint4 a, uint4 b, f32x4_t c) {
 // x == hi + mid + lo exactly (each a bf16; the two differences are exact in fp32),
 // so a product with a bf16 value is three exact bf16 products accumulated in fp32.
 // The conversions are v_cvt_pk_bf16_f32 (round to nearest even).
-__device__ __forceinline__ void split3(float x, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
-  hi = fd_pack2(x, 0.0f) & 0xffffu;
-  const float r1 = x - fd_bf16_to_f32(hi);
-  mid = fd_pack2(r1, 0.0f) & 0xffffu;
-  lo = fd_pack2(r1 - fd_bf16_to_f32(mid), 0.0f) & 0xffffu;
-}
-
 // four fp32 values -> three planes of four bf16 each (8 bytes per plane)
 __device__ __forceinline__ void split3x4(const float* x, uint2& hi, uint2& mid, uint2& lo) {
   const uint32_t h01 = fd_pack2(x[0], x[1]), h23 = fd_pack2(x[2], x[3]);
@@ -681,6 +681,7 @@ __global__ __launch_bounds__(kThreads) void gd_out_kernel(GdArgs a) {
 
   __shared__ __attribute__((aligned(16))) uint16_t sQ[kC * kRowK];
   __shared__ __attribute__((aligned(16))) float sA[kC * kRowF];
+  __shared__ __attribute__((aligned(16))) uint16_t sO[kC * kRowK];  // bf16 output rows (norm epilogue)
   __shared__ float sG[kC];
 
   const int tid = threadIdx.x;
@@ -700,6 +701,22 @@ __global__ __launch_bounds__(kThreads) void gd_out_kernel(GdArgs a) {
     *reinterpret_cast<f32x4_t*>(sA + (idx >> 6) * kRowF + (idx & 63)) = *reinterpret_cast<const f32x4_t*>(gaq + idx);
   }
   if (wv == 0) sG[l] = a.gc[hc * 3 * kC + l];  // e^{gc_t}
+  // the norm epilogue's gate rows and their silu(z) = z / (1 + exp(-z)), computed now so that the
+  // loads and the VALU work overlap the MFMA phase (16 lanes per row, row it * 16 + tid / 16;
+  // rows past the chunk's end use row L - 1)
+  float act[kC / 16][8];
+  if (a.z != nullptr) {
+#pragma unroll
+    for (int it = 0; it < kC / 16; ++it) {
+      const int t = it * 16 + (tid >> 4);
+      const int tc = t < L ? t : L - 1;
+      float zv[8];
+      unpack8(*reinterpret_cast<const uint4*>(a.z + static_cast<int64_t>(r0 + tc) * a.z_ts + h * a.z_hs +
+                                              (tid & 15) * 8), zv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) act[it][e] = zv[e] / (1.0f + expf(-zv[e]));
+    }
+  }
   __syncthreads();
 
   // bf16 MFMA over exact three-plane splits of the fp32 operands: q S takes the
@@ -757,10 +774,43 @@ __global__ __launch_bounds__(kThreads) void gd_out_kernel(GdArgs a) {
         const int t = 16 * rt + 4 * g4 + r;
         if (t < L) {
           const float val = (a.scale * sG[t]) * acc1[r] + acc2[r];
-          a.o[static_cast<size_t>(r0 + t) * o_row + h * kD + 16 * n + c16] = static_cast<uint16_t>(fd_f32_to_bf16(val));
+          const uint16_t bits = static_cast<uint16_t>(fd_pack2(val, 0.0f));
+          if (a.z != nullptr)
+            sO[t * kRowK + 16 * n + c16] = bits;
+          else
+            a.o[static_cast<size_t>(r0 + t) * o_row + h * kD + 16 * n + c16] = bits;
         }
       }
     }
+  }
+  if (a.z == nullptr) return;
+
+  // gated RMSNorm of the chunk's rows of this head, 16 lanes per row with the
+  // fd_gated_rmsnorm_fwd sequence (lane sums of 8 squares, xor butterfly 8/4/2/1):
+  //   y = bf16(x / sqrt(mean(x^2) + eps)); y2 = bf16(w y) (fp32 for an fp32 weight);
+  //   out = bf16(y2 * z / (1 + exp(-z)))
+  __syncthreads();
+  const int ln = tid & 15;
+#pragma unroll
+  for (int it = 0; it < kC / 16; ++it) {
+    const int t = it * 16 + (tid >> 4);
+    const int tc = t < L ? t : L - 1;  // rows past the chunk's end compute on row L - 1 and store nothing
+    float xv[8], y[8];
+    unpack8(*reinterpret_cast<const uint4*>(sO + tc * kRowK + ln * 8), xv);
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s = s + xv[e] * xv[e];
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) s = s + __shfl_xor(s, off);
+    const float inv = 1.0f / __builtin_sqrtf(s / static_cast<float>(kD) + a.norm_eps);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float yn = bf16r(xv[e] * inv);
+      const float gw = a.nw_f32 ? static_cast<const float*>(a.nw)[ln * 8 + e] * yn
+                                : bf16r(fd_bf16_to_f32(static_cast<const uint16_t*>(a.nw)[ln * 8 + e]) * yn);
+      y[e] = gw * act[it][e];
+    }
+    if (t < L) *reinterpret_cast<uint4*>(a.o + static_cast<size_t>(r0 + t) * o_row + h * kD + ln * 8) = pack8(y);
   }
 }
 
@@ -825,12 +875,20 @@ extern "C" FD_API int64_t fd_gated_delta_workspace_bytes(int batch, int seq_len,
   return static_cast<int64_t>(gd_layout(nc, v_heads, nseq).total);
 }
 
-extern "C" FD_API int fd_gated_delta_fwd(const void* q, const void* k, const void* v, const float* g,
-                                         const void* beta, void* out, const float* initial_state,
-                                         float* final_state, void* workspace, int64_t workspace_bytes, int batch,
-                                         int seq_len, int k_heads, int v_heads, int head_k_dim, int head_v_dim,
-                                         float scale, int beta_dtype, int l2norm_qk, const int32_t* cu_seqlens,
-                                         int n_seqs, void* stream) {
+namespace {
+
+struct GdNorm {
+  const void* z;
+  int64_t z_ts, z_hs;
+  const void* w;
+  int w_dtype;
+  float eps;
+};
+
+int gd_run(const void* q, const void* k, const void* v, const float* g, const void* beta, void* out,
+           const float* initial_state, float* final_state, void* workspace, int64_t workspace_bytes, int batch,
+           int seq_len, int k_heads, int v_heads, int head_k_dim, int head_v_dim, float scale, int beta_dtype,
+           int l2norm_qk, const int32_t* cu_seqlens, int n_seqs, void* stream, const GdNorm* norm) {
   FD_REQUIRE(q && k && v && g && beta && out && workspace, FD_ERR_INVALID_ARGUMENT,
              "fd_gated_delta_fwd: q, k, v, g, beta, out and workspace must be non-null");
   FD_REQUIRE(k_heads > 0 && v_heads > 0 && v_heads % k_heads == 0, FD_ERR_INVALID_ARGUMENT,
@@ -893,6 +951,12 @@ extern "C" FD_API int fd_gated_delta_fwd(const void* q, const void* k, const voi
   a.beta_f32 = beta_dtype == FD_DTYPE_F32;
   a.l2norm = l2norm_qk != 0;
   a.scale = scale;
+  a.z = norm ? static_cast<const uint16_t*>(norm->z) : nullptr;
+  a.z_ts = norm ? norm->z_ts : 0;
+  a.z_hs = norm ? norm->z_hs : 0;
+  a.nw = norm ? norm->w : nullptr;
+  a.nw_f32 = norm ? norm->w_dtype == FD_DTYPE_F32 : 0;
+  a.norm_eps = norm ? norm->eps : 0.0f;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int total = batch * seq_len;
@@ -906,4 +970,42 @@ extern "C" FD_API int fd_gated_delta_fwd(const void* q, const void* k, const voi
     hipLaunchKernelGGL(gd_out_kernel, dim3(static_cast<unsigned>(nc * v_heads)), dim3(kThreads), 0, s, a);
   }
   return fd_check_launch("fd_gated_delta_fwd");
+}
+
+}  // namespace
+
+extern "C" FD_API int fd_gated_delta_fwd(const void* q, const void* k, const void* v, const float* g,
+                                         const void* beta, void* out, const float* initial_state,
+                                         float* final_state, void* workspace, int64_t workspace_bytes, int batch,
+                                         int seq_len, int k_heads, int v_heads, int head_k_dim, int head_v_dim,
+                                         float scale, int beta_dtype, int l2norm_qk, const int32_t* cu_seqlens,
+                                         int n_seqs, void* stream) {
+  return gd_run(q, k, v, g, beta, out, initial_state, final_state, workspace, workspace_bytes, batch, seq_len,
+                k_heads, v_heads, head_k_dim, head_v_dim, scale, beta_dtype, l2norm_qk, cu_seqlens, n_seqs, stream,
+                nullptr);
+}
+
+extern "C" FD_API int fd_gated_delta_norm_fwd(const void* q, const void* k, const void* v, const float* g,
+                                              const void* beta, const void* z, int64_t z_token_stride,
+                                              int64_t z_head_stride, const void* norm_weight, int norm_weight_dtype,
+                                              float norm_eps, void* out, const float* initial_state,
+                                              float* final_state, void* workspace, int64_t workspace_bytes,
+                                              int batch, int seq_len, int k_heads, int v_heads, int head_k_dim,
+                                              int head_v_dim, float scale, int beta_dtype, int l2norm_qk,
+                                              const int32_t* cu_seqlens, int n_seqs, void* stream) {
+  FD_REQUIRE(z && norm_weight, FD_ERR_INVALID_ARGUMENT, "fd_gated_delta_norm_fwd: z and norm_weight must be non-null");
+  FD_REQUIRE(norm_weight_dtype == FD_DTYPE_BF16 || norm_weight_dtype == FD_DTYPE_F32, FD_ERR_INVALID_ARGUMENT,
+             "fd_gated_delta_norm_fwd: norm_weight_dtype must be FD_DTYPE_BF16 or FD_DTYPE_F32");
+  FD_REQUIRE(norm_eps >= 0.0f, FD_ERR_INVALID_ARGUMENT, "fd_gated_delta_norm_fwd: norm_eps must be >= 0");
+  FD_REQUIRE(fd_aligned16(z) && z_token_stride % 8 == 0 && z_head_stride % 8 == 0 && z_head_stride >= kD &&
+                 z_token_stride >= static_cast<int64_t>(v_heads) * z_head_stride,
+             FD_ERR_ALIGNMENT,
+             "fd_gated_delta_norm_fwd: z must be 16-byte aligned with strides that are multiples of 8 covering "
+             "[v_heads, 128]");
+  FD_REQUIRE((reinterpret_cast<uintptr_t>(norm_weight) & (norm_weight_dtype == FD_DTYPE_F32 ? 3u : 1u)) == 0,
+             FD_ERR_ALIGNMENT, "fd_gated_delta_norm_fwd: norm_weight must be aligned to its element size");
+  const GdNorm norm{z, z_token_stride, z_head_stride, norm_weight, norm_weight_dtype, norm_eps};
+  return gd_run(q, k, v, g, beta, out, initial_state, final_state, workspace, workspace_bytes, batch, seq_len,
+                k_heads, v_heads, head_k_dim, head_v_dim, scale, beta_dtype, l2norm_qk, cu_seqlens, n_seqs, stream,
+                &norm);
 }

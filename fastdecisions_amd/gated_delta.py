@@ -29,6 +29,22 @@ def _gated_delta_rule_fake(q, k, v, g, beta, cu_seqlens):
     return v.new_empty(v.shape)
 
 
+@torch.library.custom_op("fastdecisions::gated_delta_rule_norm", mutates_args=(), device_types="cuda")
+def gated_delta_rule_norm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
+                          z: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                          cu_seqlens: Optional[torch.Tensor]) -> torch.Tensor:
+    """The delta rule followed by the layer's gated RMSNorm in the same output pass
+    (``self.norm(core_attn_out, z)``, ref: src/decider/packed_conv.py:60-61)."""
+    out, _ = chunk_gated_delta_rule(q, k, v, g, beta, use_qk_l2norm_in_kernel=True, cu_seqlens=cu_seqlens,
+                                    norm=(z, norm_weight, eps))
+    return out
+
+
+@gated_delta_rule_norm.register_fake
+def _gated_delta_rule_norm_fake(q, k, v, g, beta, z, norm_weight, eps, cu_seqlens):
+    return v.new_empty(v.shape)
+
+
 def install_gated_delta_rule(core) -> int:
     """Run every Gated-DeltaNet layer's delta rule on the HIP kernels; return the count."""
     from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5GatedDeltaNet

@@ -15,7 +15,12 @@ Differences a caller can see:
 * key heads may divide the value heads (value head h reads key head
   h // (Hv / Hk)), so the caller's ``repeat_interleave`` is not needed;
 * head dims must be 128 and ``chunk_size`` 64 (the decider's geometry); q/k/v
-  must be bf16, g fp32, beta bf16 or fp32; the output is bf16.
+  must be bf16, g fp32, beta bf16 or fp32; the output is bf16;
+* ``norm=(z, weight, eps)`` applies the layer's gated RMSNorm
+  (transformers ``Qwen3_5RMSNormGated``, the call after the delta rule at
+  ref: src/decider/packed_conv.py:60-61) inside the output pass
+  (``fd_gated_delta_norm_fwd``): the result equals ``gated_rms_norm`` of the
+  plain output, bit for bit; z is a ``[B, T, Hv, Dv]`` bf16 view.
 """
 from __future__ import annotations
 
@@ -45,6 +50,7 @@ def chunk_gated_delta_rule(
     *,
     scale: float | None = None,
     cu_seqlens: torch.Tensor | None = None,
+    norm: tuple | None = None,
     **kwargs,
 ):
     if not value.is_cuda:
@@ -92,15 +98,42 @@ def chunk_gated_delta_rule(
     if scale is None:
         scale = 1.0 / Dk ** 0.5
 
+    norm_args = None
+    if norm is not None:
+        z, norm_weight, norm_eps = norm
+        norm_args = _norm_args(z, norm_weight, B, T, Hv, Dv, value.device)
     with torch.cuda.device(value.device):
         out = torch.empty((B, T, Hv, Dv), device=value.device, dtype=torch.bfloat16)
         final = torch.empty(state_shape, device=value.device, dtype=torch.float32) if output_final_state else None
         nbytes = workspace_bytes(B, T, Hv, n_seqs)
         work = torch.empty(max(nbytes, 16), device=value.device, dtype=torch.uint8)
         beta_dtype = _lib.FD_DTYPE_F32 if beta.dtype == torch.float32 else _lib.FD_DTYPE_BF16
-        _lib.check("fd_gated_delta_fwd", _lib.lib().fd_gated_delta_fwd(
-            query.data_ptr(), key.data_ptr(), value.data_ptr(), g.data_ptr(), beta.data_ptr(), out.data_ptr(),
-            _lib.ptr(initial_state), _lib.ptr(final), work.data_ptr(), nbytes,
-            B, T, Hk, Hv, Dk, Dv, float(scale), beta_dtype, int(bool(use_qk_l2norm_in_kernel)),
-            cu_ptr, n_seqs, _lib.stream_handle(value.device)))
+        tail = (_lib.ptr(initial_state), _lib.ptr(final), work.data_ptr(), nbytes,
+                B, T, Hk, Hv, Dk, Dv, float(scale), beta_dtype, int(bool(use_qk_l2norm_in_kernel)),
+                cu_ptr, n_seqs, _lib.stream_handle(value.device))
+        if norm_args is None:
+            _lib.check("fd_gated_delta_fwd", _lib.lib().fd_gated_delta_fwd(
+                query.data_ptr(), key.data_ptr(), value.data_ptr(), g.data_ptr(), beta.data_ptr(), out.data_ptr(),
+                *tail))
+        else:
+            _lib.check("fd_gated_delta_norm_fwd", _lib.lib().fd_gated_delta_norm_fwd(
+                query.data_ptr(), key.data_ptr(), value.data_ptr(), g.data_ptr(), beta.data_ptr(), *norm_args,
+                float(norm_eps), out.data_ptr(), *tail))
     return out, final
+
+
+_NORM_W_DTYPES = {torch.bfloat16: _lib.FD_DTYPE_BF16, torch.float32: _lib.FD_DTYPE_F32}
+
+
+def _norm_args(z: torch.Tensor, weight: torch.Tensor, B: int, T: int, Hv: int, Dv: int, device):
+    """(z pointer, token stride, head stride, weight pointer, weight dtype) for the gated-norm epilogue;
+    z is a [B, T, Hv, Dv] bf16 view with unit feature stride and uniformly strided tokens."""
+    if z.shape != (B, T, Hv, Dv) or z.dtype != torch.bfloat16 or z.device != device:
+        raise ValueError(f"z must be a BF16 [{B}, {T}, {Hv}, {Dv}] tensor on value's device")
+    ts, hs = z.stride(1), z.stride(2)
+    if z.stride(3) != 1 or (B > 1 and z.stride(0) != T * ts) or ts % 8 or hs % 8 or z.data_ptr() % 16:
+        raise ValueError("z rows must be contiguous, 16-byte aligned and uniformly strided over tokens")
+    if weight.shape != (Dv,) or weight.dtype not in _NORM_W_DTYPES or weight.device != device \
+            or not weight.is_contiguous():
+        raise ValueError(f"the norm weight must be a contiguous BF16 or FP32 vector [{Dv}] on value's device")
+    return z.data_ptr(), ts, hs, weight.data_ptr(), _NORM_W_DTYPES[weight.dtype]

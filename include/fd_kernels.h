@@ -17,6 +17,7 @@
  *   fd_gated_delta_fwd  chunked gated delta rule of the Gated-DeltaNet layers
  *                       replaces the torch_chunk_gated_delta_rule call
  *                       (ref: src/decider/packed_conv.py:55-59)
+ *   fd_gated_delta_norm_fwd  fd_gated_delta_fwd with the layer's gated RMSNorm applied in the output pass
  *   fd_gqa_gated_fwd    fd_gqa_fwd with the attention layer's sigmoid output gate applied in the store
  *   fd_attn_prologue_fwd   q/k RMSNorm over head_dim + partial rotary embedding of the attention layers
  *                       replaces the eager prologue of the patched attention forward
@@ -54,7 +55,7 @@ extern "C" {
 #define FD_API
 #endif
 
-#define FD_ABI_VERSION 7
+#define FD_ABI_VERSION 8
 
 #define FD_OK 0
 #define FD_ERR_INVALID_ARGUMENT (-1) /* shape, size, stride or flag out of range */
@@ -242,6 +243,28 @@ FD_API int fd_gated_delta_fwd(const void* q, const void* k, const void* v, const
                               int batch, int seq_len, int k_heads, int v_heads, int head_k_dim,
                               int head_v_dim, float scale, int beta_dtype, int l2norm_qk,
                               const int32_t* cu_seqlens, int n_seqs, void* stream);
+
+/*
+ * fd_gated_delta_fwd followed by the layer's gated RMSNorm (transformers
+ * Qwen3_5RMSNormGated, the call after the delta rule at ref: src/decider/packed_conv.py:60-61),
+ * applied in the output pass to each (token, head) row of 128 before it is stored:
+ *   x = bf16(delta-rule output);  y = bf16(x / sqrt(mean(x^2) + eps));
+ *   y2 = bf16(w * y) (fp32 for an fp32 weight);  out = bf16(y2 * z / (1 + exp(-z)))
+ * the same values fd_gated_delta_fwd then fd_gated_rmsnorm_fwd produce.
+ *   z  gate of token row r (the batch's flattened token index), value head h at
+ *      z + r * z_token_stride + h * z_head_stride (bf16, 128 contiguous; e.g. part of a
+ *      combined projection output)
+ *   norm_weight [128] of norm_weight_dtype (FD_DTYPE_BF16 or FD_DTYPE_F32)
+ * Other arguments and limits as fd_gated_delta_fwd; z strides multiples of 8 elements.
+ */
+FD_API int fd_gated_delta_norm_fwd(const void* q, const void* k, const void* v, const float* g,
+                                   const void* beta, const void* z, int64_t z_token_stride,
+                                   int64_t z_head_stride, const void* norm_weight, int norm_weight_dtype,
+                                   float norm_eps, void* out, const float* initial_state,
+                                   float* final_state, void* workspace, int64_t workspace_bytes,
+                                   int batch, int seq_len, int k_heads, int v_heads, int head_k_dim,
+                                   int head_v_dim, float scale, int beta_dtype, int l2norm_qk,
+                                   const int32_t* cu_seqlens, int n_seqs, void* stream);
 
 /*
  * Gate transform of the Gated-DeltaNet layers (ref: src/decider/unpack_gate_transform_kernel.py:51-91,

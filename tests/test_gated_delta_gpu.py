@@ -194,3 +194,27 @@ def test_wrapper_rejects_bad_inputs():
                                                                                           device="cuda"))
     with pytest.raises(ValueError, match="initial_state"):
         rule(q, k, v, g, beta, initial_state=torch.zeros((1, 2, 128, 64), device="cuda"))
+
+
+def test_norm_epilogue_equals_delta_rule_then_gated_norm():
+    """fd_gated_delta_norm_fwd: the gated RMSNorm applied in the output pass gives the
+    values of fd_gated_delta_fwd followed by fd_gated_rmsnorm_fwd, bit for bit (a ragged
+    tail, grouped heads, the decider shape, packed requests with an empty one, bf16 and
+    fp32 norm weights; the gate is a strided view as in the combined projection)."""
+    from fastdecisions_amd.gated_norm_kernel import gated_rms_norm
+    rule = _rule()
+    cases = ((300, 2, 4, None, torch.bfloat16), (2048, 16, 16, None, torch.bfloat16),
+             (200, 2, 2, [0, 37, 37, 150, 200], torch.float32))
+    for T, hk, hv, cu, wdtype in cases:
+        announce(f"gated delta + norm epilogue T={T} hk={hk} hv={hv} cu={cu} w={wdtype}")
+        q, k, v, g, beta = (t.cuda() for t in _inputs(T, hk, hv, seed=21))
+        gen = torch.Generator().manual_seed(5)
+        zbig = torch.randn((1, T, hv * 128 + 64), generator=gen).to(torch.bfloat16).cuda()
+        z = zbig[..., :hv * 128].view(1, T, hv, 128)
+        w = (1.0 + 0.02 * torch.randn(128, generator=gen)).to(wdtype).cuda()
+        cu_t = torch.tensor(cu, dtype=torch.int32).cuda() if cu else None
+        plain, _ = rule(q, k, v, g, beta, use_qk_l2norm_in_kernel=True, cu_seqlens=cu_t)
+        ref = gated_rms_norm(plain.reshape(-1, 128), z, w, 1e-6).reshape(plain.shape)
+        fused, _ = rule(q, k, v, g, beta, use_qk_l2norm_in_kernel=True, cu_seqlens=cu_t, norm=(z, w, 1e-6))
+        torch.cuda.synchronize()
+        assert torch.equal(fused, ref), (T, hk, hv, cu)
