@@ -27,8 +27,9 @@
 //   3. gd_state_kernel — one workgroup per (request, value head, 16 value
 //      columns): the only sequential part.  Each state column evolves on its
 //      own, so the 128 value columns split over 8 workgroups.  The state slice
-//      lives in registers; every operand of the next chunk is loaded straight
-//      into registers while the current chunk runs; two barriers per chunk.
+//      lives in registers; the operands of the chunks two ahead are loaded
+//      straight into registers (three register sets, one wavefront per SIMD)
+//      while the current chunk runs; two barriers per chunk.
 //      Its products run on bf16 MFMA over exact bf16 splits of the fp32 operands.
 //   4. gd_out_kernel — one workgroup per (chunk, value head), chunk-parallel:
 //      o = scale e^{gc} (q S_chunk) + A v', on bf16 MFMA over the same splits.
@@ -503,7 +504,7 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
 constexpr int kRowSB = kD + 8;   // bf16 row stride of a transposed state plane (272 B)
 constexpr int kRowVB = kC + 8;   // bf16 row stride of a transposed v' plane (144 B)
 
-__global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gd_state_kernel(GdArgs a) {
   // XCD-aware order: block b runs on XCD b % 8; the logical index below gives
   // each XCD a contiguous range, so the 8 column slices of one head (which read
   // the same w / k tiles) share one L2.  The grid is a multiple of 8.
@@ -648,14 +649,20 @@ __global__ __launch_bounds__(kThreads) void gd_state_kernel(GdArgs a) {
   };
 
   if (first < last) {
-    ChunkRegs A, B;
+    // three register sets, loads two chunks ahead of the step that uses them
+    ChunkRegs A, B, Cr;
     load_chunk(A, first);
-    for (int c = first; c < last; c += 2) {
-      load_chunk(B, c + 1);
+    load_chunk(B, first + 1);
+    for (int c = first; c < last; c += 3) {
+      load_chunk(Cr, c + 2);
       step(A, c);
       if (c + 1 < last) {
-        load_chunk(A, c + 2);
+        load_chunk(A, c + 3);
         step(B, c + 1);
+      }
+      if (c + 2 < last) {
+        load_chunk(B, c + 4);
+        step(Cr, c + 2);
       }
     }
   }
