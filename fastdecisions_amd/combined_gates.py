@@ -68,16 +68,21 @@ def install_combined_gates(core) -> int:
 
 
 def install_combined_projections(core) -> int:
-    """One GEMM for in_proj_qkv | in_proj_z | in_proj_a | in_proj_b of every
-    Gated-DeltaNet layer (a non-persistent buffer; reinvoke after changing weights)."""
+    """One GEMM for in_proj_qkv | in_proj_z of every Gated-DeltaNet layer, and one
+    narrow GEMM for in_proj_a | in_proj_b (non-persistent buffers; reinvoke after
+    changing weights).
+
+    The a|b rows stay out of the wide GEMM: at the decider's shapes the 32 extra
+    output columns cost hipBLASLt a partial column of 256-wide tiles and a worse
+    tiling (M=2048, K=2048 measured on MI355X: N=8224 79.6 us, N=8192 55.3 us, the
+    separate N=32 GEMM 6.1 us)."""
     from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5GatedDeltaNet
-    from .packed_conv import install_packed_conv
-    install_packed_conv(core)
+    install_combined_gates(core)
     count = 0
     for module in core.modules():
         if isinstance(module, Qwen3_5GatedDeltaNet):
-            projs = (module.in_proj_qkv, module.in_proj_z, module.in_proj_a, module.in_proj_b)
-            if any(p.bias is not None for p in projs):
+            projs = (module.in_proj_qkv, module.in_proj_z)
+            if any(p.bias is not None for p in projs) or not hasattr(module, "_combined_gate_weight"):
                 continue
             with torch.no_grad():
                 weight = torch.cat([p.weight for p in projs], dim=0).detach()

@@ -78,7 +78,7 @@ def _forward(self, hidden_states, cache_params=None, attention_mask=None, **kwar
     batch, seq, _ = hidden_states.shape
     combined = hasattr(self, "_fd_in_proj_weight")
     if combined:
-        # q|k|v, z, a, b from one GEMM, read below as strided views
+        # q|k|v and z from one GEMM, read below as strided views; a|b from its own
         proj = F.linear(hidden_states, self._fd_in_proj_weight)
         c0 = 2 * self.key_dim + self.value_dim
         c1 = c0 + self.value_dim
@@ -91,10 +91,10 @@ def _forward(self, hidden_states, cache_params=None, attention_mask=None, **kwar
     else:
         query, key, value = packed_conv(mixed, self.conv1d.weight)
     if combined:
-        from .combined_gates import gate_transform_op
+        from .combined_gates import unpack_gate_op
         z = proj[..., c0:c1].view(batch, seq, -1, self.head_v_dim)
-        h = self.num_v_heads
-        g, beta = gate_transform_op(proj[..., c1:c1 + h], proj[..., c1 + h:c1 + 2 * h], self.A_log, self.dt_bias)
+        ab = F.linear(hidden_states, self._combined_gate_weight)
+        g, beta = unpack_gate_op(ab, self.A_log, self.dt_bias)
     elif hasattr(self, "_combined_gate_weight"):
         z = self.in_proj_z(hidden_states).reshape(batch, seq, -1, self.head_v_dim)
         # one GEMM for both gate projections, one kernel for both transforms (ref: :45-48)
