@@ -18,7 +18,7 @@ from __future__ import annotations
 
 import torch
 
-from .unpack_gate_transform_kernel import gate_transform, unpack_gate
+from .unpack_gate_transform_kernel import gate_projection, gate_transform, unpack_gate
 
 
 @torch.library.custom_op("fastdecisions::gate_transform", mutates_args=(), device_types="cuda")
@@ -30,6 +30,18 @@ def gate_transform_op(a: torch.Tensor, b: torch.Tensor, a_log: torch.Tensor,
 @gate_transform_op.register_fake
 def _gate_transform_fake(a, b, a_log, dt_bias):
     return (a.new_empty(a.shape, dtype=torch.float32), a.new_empty(a.shape, dtype=torch.bfloat16))
+
+
+@torch.library.custom_op("fastdecisions::gate_proj", mutates_args=(), device_types="cuda")
+def gate_proj_op(x: torch.Tensor, weight: torch.Tensor, a_log: torch.Tensor,
+                 dt_bias: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    return gate_projection(x, weight, a_log, dt_bias)
+
+
+@gate_proj_op.register_fake
+def _gate_proj_fake(x, weight, a_log, dt_bias):
+    shape = (*x.shape[:-1], weight.shape[0] // 2)
+    return (x.new_empty(shape, dtype=torch.float32), x.new_empty(shape, dtype=torch.bfloat16))
 
 
 @torch.library.custom_op("fastdecisions::unpack_gate", mutates_args=(), device_types="cuda")

@@ -14,9 +14,13 @@
 //   at the end).  Two wavefronts per SIMD let one run softmax VALU work while
 //   the other issues MFMAs.  head_dim 256 runs 4 wavefronts (register budget).
 // * K and V tiles (64 keys) are copied global -> LDS with global_load_lds
-//   (no staging registers, no VALU) into a ring of 3 stages (2 for
-//   head_dim 256, whose 3 stages would not fit the 160 KiB LDS), one barrier
-//   per tile.
+//   (no staging registers, no VALU), one barrier per tile.  For head_dim
+//   <= 128 the ring has 4 stages and the loop is software-pipelined: while a
+//   wavefront finishes tile t (mask, softmax, P·V), the scores of tile t+1
+//   are computed, one MFMA of that dependent chain after each of eight pieces
+//   of the softmax, so the VALU work issues while the MFMAs run; tiles t+2 and
+//   t+3 are in flight.  head_dim 256 (whose 4 stages would not fit the
+//   160 KiB LDS) runs tile by tile over 2 stages.
 //   16-byte chunks are XOR-swizzled per row so that the MFMA operand reads
 //   below are bank-conflict free.
 // * The score tile is computed transposed, S^T = K · Q^T, with
@@ -85,9 +89,12 @@ struct Cfg {
   static constexpr int kTileBytes = kBlockN * kChunksRow * 16;
   static constexpr int kLoads = kBlockN * kChunksRow / kThreads;  // global_load_lds per thread per K (or V) tile
   static constexpr int kStageBytes = 2 * kTileBytes;         // K tile + V tile
-  // LDS ring depth: tile t+2 is in flight while tile t is consumed (3 stages
-  // where they fit next to the merge area, else 2)
-  static constexpr int kStages = 3 * kStageBytes <= 160 * 1024 ? 3 : 2;
+  // Pipelined loop (two wavefronts per (head, query block) and 4 stages in
+  // LDS): the scores of tile t+1 are computed while tile t is finished, and
+  // tiles t+2, t+3 are in flight.  Otherwise a ring of 3 stages where they fit
+  // next to the merge area (tile t+2 in flight while tile t is consumed), else 2.
+  static constexpr bool kPipe = KSPLIT > 1 && 4 * kStageBytes <= 160 * 1024;
+  static constexpr int kStages = kPipe ? 4 : 3 * kStageBytes <= 160 * 1024 ? 3 : 2;
   static constexpr int kCombineBytes = KSPLIT > 1 ? 4 * 64 * (D / 2 + 2) * 4 : 0;
   static constexpr int kSmemBytes =
       (kStages * kStageBytes > kCombineBytes) ? kStages * kStageBytes : kCombineBytes;
@@ -293,30 +300,11 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
   float m_run = -__builtin_inff();  // running max (log2-scaled units), may lag the true max by <= 8
   float l_run = 0.0f;               // this lane's partial denominator
 
-  // Prologue: tiles 0 (and 1) in flight; wait for tile 0 only.  Each
-  // issue_tile is 2*kLoads VMEM instructions per thread.
-  constexpr int kPerTile = 2 * C::kLoads;
-  constexpr int kAhead = C::kStages - 1;  // prefetch distance in tiles
-  issue_tile(0, 0);
-  if (C::kStages == 3 && ntiles > 1) {
-    issue_tile(1, 1);
-    __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(kPerTile));
-  } else {
-    __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(0));
-  }
-  __syncthreads();
+  constexpr int kPerTile = 2 * C::kLoads;  // VMEM instructions per thread of one issue_tile
 
-  // One 64-key tile in LDS stage BUF (a constant after inlining where the loop
-  // is unrolled by the stage count).
-  auto tile_step = [&](int t, int BUF) {
-    const bool issued = t + kAhead < ntiles;
-    if (issued) issue_tile(t + kAhead, (BUF + kAhead) % C::kStages);
+  // S^T for this wavefront's 32-key block(s) of the tile in LDS stage BUF
+  auto scores = [&](int BUF, f32x16_t (&s)[C::kBlocks]) {
     const unsigned char* kt = k_lds + BUF * C::kTileBytes;
-    const unsigned char* vt = v_lds + BUF * C::kTileBytes;
-    const int ks0 = seq_start + t * kBlockN;
-
-    // S^T for this wavefront's 32-key block(s) of the tile
-    f32x16_t s[C::kBlocks];
 #pragma unroll
     for (int bl = 0; bl < C::kBlocks; ++bl) {
       s[bl] = f32x16_t{};
@@ -331,9 +319,13 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
           s[bl] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kk], qf[k0 + kk], s[bl], 0, 0, 0);
       }
     }
+  };
 
-    // causal / end-of-sequence mask on diagonal and tail tiles only
-    const int kb0 = ks0 + kh * C::kBlocks * 32;  // first key of this wavefront's part
+  // Mask and online softmax of tile t (scores s): P as bf16 MFMA operands in pb,
+  // the running max / denominator updated; returns the O rescale factor.
+  // causal / end-of-sequence mask of tile t, on diagonal and tail tiles only
+  auto mask = [&](int t, f32x16_t (&s)[C::kBlocks]) {
+    const int kb0 = seq_start + t * kBlockN + kh * C::kBlocks * 32;  // first key of this wavefront's part
     if (kb0 + C::kBlocks * 32 - 1 > qw0 || kb0 + C::kBlocks * 32 > seq_end) {
 #pragma unroll
       for (int bl = 0; bl < C::kBlocks; ++bl)
@@ -343,8 +335,11 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
           if (key > qpos || key >= seq_end) s[bl][r] = -__builtin_inff();
         }
     }
+  };
 
-    // online softmax (exp2 domain, lazily raised max)
+  auto softmax = [&](int t, f32x16_t (&s)[C::kBlocks], bf16x8_t (&pb)[2 * C::kBlocks], bool& grow_any) {
+    mask(t, s);
+    // exp2 domain, lazily raised max
     float mx = -__builtin_inff();
 #pragma unroll
     for (int bl = 0; bl < C::kBlocks; ++bl)
@@ -357,7 +352,6 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
     const float m_sub = (m_new == -__builtin_inff()) ? 0.0f : m_new;  // fully masked so far: p = 0
     m_run = m_new;
     float psum = 0.0f;
-    bf16x8_t pb[2 * C::kBlocks];
 #pragma unroll
     for (int bl = 0; bl < C::kBlocks; ++bl) {
 #pragma unroll
@@ -373,13 +367,19 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
       }
     }
     l_run = l_run * alpha + psum;
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+    grow_any = __builtin_amdgcn_ballot_w64(grow) != 0;
+    return alpha;
+  };
+
+  // O = alpha O + V^T · P^T with V in stage BUF: the V^T A operand of each
+  // 16-key slice comes from two transposing reads of the row-major V tile
+  // (keys +0..3 and +4..7)
+  auto accumulate = [&](int BUF, const bf16x8_t (&pb)[2 * C::kBlocks], float alpha, bool grow_any) {
+    const unsigned char* vt = v_lds + BUF * C::kTileBytes;
+    if (grow_any) {
 #pragma unroll
       for (int db = 0; db < D / 32; ++db) o[db] *= alpha;
     }
-
-    // O^T += V^T · P^T: the V^T A operand of each 16-key slice comes from two
-    // transposing reads of the row-major V tile (keys +0..3 and +4..7)
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
@@ -390,26 +390,146 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vv), pb[cs], o[db], 0, 0, 0);
       }
     }
-    // tile t+1 must have landed (only tile t+kAhead may still be in flight);
-    // the barrier makes every thread's copies visible and frees stage BUF
-    if (C::kStages == 3 && issued)
-      __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(kPerTile));
-    else
-      __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(0));
-    __syncthreads();
   };
 
-  if constexpr (C::kStages == 3) {
-    int t = 0;
-    for (; t + 3 <= ntiles; t += 3) {
-      tile_step(t, 0);
-      tile_step(t + 1, 1);
-      tile_step(t + 2, 2);
+  if constexpr (C::kPipe) {
+    // Prologue: tiles 0..2 in flight, wait for tiles 0 and 1, scores of tile 0.
+    issue_tile(0, 0);
+    if (ntiles > 1) issue_tile(1, 1);
+    if (ntiles > 2) {
+      issue_tile(2, 2);
+      __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(kPerTile));
+    } else {
+      __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(0));
     }
-    if (t < ntiles) tile_step(t, 0);
-    if (t + 1 < ntiles) tile_step(t + 1, 1);
+    __syncthreads();
+    f32x16_t sA[C::kBlocks], sB[C::kBlocks];
+    scores(0, sA);
+
+    // Step t (stage BUF = t % 4): tile t+3 is issued into the stage tile t-1
+    // left (every wavefront passed the previous step's barrier); the softmax
+    // of tile t and the scores of tile t+1 (complete since the previous step)
+    // are independent, so their VALU and MFMA work can interleave.  At the
+    // end only tile t+3 may still be in flight: tile t+2, which the next
+    // step's scores read, has landed, and the barrier makes it visible.  The
+    // last step's scores read a stale stage and are discarded.
+    auto step = [&](int t, int BUF, f32x16_t (&sc)[C::kBlocks], f32x16_t (&sn)[C::kBlocks]) {
+      static_assert(C::kBlocks == 1, "the pipelined step takes one 32-key block per wavefront");
+      const bool issued = t + 3 < ntiles;
+      if (issued) issue_tile(t + 3, (BUF + 3) & 3);
+      mask(t, sc);
+      // The next tile's scores are a chain of D/16 dependent MFMAs; after each
+      // one the wavefront issues one piece of this tile's softmax (8 pieces),
+      // which runs while the MFMA does.  sched_barrier keeps the pieces apart.
+      constexpr int kSteps = D / 16;
+      constexpr int kPer = 8 / kSteps;  // softmax pieces per MFMA
+      const unsigned char* ktn = k_lds + ((BUF + 1) & 3) * C::kTileBytes;
+      float mx = -__builtin_inff(), alpha = 1.0f, m_sub = 0.0f, psum = 0.0f;
+      bool grow = false;
+      f32x8_t pv[2];
+      bf16x8_t pb[2];
+      auto piece = [&](int k) {
+        if (k == 0) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[0][r]);
+        } else if (k == 1) {
+          mx = half_max(mx) * c;
+          grow = mx > m_run + 8.0f;
+          const float m_new = grow ? mx : m_run;
+          alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+          m_sub = (m_new == -__builtin_inff()) ? 0.0f : m_new;  // fully masked so far: p = 0
+          m_run = m_new;
+        } else if (k < 6) {
+          const int r0 = 4 * (k - 2);  // scores r0 .. r0 + 3
+#pragma unroll
+          for (int r = r0; r < r0 + 4; ++r) {
+            float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[0][r], c, -m_sub));
+            asm volatile("" : "+v"(p));  // computed here, not sunk towards its use in P·V
+            psum += p;
+            pv[r >> 3][r & 7] = p;
+          }
+        } else if (k == 6) {
+          pb[0] = __builtin_convertvector(pv[0], bf16x8_t);
+          pb[1] = __builtin_convertvector(pv[1], bf16x8_t);
+          asm volatile("" : "+v"(pb[0]), "+v"(pb[1]));
+        } else {
+          l_run = l_run * alpha + psum;
+          asm volatile("" : "+v"(l_run));
+        }
+      };
+      sn[0] = f32x16_t{};
+      bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(ktn + k_off(0, 0));
+#pragma unroll
+      for (int kk = 0; kk < kSteps; ++kk) {
+        bf16x8_t kn = kf;
+        if (kk + 1 < kSteps) kn = *reinterpret_cast<const bf16x8_t*>(ktn + k_off(0, kk + 1));
+        sn[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sn[0], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) piece(kk * kPer + j);
+        __builtin_amdgcn_sched_barrier(0);
+        kf = kn;
+      }
+      const bool grow_any = __builtin_amdgcn_ballot_w64(grow) != 0;
+      accumulate(BUF, pb, alpha, grow_any);
+      if (issued)
+        __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(kPerTile));
+      else
+        __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(0));
+      __syncthreads();
+    };
+    int t = 0;
+    for (; t + 4 <= ntiles; t += 4) {
+      step(t, 0, sA, sB);
+      step(t + 1, 1, sB, sA);
+      step(t + 2, 2, sA, sB);
+      step(t + 3, 3, sB, sA);
+    }
+    if (t < ntiles) step(t, 0, sA, sB);
+    if (t + 1 < ntiles) step(t + 1, 1, sB, sA);
+    if (t + 2 < ntiles) step(t + 2, 2, sA, sB);
   } else {
-    for (int t = 0; t < ntiles; ++t) tile_step(t, t & 1);
+    // Prologue: tiles 0 (and 1) in flight; wait for tile 0 only.
+    constexpr int kAhead = C::kStages - 1;  // prefetch distance in tiles
+    issue_tile(0, 0);
+    if (C::kStages == 3 && ntiles > 1) {
+      issue_tile(1, 1);
+      __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(kPerTile));
+    } else {
+      __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(0));
+    }
+    __syncthreads();
+
+    // One 64-key tile in LDS stage BUF (a constant after inlining where the
+    // loop is unrolled by the stage count).
+    auto tile_step = [&](int t, int BUF) {
+      const bool issued = t + kAhead < ntiles;
+      if (issued) issue_tile(t + kAhead, (BUF + kAhead) % C::kStages);
+      f32x16_t s[C::kBlocks];
+      scores(BUF, s);
+      bf16x8_t pb[2 * C::kBlocks];
+      bool grow_any;
+      const float alpha = softmax(t, s, pb, grow_any);
+      accumulate(BUF, pb, alpha, grow_any);
+      // tile t+1 must have landed (only tile t+kAhead may still be in flight);
+      // the barrier makes every thread's copies visible and frees stage BUF
+      if (C::kStages == 3 && issued)
+        __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(kPerTile));
+      else
+        __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(0));
+      __syncthreads();
+    };
+    if constexpr (C::kStages == 3) {
+      int t = 0;
+      for (; t + 3 <= ntiles; t += 3) {
+        tile_step(t, 0);
+        tile_step(t + 1, 1);
+        tile_step(t + 2, 2);
+      }
+      if (t < ntiles) tile_step(t, 0);
+      if (t + 1 < ntiles) tile_step(t + 1, 1);
+    } else {
+      for (int t = 0; t < ntiles; ++t) tile_step(t, t & 1);
+    }
   }
 
   // ---- merge the key parts of each (head, query block), then normalise and store

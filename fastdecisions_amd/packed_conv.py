@@ -61,6 +61,12 @@ def _segments(kwargs):
     return None if bounds is None else list(bounds)
 
 
+def _gate_proj_fits(self, hidden_states) -> bool:
+    """Sizes the fused a|b projection + gate transform kernel takes."""
+    return (self.num_v_heads in (8, 16, 24, 32) and hidden_states.shape[-1] % 1024 == 0
+            and hidden_states.stride(-1) == 1 and hidden_states.is_contiguous())
+
+
 def _forward(self, hidden_states, cache_params=None, attention_mask=None, **kwargs):
     # The original method owns caches, training and other geometries (ref: src/decider/packed_conv.py:25-38).
     if (cache_params is not None or self.training or torch.is_grad_enabled()
@@ -91,10 +97,15 @@ def _forward(self, hidden_states, cache_params=None, attention_mask=None, **kwar
     else:
         query, key, value = packed_conv(mixed, self.conv1d.weight)
     if combined:
-        from .combined_gates import unpack_gate_op
         z = proj[..., c0:c1].view(batch, seq, -1, self.head_v_dim)
-        ab = F.linear(hidden_states, self._combined_gate_weight)
-        g, beta = unpack_gate_op(ab, self.A_log, self.dt_bias)
+        if _gate_proj_fits(self, hidden_states):
+            # the a|b projection and the gate transform in one kernel
+            from .combined_gates import gate_proj_op
+            g, beta = gate_proj_op(hidden_states, self._combined_gate_weight, self.A_log, self.dt_bias)
+        else:
+            from .combined_gates import unpack_gate_op
+            ab = F.linear(hidden_states, self._combined_gate_weight)
+            g, beta = unpack_gate_op(ab, self.A_log, self.dt_bias)
     elif hasattr(self, "_combined_gate_weight"):
         z = self.in_proj_z(hidden_states).reshape(batch, seq, -1, self.head_v_dim)
         # one GEMM for both gate projections, one kernel for both transforms (ref: :45-48)

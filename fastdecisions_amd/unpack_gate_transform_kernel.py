@@ -10,6 +10,12 @@ reference fixes H = 16; any H works here.
 
 ``gate_transform(a, b, a_log, dt_bias)`` takes the two projections separately
 (any row-contiguous ``[B, T, H]`` views, e.g. of one combined tensor).
+
+``gate_projection(x, weight, a_log, dt_bias)`` also does the combined a|b
+projection itself (``fd_gate_proj_fwd``): ``weight`` is
+``cat(in_proj_a.weight, in_proj_b.weight)`` ``[2H, hidden]`` and ``x`` the
+layer input ``[B, T, hidden]``, replacing the reference's separate GEMM and
+transform (ref: src/decider/combined_gates.py:19-43).
 """
 from __future__ import annotations
 
@@ -67,3 +73,29 @@ def unpack_gate(combined: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tens
         raise ValueError("B and T must be positive")
     H = H2 // 2
     return gate_transform(combined[..., :H], combined[..., H:], a_log, dt_bias)
+
+
+def gate_projection(x: torch.Tensor, weight: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor,
+                    ab: torch.Tensor | None = None):
+    if not x.is_cuda or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or weight.device != x.device:
+        raise ValueError("x and weight must be CUDA BF16 on one device")
+    if x.ndim != 3 or weight.ndim != 2 or weight.shape[1] != x.shape[2] or weight.shape[0] % 2:
+        raise ValueError("x must be [B, T, hidden] and weight [2H, hidden]")
+    B, T, hidden = x.shape
+    H = weight.shape[0] // 2
+    if B < 1 or T < 1:
+        raise ValueError("B and T must be positive")
+    if x.stride(2) != 1 or x.stride(0) != T * x.stride(1) or not weight.is_contiguous():
+        raise ValueError("x must be row-contiguous [B, T, hidden] and weight contiguous")
+    _check_params(a_log, dt_bias, H, x.device)
+    if ab is not None and (ab.shape != (B, T, 2 * H) or ab.dtype != torch.bfloat16 or not ab.is_contiguous()
+                           or ab.device != x.device):
+        raise ValueError("ab must be a contiguous BF16 [B, T, 2H] tensor on x's device")
+    with torch.cuda.device(x.device):
+        decay = torch.empty((B, T, H), device=x.device, dtype=torch.float32)
+        beta = torch.empty((B, T, H), device=x.device, dtype=torch.bfloat16)
+        _lib.check("fd_gate_proj_fwd", _lib.lib().fd_gate_proj_fwd(
+            x.data_ptr(), x.stride(1), weight.data_ptr(), hidden, a_log.data_ptr(), _PARAM_DTYPES[a_log.dtype],
+            dt_bias.data_ptr(), _PARAM_DTYPES[dt_bias.dtype], decay.data_ptr(), beta.data_ptr(), _lib.ptr(ab),
+            B * T, H, _lib.stream_handle(x.device)))
+    return decay, beta

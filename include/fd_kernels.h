@@ -30,6 +30,9 @@
  *   fd_gate_transform_fwd  gate transform (decay g and beta) of the Gated-DeltaNet layers
  *                       replaces unpack_gate(combined, a_log, dt_bias)
  *                       (ref: src/decider/unpack_gate_transform_kernel.py:94-133, kernel :51-91)
+ *   fd_gate_proj_fwd    the combined a|b gate projection fused with the gate transform
+ *                       replaces F.linear(x, cat(W_a, W_b)) + unpack_gate
+ *                       (ref: src/decider/combined_gates.py:19-43, packed_conv.py:45-53)
  *
  * Conventions shared by every entry point:
  *   - every tensor pointer is a device pointer; bf16 tensors are passed as raw
@@ -55,7 +58,7 @@ extern "C" {
 #define FD_API
 #endif
 
-#define FD_ABI_VERSION 8
+#define FD_ABI_VERSION 9
 
 #define FD_OK 0
 #define FD_ERR_INVALID_ARGUMENT (-1) /* shape, size, stride or flag out of range */
@@ -285,6 +288,28 @@ FD_API int fd_gate_transform_fwd(const void* a, const void* b, int64_t a_row_str
                                  int64_t b_row_stride, const void* a_log, int a_log_dtype,
                                  const void* dt_bias, int dt_bias_dtype, float* g, void* beta,
                                  int64_t rows, int heads, void* stream);
+
+/*
+ * The combined a|b gate projection of a Gated-DeltaNet layer fused with the
+ * gate transform: the reference's F.linear(x, cat(in_proj_a.weight,
+ * in_proj_b.weight)) followed by unpack_gate (ref: src/decider/combined_gates.py:19-43,
+ * src/decider/packed_conv.py:45-53), in one launch:
+ *   a = bf16(x . W[h]),  b = bf16(x . W[heads + h])   (bf16 products, fp32 sums)
+ *   g, beta as fd_gate_transform_fwd on those a, b
+ *
+ *   x        token r at x + r*x_row_stride, [hidden] bf16 contiguous
+ *   weight   [2*heads, hidden] bf16 contiguous (a rows, then b rows)
+ *   g        [rows, heads] fp32, beta [rows, heads] bf16 (contiguous)
+ *   ab       NULL or [rows, 2*heads] bf16: the a|b values the transform used
+ *
+ * Limits: heads in {8, 16, 24, 32}; hidden a multiple of 1024; x rows and
+ * weight 16-byte aligned.  The fp32 sums run in a fixed order (8 hidden-
+ * dimension parts added in order), so a and b can differ from another GEMM's
+ * bf16 output by one bf16 ulp where the sum lies near a rounding boundary.
+ */
+FD_API int fd_gate_proj_fwd(const void* x, int64_t x_row_stride, const void* weight, int hidden,
+                            const void* a_log, int a_log_dtype, const void* dt_bias, int dt_bias_dtype,
+                            float* g, void* beta, void* ab, int64_t rows, int heads, void* stream);
 
 /*
  * Slot-only readout: for each slot n (hidden row slot_rows[n], position

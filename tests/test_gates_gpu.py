@@ -98,3 +98,63 @@ def test_wrapper_rejects_bad_inputs():
         unpack(c, torch.zeros(8, device="cuda"), p)
     with pytest.raises(ValueError, match="BF16 or FP32"):
         unpack(c, p.double(), p)
+
+
+@pytest.mark.parametrize("B,T,H,hidden,pdt", [
+    (1, 2048, 16, 2048, torch.bfloat16),   # the decider's layer
+    (2, 37, 8, 1024, torch.float32),       # ragged token count (tail workgroup), fp32 parameters
+    (1, 100, 32, 3072, torch.bfloat16),
+])
+def test_fused_projection_vs_float64_and_hipblaslt(oracle, B, T, H, hidden, pdt):
+    """fd_gate_proj_fwd: the a|b projection against the float64 dot product, under the bound any
+    fp32 summation order meets, |a - a64| <= (n - 1) 2^-24 sum|x_k w_k| + one bf16 ulp of a64,
+    which hipBLASLt's bf16 GEMM (F.linear) meets too, and with > 99 % bit-exact; the transform of
+    the a|b it used (returned through `ab`) at the gate-transform bar against the float64 oracle."""
+    from fastdecisions_amd.unpack_gate_transform_kernel import gate_projection
+    gen = torch.Generator().manual_seed(5 + T)
+    x = torch.randn((B, T, hidden), generator=gen).to(torch.bfloat16)
+    w = (torch.randn((2 * H, hidden), generator=gen) * 0.03).to(torch.bfloat16)
+    a_log = torch.log(torch.empty(H).uniform_(1, 16, generator=gen)).to(pdt)
+    bias = torch.randn(H, generator=gen).to(pdt)
+    announce(f"fused gate projection B={B} T={T} H={H} hidden={hidden}")
+    xc, wc, lc, dc = (t.cuda() for t in (x, w, a_log, bias))
+    ab = torch.empty((B, T, 2 * H), dtype=torch.bfloat16, device="cuda")
+    g, beta = gate_projection(xc, wc, lc, dc, ab=ab)
+    lin = F.linear(xc, wc)
+    g2, beta2 = gate_projection(xc, wc, lc, dc)
+    torch.cuda.synchronize()
+    want = x.double().numpy() @ w.double().numpy().T
+    scale = np.abs(x.double().numpy()) @ np.abs(w.double().numpy()).T
+    bf16_ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64) * 2.0 ** 16
+    bound = (hidden - 1) * 2.0 ** -24 * scale + bf16_ulp
+    want_bits = oracle.f32_to_bf16(want.astype(np.float32))
+    exact = (to_bits(ab) == want_bits).mean()
+    print(f"a|b vs float64: exact {exact:.5f}, max |err|/bound "
+          f"{(np.abs(ab.float().cpu().numpy() - want) / bound).max():.3f}; "
+          f"F.linear vs float64 exact {(to_bits(lin) == want_bits).mean():.5f}")
+    assert (np.abs(ab.float().cpu().numpy() - want) <= bound).all() and exact > 0.99
+    assert (np.abs(lin.float().cpu().numpy() - want) <= bound).all()
+    ab_bits = to_bits(ab)
+    ref_g, ref_beta = oracle.gate_transform(ab_bits[..., :H], ab_bits[..., H:], a_log.float().numpy(),
+                                            bias.float().numpy())
+    assert _f32_ulps(g.cpu().numpy(), ref_g).max() < 4
+    assert ulp_diff(to_bits(beta), oracle.f32_to_bf16(ref_beta.astype(np.float32))).max() <= 1
+    # the optional ab output changes nothing; the result is deterministic
+    assert torch.equal(g, g2) and torch.equal(beta, beta2)
+
+
+def test_fused_projection_rejects_bad_inputs():
+    from fastdecisions_amd import _lib
+    from fastdecisions_amd.unpack_gate_transform_kernel import gate_projection
+    x = torch.zeros((1, 8, 2048), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros((32, 2048), dtype=torch.bfloat16, device="cuda")
+    p = torch.zeros(16, device="cuda")
+    with pytest.raises(ValueError, match="weight \\[2H, hidden\\]"):
+        gate_projection(x, w[:, :1024], p, p)
+    with pytest.raises(ValueError, match="a_log must have shape"):
+        gate_projection(x, w, torch.zeros(8, device="cuda"), p)
+    with pytest.raises(RuntimeError, match="heads must be"):
+        gate_projection(x, torch.zeros((20, 2048), dtype=torch.bfloat16, device="cuda"),
+                        torch.zeros(10, device="cuda"), torch.zeros(10, device="cuda"))
+    with pytest.raises(RuntimeError, match="multiple of 1024"):
+        gate_projection(x[..., :1536].contiguous(), w[:, :1536].contiguous(), p, p)
