@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: copy destinations stay scalar
   const int w4 = wave & 3;     // (head, query block) slot
   const int kh = wave >> 2;    // key part of each tile (0 when KSPLIT == 1)
   const int col = lane & 31;   // query within the wavefront's block
@@ -251,7 +251,7 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
 #pragma unroll
       for (int cs = 0; cs < 2 * C::kBlocks; ++cs)
 #pragma unroll
-        for (int r2 = 0; r2 < 2; ++r2) v_rd[db][cs][r2] = v_off_calc(db, cs, r2);
+        for (int r2 = 0; r2 < 2; ++r2) v_rd[db][cs][r2] = C::kStages * C::kTileBytes + v_off_calc(db, cs, r2);
   }
   int cp_krel[kHoist ? C::kLoads : 1], cp_vrel[kHoist ? C::kLoads : 1];
   if constexpr (kHoist) {
@@ -264,8 +264,11 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
   auto k_off = [&](int bl, int kk) {
     if constexpr (kHoist) return k_rd[bl][kk]; else return k_off_calc(bl, kk);
   };
-  auto v_off = [&](int db, int cs, int r2) {
-    if constexpr (kHoist) return v_rd[db][cs][r2]; else return v_off_calc(db, cs, r2);
+  // V^T operand address in stage BUF: the hoisted offsets include the V region's
+  // base, so the stage offset (< 64 KiB) is the read's immediate
+  auto v_addr = [&](int BUF, int db, int cs, int r2) -> const unsigned char* {
+    if constexpr (kHoist) return smem + BUF * C::kTileBytes + v_rd[db][cs][r2];
+    else return v_lds + BUF * C::kTileBytes + v_off_calc(db, cs, r2);
   };
 
   // rows past the end of the sequence re-read its last row: finite data the mask discards
@@ -289,8 +292,11 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
         krel = r * static_cast<int>(a.ks[2]) + cp_koff(i);
         vrel = r * static_cast<int>(a.vs[2]) + cp_voff(i);
       }
-      __builtin_amdgcn_global_load_lds(kg + krel, (lds_void_t*)(kt + blk * 1024), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vg + vrel, (lds_void_t*)(vt + blk * 1024), 16, 0, 0);
+      // uniform tile base + 32-bit per-lane byte offset (scalar-base addressing)
+      const void* ksrc = reinterpret_cast<const unsigned char*>(kg) + static_cast<uint32_t>(krel) * 2u;
+      const void* vsrc = reinterpret_cast<const unsigned char*>(vg) + static_cast<uint32_t>(vrel) * 2u;
+      __builtin_amdgcn_global_load_lds(ksrc, (lds_void_t*)(kt + blk * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vsrc, (lds_void_t*)(vt + blk * 1024), 16, 0, 0);
     }
   };
 
@@ -375,7 +381,6 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
   // 16-key slice comes from two transposing reads of the row-major V tile
   // (keys +0..3 and +4..7)
   auto accumulate = [&](int BUF, const bf16x8_t (&pb)[2 * C::kBlocks], float alpha, bool grow_any) {
-    const unsigned char* vt = v_lds + BUF * C::kTileBytes;
     if (grow_any) {
 #pragma unroll
       for (int db = 0; db < D / 32; ++db) o[db] *= alpha;
@@ -384,8 +389,8 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
     for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
       for (int cs = 0; cs < 2 * C::kBlocks; ++cs) {
-        const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(vt + v_off(db, cs, 0)));
-        const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(vt + v_off(db, cs, 1)));
+        const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)v_addr(BUF, db, cs, 0));
+        const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)v_addr(BUF, db, cs, 1));
         const short __attribute__((ext_vector_type(8))) vv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vv), pb[cs], o[db], 0, 0, 0);
       }
