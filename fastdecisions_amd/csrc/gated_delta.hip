@@ -545,15 +545,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     f32x4_t dec;    // e^{gl - gc_t}, t = 16wv + 4g4 .. +3
     float egl;      // e^{gl}
   };
-  auto load_chunk = [&](ChunkRegs& R, int c) {
+  // Part `part` of the operand loads of chunk c: parts 0-2 are the w planes,
+  // part 3 k^T, u and the exponentials; -1 loads all of them.
+  auto load_chunk = [&](ChunkRegs& R, int c, int part = -1) {
     c = min(c, last - 1);
     const size_t hc = static_cast<size_t>(h) * a.nc + c;
     // operand-ordered tiles: each wavefront load is 1 KiB contiguous (lane l = 16 g4 + c16)
     const uint16_t* w = a.w + hc * 3 * kC * kD + (wv * 4 * 64 + l) * 8;
 #pragma unroll
-    for (int x = 0; x < 3; ++x)
+    for (int x = 0; x < 3; ++x) {
+      if (part >= 0 && part != x) continue;
 #pragma unroll
       for (int st = 0; st < 4; ++st) R.w[x][st] = *reinterpret_cast<const uint4*>(w + x * kC * kD + st * 64 * 8);
+    }
+    if (part >= 0 && part != 3) return;
     const uint16_t* kt = a.kn + hc * kC * kD + (wv * 4 * 64 + l) * 8;
 #pragma unroll
     for (int m = 0; m < 2; ++m)
@@ -567,7 +572,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     R.egl = gx[2 * kC];
   };
 
-  auto step = [&](const ChunkRegs& R, int c) {
+  // One chunk.  The loads of chunk cp (two ahead) into P go out in four parts,
+  // each where the wavefront waits anyway (before a barrier, behind an issued
+  // MFMA group): the address unit takes about 16 cycles per 1 KiB load per CU,
+  // and one burst of all 19 would stall the in-order wavefront for most of a
+  // step.  sched_barrier keeps each part in place.
+  auto step = [&](const ChunkRegs& R, int c, ChunkRegs& P, int cp) {
     const size_t hc = static_cast<size_t>(h) * a.nc + c;
     // state at the chunk start: bf16 planes to LDS (B of w S), fp32 to the workspace (output pass)
     // (in the output pass's B-operand order: S[dk][col] at step s = dk / 32 of column group
@@ -584,6 +594,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       *reinterpret_cast<f32x4_t*>(sc + (wv * 64 + 16 * (2 * m + (g4 >> 1)) + c16) * 8 + 4 * (g4 & 1)) =
           f32x4_t{S[m][0], S[m][1], S[m][2], S[m][3]};
     }
+    __builtin_amdgcn_sched_barrier(0);
+    load_chunk(P, cp, 0);
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
 
     // v' = u - w S for rows 16wv..16wv+15 of this slice
@@ -602,6 +615,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       acc0 = mfma_bf16(R.w[1][st], sm, acc0);
       acc1 = mfma_bf16(R.w[2][st], sh, acc1);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    load_chunk(P, cp, 1);
+    __builtin_amdgcn_sched_barrier(0);
     f32x4_t vnew;
     float vdec[4];
 #pragma unroll
@@ -621,6 +637,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       *reinterpret_cast<uint2*>(sVd[1] + off) = pm;
       *reinterpret_cast<uint2*>(sVd[2] + off) = pl;
     }
+    __builtin_amdgcn_sched_barrier(0);
+    load_chunk(P, cp, 2);
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
 
     // S <- e^{gl} S + k^T (e^{gl - gc} v'), dk rows 32wv..32wv+31
@@ -639,6 +658,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       st0 = mfma_bf16(R.k[0][st], dl, st0);
       st1 = mfma_bf16(R.k[1][st], dl, st1);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    load_chunk(P, cp, 3);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       S[0][r] = st0[r];
@@ -654,16 +676,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     load_chunk(A, first);
     load_chunk(B, first + 1);
     for (int c = first; c < last; c += 3) {
-      load_chunk(Cr, c + 2);
-      step(A, c);
-      if (c + 1 < last) {
-        load_chunk(A, c + 3);
-        step(B, c + 1);
-      }
-      if (c + 2 < last) {
-        load_chunk(B, c + 4);
-        step(Cr, c + 2);
-      }
+      step(A, c, Cr, c + 2);
+      if (c + 1 < last) step(B, c + 1, A, c + 3);
+      if (c + 2 < last) step(Cr, c + 2, B, c + 4);
     }
   }
 
