@@ -93,6 +93,13 @@ SIGNATURES = {
         [_c_void_p, ctypes.c_int64, _c_void_p, ctypes.c_int, _c_void_p, ctypes.c_int, _c_void_p, ctypes.c_int,
          _c_void_p, _c_void_p, _c_void_p, ctypes.c_int64, ctypes.c_int, _c_void_p],
     ),
+    "fd_packed_conv_gate_fwd": (
+        ctypes.c_int,
+        [_c_void_p, ctypes.c_int64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p, ctypes.c_int,
+         _c_void_p, ctypes.c_int64, _c_void_p, ctypes.c_int, _c_void_p, ctypes.c_int, _c_void_p, ctypes.c_int,
+         _c_void_p, _c_void_p, ctypes.c_int, _c_void_p],
+    ),
     "fd_gate_transform_fwd": (
         ctypes.c_int,
         [_c_void_p, _c_void_p, ctypes.c_int64, ctypes.c_int64, _c_void_p, ctypes.c_int, _c_void_p, ctypes.c_int,

@@ -11,21 +11,13 @@
 // projection output (row stride 2*heads), as the reference's combined gate
 // projection produces (ref: src/decider/combined_gates.py:19-43).
 #include "fd_common.h"
+#include "gate_proj_body.h"
 
 namespace {
 
 constexpr int kThreads = 256;
 
-template <typename PT>
-__device__ __forceinline__ float load_param(const void* p, int i);
-template <>
-__device__ __forceinline__ float load_param<uint16_t>(const void* p, int i) {
-  return fd_bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
-}
-template <>
-__device__ __forceinline__ float load_param<float>(const void* p, int i) {
-  return static_cast<const float*>(p)[i];
-}
+using fd_gate::load_param;
 
 template <typename LT, typename BT>
 __global__ __launch_bounds__(kThreads) void gate_transform_kernel(const uint16_t* __restrict__ a,
@@ -45,82 +37,12 @@ __global__ __launch_bounds__(kThreads) void gate_transform_kernel(const uint16_t
 }
 
 // ---------------------------------------------------------------------------
-// a|b projection fused with the transform (fd_gate_proj_fwd).
-//
-// One workgroup per 16 tokens, 8 wavefronts; wavefront wv accumulates the
-// hidden-dimension part [wv*hidden/8, (wv+1)*hidden/8) of all 2*heads outputs
-// on v_mfma_f32_16x16x32_bf16 (exact bf16 products, fp32 sums).  Lane l
-// supplies A = x[row0 + l%16][k + 8(l/16) .. +7] and B = W[n0 + l%16][same k]
-// (16-byte loads); D[4(l/16)+r][l%16] is (token, output).  The 8 partial sums
-// are added in wavefront order through LDS and rounded to bf16, the value a
-// bf16 GEMM (F.linear) stores, then transformed as gate_transform_kernel does.
-constexpr int kProjRows = 16;
-constexpr int kProjWaves = 8;
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
+// a|b projection fused with the transform (fd_gate_proj_fwd): one workgroup per
+// 16 tokens, 8 wavefronts, one hidden-dimension part each (gate_proj_body.h).
 template <typename LT, typename BT, int NB>
-__global__ __launch_bounds__(64 * kProjWaves) void gate_proj_kernel(
-    const uint16_t* __restrict__ x, int64_t xs, const uint16_t* __restrict__ w, int hidden, const void* a_log,
-    const void* dt_bias, float* __restrict__ g, uint16_t* __restrict__ beta, uint16_t* __restrict__ ab,
-    int64_t rows) {
-  constexpr int heads = 8 * NB;  // 2 * heads = NB blocks of 16 outputs
-  __shared__ float part[kProjWaves][NB * 16][kProjRows + 1];
-  const int tid = threadIdx.x;
-  const int wv = tid >> 6;
-  const int l = tid & 63;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kProjRows;
-  const int64_t xrow = min(row0 + (l & 15), rows - 1);  // rows past the end re-read the last one
-  const int kq = hidden / kProjWaves;
-  const uint16_t* xp = x + xrow * xs + wv * kq + 8 * (l >> 4);
-  const uint16_t* wp = w + static_cast<int64_t>(l & 15) * hidden + wv * kq + 8 * (l >> 4);
-  f32x4_t acc[NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4_t{};
-  for (int k = 0; k < kq; k += 128) {
-    bf16x8_t av[4], bv[4][NB];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      av[s] = *reinterpret_cast<const bf16x8_t*>(xp + k + 32 * s);
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-        bv[s][nb] = *reinterpret_cast<const bf16x8_t*>(wp + static_cast<int64_t>(16 * nb) * hidden + k + 32 * s);
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[s], bv[s][nb], acc[nb], 0, 0, 0);
-  }
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) part[wv][16 * nb + (l & 15)][4 * (l >> 4) + r] = acc[nb][r];
-  __syncthreads();
-  if (tid >= kProjRows * heads) return;
-  const int rr = tid / heads;
-  const int h = tid - rr * heads;
-  const int64_t row = row0 + rr;
-  if (row >= rows) return;
-  float sa = part[0][h][rr];
-  float sb = part[0][heads + h][rr];
-#pragma unroll
-  for (int p = 1; p < kProjWaves; ++p) {
-    sa = sa + part[p][h][rr];
-    sb = sb + part[p][heads + h][rr];
-  }
-  const uint32_t abits = fd_f32_to_bf16(sa);
-  const uint32_t bbits = fd_f32_to_bf16(sb);
-  if (ab != nullptr) {
-    ab[row * 2 * heads + h] = static_cast<uint16_t>(abits);
-    ab[row * 2 * heads + heads + h] = static_cast<uint16_t>(bbits);
-  }
-  const float xa = fd_bf16_to_f32(abits) + load_param<BT>(dt_bias, h);
-  const float sp = xa > 20.0f ? xa : log1pf(expf(xa));
-  g[row * heads + h] = -expf(load_param<LT>(a_log, h)) * sp;
-  const float y = fd_bf16_to_f32(bbits);
-  beta[row * heads + h] = static_cast<uint16_t>(fd_f32_to_bf16(1.0f / (1.0f + expf(-y))));
+__global__ __launch_bounds__(64 * fd_gate::kProjParts) void gate_proj_kernel(fd_gate::GateProjArgs args) {
+  __shared__ fd_gate::PartSmem<NB> part;
+  fd_gate::gate_proj_rows<LT, BT, NB, fd_gate::kProjParts>(blockIdx.x, args, part);
 }
 
 }  // namespace
@@ -128,30 +50,17 @@ __global__ __launch_bounds__(64 * kProjWaves) void gate_proj_kernel(
 extern "C" FD_API int fd_gate_proj_fwd(const void* x, int64_t x_row_stride, const void* weight, int hidden,
                                        const void* a_log, int a_log_dtype, const void* dt_bias, int dt_bias_dtype,
                                        float* g, void* beta, void* ab, int64_t rows, int heads, void* stream) {
-  FD_REQUIRE(x && weight && a_log && dt_bias && g && beta, FD_ERR_INVALID_ARGUMENT,
-             "fd_gate_proj_fwd: pointers must be non-null");
-  FD_REQUIRE(rows >= 0, FD_ERR_INVALID_ARGUMENT, "fd_gate_proj_fwd: rows must be >= 0");
-  FD_REQUIRE(heads == 8 || heads == 16 || heads == 24 || heads == 32, FD_ERR_UNSUPPORTED,
-             "fd_gate_proj_fwd: heads must be 8, 16, 24 or 32 (got %d)", heads);
-  FD_REQUIRE(hidden > 0 && hidden % (kProjWaves * 128) == 0, FD_ERR_UNSUPPORTED,
-             "fd_gate_proj_fwd: hidden must be a positive multiple of %d (got %d)", kProjWaves * 128, hidden);
-  FD_REQUIRE(x_row_stride >= hidden && x_row_stride % 8 == 0 && fd_aligned16(x) && fd_aligned16(weight),
-             FD_ERR_ALIGNMENT, "fd_gate_proj_fwd: x rows and weight must be 16-byte aligned, row stride >= hidden");
-  FD_REQUIRE((a_log_dtype == FD_DTYPE_BF16 || a_log_dtype == FD_DTYPE_F32) &&
-                 (dt_bias_dtype == FD_DTYPE_BF16 || dt_bias_dtype == FD_DTYPE_F32),
-             FD_ERR_INVALID_ARGUMENT, "fd_gate_proj_fwd: parameter dtypes must be FD_DTYPE_BF16 or FD_DTYPE_F32");
+  const int rc = fd_gate::gate_proj_check("fd_gate_proj_fwd", x, x_row_stride, weight, hidden, a_log, a_log_dtype,
+                                          dt_bias, dt_bias_dtype, g, beta, rows, heads);
+  if (rc != FD_OK) return rc;
   if (rows == 0) return FD_OK;
-  const int64_t blocks = (rows + kProjRows - 1) / kProjRows;
-  FD_REQUIRE(blocks < (1LL << 31), FD_ERR_INVALID_ARGUMENT, "fd_gate_proj_fwd: problem too large");
-  const dim3 grid(static_cast<unsigned>(blocks));
+  const dim3 grid(static_cast<unsigned>((rows + fd_gate::kProjRows - 1) / fd_gate::kProjRows));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const uint16_t* xp = static_cast<const uint16_t*>(x);
-  const uint16_t* wp = static_cast<const uint16_t*>(weight);
-  uint16_t* betap = static_cast<uint16_t*>(beta);
-  uint16_t* abp = static_cast<uint16_t*>(ab);
-#define FD_PROJ_LAUNCH(LT, BT, NB)                                                                           \
-  hipLaunchKernelGGL((gate_proj_kernel<LT, BT, NB>), grid, dim3(64 * kProjWaves), 0, s, xp, x_row_stride, wp, \
-                     hidden, a_log, dt_bias, g, betap, abp, rows)
+  const fd_gate::GateProjArgs args{static_cast<const uint16_t*>(x), x_row_stride, static_cast<const uint16_t*>(weight),
+                                   hidden, a_log, dt_bias, g, static_cast<uint16_t*>(beta),
+                                   static_cast<uint16_t*>(ab), rows};
+#define FD_PROJ_LAUNCH(LT, BT, NB) \
+  hipLaunchKernelGGL((gate_proj_kernel<LT, BT, NB>), grid, dim3(64 * fd_gate::kProjParts), 0, s, args)
 #define FD_PROJ_HEADS(LT, BT)                 \
   switch (heads) {                            \
     case 8: FD_PROJ_LAUNCH(LT, BT, 1); break;  \

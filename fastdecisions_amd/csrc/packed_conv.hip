@@ -23,6 +23,7 @@
 // The tap order is the reference's (ref: :139-177); a product of two bf16
 // values is exact in fp32, so each fma equals the multiply-then-add there.
 #include "fd_common.h"
+#include "gate_proj_body.h"
 
 namespace {
 
@@ -50,15 +51,33 @@ __device__ __forceinline__ uint4 load16(const uint16_t* p) { return *reinterpret
 // runs on XCD b % 8; logical block L = (b % 8) * (nblocks / 8) + b / 8, so the
 // logical blocks of one XCD are contiguous: all channel columns of a run, then
 // the next run.
+struct ConvArgs {
+  const uint16_t* x;     // [total_rows, C] bf16, row stride x_row elements
+  const uint16_t* w;     // [C, WIDTH] bf16
+  const uint16_t* bias;  // [C] bf16 or null
+  uint16_t* q;           // [total_rows, key_dim]
+  uint16_t* k;           // [total_rows, key_dim]
+  uint16_t* v;           // [total_rows, value_dim]
+  int64_t x_row;
+  int total_rows, seq_len, key_dim, value_dim;
+  const int32_t* cu_seqlens;  // [n_seqs + 1] or null
+  int n_seqs, n_runs, n_col;
+};
+
+// The conv work of linear block `lin` of `nblocks` (a multiple of 8).
 template <int WIDTH, int RUN, bool SILU, bool HAS_BIAS>
-__global__ __launch_bounds__(kThreads) void packed_conv_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias,
-    uint16_t* __restrict__ q, uint16_t* __restrict__ k, uint16_t* __restrict__ v, int64_t x_row, int total_rows,
-    int seq_len, int key_dim, int value_dim, const int32_t* __restrict__ cu_seqlens, int n_seqs, int n_runs,
-    int n_col) {
+__device__ __forceinline__ void conv_block(int lin, int nblocks, const ConvArgs& a) {
+  const uint16_t* __restrict__ x = a.x;
+  const uint16_t* __restrict__ w = a.w;
+  const uint16_t* __restrict__ bias = a.bias;
+  uint16_t* __restrict__ q = a.q;
+  uint16_t* __restrict__ k = a.k;
+  uint16_t* __restrict__ v = a.v;
+  const int64_t x_row = a.x_row;
+  const int total_rows = a.total_rows, seq_len = a.seq_len, key_dim = a.key_dim, value_dim = a.value_dim;
+  const int32_t* __restrict__ cu_seqlens = a.cu_seqlens;
+  const int n_seqs = a.n_seqs, n_runs = a.n_runs, n_col = a.n_col;
   const int C = 2 * key_dim + value_dim;
-  const int nblocks = gridDim.x;
-  const int lin = blockIdx.x;
   const int logical = (lin % kNumXcd) * (nblocks / kNumXcd) + lin / kNumXcd;
   const int run = logical / n_col;
   const int chunk = (logical % n_col) * kThreads + threadIdx.x;  // 8-channel chunk
@@ -175,17 +194,61 @@ __global__ __launch_bounds__(kThreads) void packed_conv_kernel(
   }
 }
 
+template <int WIDTH, int RUN, bool SILU, bool HAS_BIAS>
+__global__ __launch_bounds__(kThreads) void packed_conv_kernel(ConvArgs args) {
+  conv_block<WIDTH, RUN, SILU, HAS_BIAS>(blockIdx.x, gridDim.x, args);
+}
+
+// The conv (SiLU, no bias) and the a|b gate projection of the same layer in one
+// launch.  The two are independent, and the projection alone is a small,
+// latency-bound launch: its first `gate_blocks` workgroups (a multiple of 8,
+// so every conv block keeps its XCD) run the projection of 16 tokens each with
+// 4 wavefronts taking two hidden-dimension parts apiece, and the rest run
+// exactly the conv's blocks.  The projection's bits equal fd_gate_proj_fwd's.
+// The register budget is held to the conv kernel's own occupancy (5
+// wavefronts per SIMD), which the projection body would otherwise lower.
+template <int WIDTH, int RUN, typename LT, typename BT, int NB>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) void conv_gate_kernel(ConvArgs conv, fd_gate::GateProjArgs gate,
+                                                             int gate_blocks) {
+  __shared__ fd_gate::PartSmem<NB> part;
+  const int b = blockIdx.x;
+  if (b < gate_blocks) {
+    fd_gate::gate_proj_rows<LT, BT, NB, kThreads / 64>(b, gate, part);
+    return;
+  }
+  conv_block<WIDTH, RUN, true, false>(b - gate_blocks, gridDim.x - gate_blocks, conv);
+}
+
+// Gate projection launched with the conv (fd_packed_conv_gate_fwd), or none.
+struct GateSpec {
+  fd_gate::GateProjArgs args;
+  int a_log_dtype, dt_bias_dtype, heads;
+};
+
+template <int WIDTH, int RUN, typename LT, typename BT>
+void launch_conv_gate(const ConvArgs& conv, const GateSpec& gate, int conv_blocks, hipStream_t stream) {
+  int gate_blocks = static_cast<int>((gate.args.rows + fd_gate::kProjRows - 1) / fd_gate::kProjRows);
+  gate_blocks = (gate_blocks + kNumXcd - 1) / kNumXcd * kNumXcd;  // blocks past the last token exit at once
+  const dim3 grid(static_cast<unsigned>(gate_blocks + conv_blocks)), block(kThreads);
+  switch (gate.heads) {
+    case 8: hipLaunchKernelGGL((conv_gate_kernel<WIDTH, RUN, LT, BT, 1>), grid, block, 0, stream, conv, gate.args, gate_blocks); break;
+    case 16: hipLaunchKernelGGL((conv_gate_kernel<WIDTH, RUN, LT, BT, 2>), grid, block, 0, stream, conv, gate.args, gate_blocks); break;
+    case 24: hipLaunchKernelGGL((conv_gate_kernel<WIDTH, RUN, LT, BT, 3>), grid, block, 0, stream, conv, gate.args, gate_blocks); break;
+    default: hipLaunchKernelGGL((conv_gate_kernel<WIDTH, RUN, LT, BT, 4>), grid, block, 0, stream, conv, gate.args, gate_blocks); break;
+  }
+}
+
 template <int WIDTH, int RUN>
-int launch_run(const void* x, int64_t x_row, const void* w, const void* bias, void* q, void* k, void* v,
-               int total_rows, int seq_len, int key_dim, int value_dim, const int32_t* cu, int n_seqs, int act,
-               hipStream_t stream) {
+int launch_run(const char* who, const void* x, int64_t x_row, const void* w, const void* bias, void* q, void* k,
+               void* v, int total_rows, int seq_len, int key_dim, int value_dim, const int32_t* cu, int n_seqs,
+               int act, const GateSpec* gate, hipStream_t stream) {
   const int C = 2 * key_dim + value_dim;
   const int chunks = C / 8;
   const int n_runs = (total_rows + RUN - 1) / RUN;
   const int n_col = (chunks + kThreads - 1) / kThreads;
   int64_t nblocks = static_cast<int64_t>(n_col) * n_runs;
   nblocks = (nblocks + kNumXcd - 1) / kNumXcd * kNumXcd;  // padded blocks exit at once
-  if (nblocks > 2147483647LL) return fd_set_error(FD_ERR_INVALID_ARGUMENT, "fd_packed_conv_fwd: grid too large");
+  if (nblocks > (1LL << 30)) return fd_set_error(FD_ERR_INVALID_ARGUMENT, "%s: grid too large", who);
   dim3 grid(static_cast<unsigned>(nblocks)), block(kThreads);
   auto xs = static_cast<const uint16_t*>(x);
   auto ws = static_cast<const uint16_t*>(w);
@@ -193,16 +256,26 @@ int launch_run(const void* x, int64_t x_row, const void* w, const void* bias, vo
   auto qs = static_cast<uint16_t*>(q);
   auto ks = static_cast<uint16_t*>(k);
   auto vs = static_cast<uint16_t*>(v);
-#define FD_CONV_LAUNCH(SILU, BIAS)                                                                         \
-  hipLaunchKernelGGL((packed_conv_kernel<WIDTH, RUN, SILU, BIAS>), grid, block, 0, stream, xs, ws, bsp, qs, ks, vs, \
-                     x_row, total_rows, seq_len, key_dim, value_dim, cu, n_seqs, n_runs, n_col)
+  const ConvArgs args{xs, ws, bsp, qs, ks, vs, x_row, total_rows, seq_len, key_dim, value_dim, cu, n_seqs, n_runs,
+                      n_col};
+  if (gate != nullptr) {
+    const bool lf = gate->a_log_dtype == FD_DTYPE_F32, bf = gate->dt_bias_dtype == FD_DTYPE_F32;
+    const int nb = static_cast<int>(nblocks);
+    if (lf && bf) launch_conv_gate<WIDTH, RUN, float, float>(args, *gate, nb, stream);
+    else if (lf) launch_conv_gate<WIDTH, RUN, float, uint16_t>(args, *gate, nb, stream);
+    else if (bf) launch_conv_gate<WIDTH, RUN, uint16_t, float>(args, *gate, nb, stream);
+    else launch_conv_gate<WIDTH, RUN, uint16_t, uint16_t>(args, *gate, nb, stream);
+    return fd_check_launch(who);
+  }
+#define FD_CONV_LAUNCH(SILU, BIAS) \
+  hipLaunchKernelGGL((packed_conv_kernel<WIDTH, RUN, SILU, BIAS>), grid, block, 0, stream, args)
   const bool silu = act == FD_ACT_SILU;
   if (silu && bsp == nullptr) FD_CONV_LAUNCH(true, false);
   else if (silu) FD_CONV_LAUNCH(true, true);
   else if (bsp == nullptr) FD_CONV_LAUNCH(false, false);
   else FD_CONV_LAUNCH(false, true);
 #undef FD_CONV_LAUNCH
-  return fd_check_launch("fd_packed_conv_fwd");
+  return fd_check_launch(who);
 }
 
 #ifndef FD_CONV_RUN
@@ -213,42 +286,39 @@ int launch_run(const void* x, int64_t x_row, const void* w, const void* bias, vo
 // so occupancy matters more than the 3/4 halo re-read, which hits L2).
 constexpr int kRun = FD_CONV_RUN;
 
-int packed_conv_entry(const void* x, int64_t x_row_stride, const void* weight, const void* bias, void* q, void* k,
-                      void* v, int batch, int seq_len, int key_dim, int value_dim, int width,
-                      const int32_t* cu_seqlens, int n_seqs, int activation, void* stream) {
+int packed_conv_entry(const char* who, const void* x, int64_t x_row_stride, const void* weight, const void* bias,
+                      void* q, void* k, void* v, int batch, int seq_len, int key_dim, int value_dim, int width,
+                      const int32_t* cu_seqlens, int n_seqs, int activation, const GateSpec* gate, void* stream) {
   FD_REQUIRE(x != nullptr && weight != nullptr && q != nullptr && k != nullptr && v != nullptr,
-             FD_ERR_INVALID_ARGUMENT, "fd_packed_conv_fwd: x, weight, q, k and v must be non-null");
+             FD_ERR_INVALID_ARGUMENT, "%s: x, weight, q, k and v must be non-null", who);
   FD_REQUIRE(batch >= 0 && seq_len >= 0, FD_ERR_INVALID_ARGUMENT,
-             "fd_packed_conv_fwd: batch and seq_len must be >= 0 (got %d, %d)", batch, seq_len);
+             "%s: batch and seq_len must be >= 0 (got %d, %d)", who, batch, seq_len);
   FD_REQUIRE(key_dim > 0 && value_dim > 0 && key_dim % 8 == 0 && value_dim % 8 == 0, FD_ERR_INVALID_ARGUMENT,
-             "fd_packed_conv_fwd: key_dim and value_dim must be positive multiples of 8 (got %d, %d)", key_dim,
-             value_dim);
-  FD_REQUIRE(width >= 1 && width <= 4, FD_ERR_UNSUPPORTED,
-             "fd_packed_conv_fwd: width must be in [1, 4] (got %d)", width);
+             "%s: key_dim and value_dim must be positive multiples of 8 (got %d, %d)", who, key_dim, value_dim);
+  FD_REQUIRE(width >= 1 && width <= 4, FD_ERR_UNSUPPORTED, "%s: width must be in [1, 4] (got %d)", who, width);
   FD_REQUIRE(activation == FD_ACT_NONE || activation == FD_ACT_SILU, FD_ERR_INVALID_ARGUMENT,
-             "fd_packed_conv_fwd: activation must be FD_ACT_NONE or FD_ACT_SILU (got %d)", activation);
+             "%s: activation must be FD_ACT_NONE or FD_ACT_SILU (got %d)", who, activation);
   const int64_t total = static_cast<int64_t>(batch) * seq_len;
   const int64_t C = 2 * static_cast<int64_t>(key_dim) + value_dim;
   FD_REQUIRE(x_row_stride >= C && x_row_stride % 8 == 0, FD_ERR_ALIGNMENT,
-             "fd_packed_conv_fwd: the row stride of x must be a multiple of 8 and >= C");
+             "%s: the row stride of x must be a multiple of 8 and >= C", who);
   FD_REQUIRE(total * x_row_stride < (static_cast<int64_t>(1) << 40) && total < 2147483647LL && C <= 1048576,
-             FD_ERR_INVALID_ARGUMENT, "fd_packed_conv_fwd: problem too large");
+             FD_ERR_INVALID_ARGUMENT, "%s: problem too large", who);
   if (cu_seqlens != nullptr) {
-    FD_REQUIRE(batch == 1, FD_ERR_INVALID_ARGUMENT,
-               "fd_packed_conv_fwd: cu_seqlens requires batch == 1 (got %d)", batch);
-    FD_REQUIRE(n_seqs >= 1, FD_ERR_INVALID_ARGUMENT, "fd_packed_conv_fwd: n_seqs must be >= 1 (got %d)", n_seqs);
+    FD_REQUIRE(batch == 1, FD_ERR_INVALID_ARGUMENT, "%s: cu_seqlens requires batch == 1 (got %d)", who, batch);
+    FD_REQUIRE(n_seqs >= 1, FD_ERR_INVALID_ARGUMENT, "%s: n_seqs must be >= 1 (got %d)", who, n_seqs);
   }
   FD_REQUIRE(fd_aligned16(x) && fd_aligned16(weight) && fd_aligned16(q) && fd_aligned16(k) && fd_aligned16(v) &&
                  (bias == nullptr || fd_aligned16(bias)),
-             FD_ERR_ALIGNMENT, "fd_packed_conv_fwd: inputs must be aligned to 16 bytes");
+             FD_ERR_ALIGNMENT, "%s: inputs must be aligned to 16 bytes", who);
   if (total == 0) return FD_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int rows = static_cast<int>(total);
   switch (width) {
-    case 1: return launch_run<1, kRun>(x, x_row_stride, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, s);
-    case 2: return launch_run<2, kRun>(x, x_row_stride, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, s);
-    case 3: return launch_run<3, kRun>(x, x_row_stride, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, s);
-    default: return launch_run<4, kRun>(x, x_row_stride, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, s);
+    case 1: return launch_run<1, kRun>(who, x, x_row_stride, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, gate, s);
+    case 2: return launch_run<2, kRun>(who, x, x_row_stride, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, gate, s);
+    case 3: return launch_run<3, kRun>(who, x, x_row_stride, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, gate, s);
+    default: return launch_run<4, kRun>(who, x, x_row_stride, weight, bias, q, k, v, rows, seq_len, key_dim, value_dim, cu_seqlens, n_seqs, activation, gate, s);
   }
 }
 
@@ -257,14 +327,34 @@ int packed_conv_entry(const void* x, int64_t x_row_stride, const void* weight, c
 extern "C" int fd_packed_conv_fwd(const void* x, const void* weight, const void* bias, void* q, void* k, void* v,
                                   int batch, int seq_len, int key_dim, int value_dim, int width,
                                   const int32_t* cu_seqlens, int n_seqs, int activation, void* stream) {
-  return packed_conv_entry(x, 2 * static_cast<int64_t>(key_dim) + value_dim, weight, bias, q, k, v, batch, seq_len,
-                           key_dim, value_dim, width, cu_seqlens, n_seqs, activation, stream);
+  return packed_conv_entry("fd_packed_conv_fwd", x, 2 * static_cast<int64_t>(key_dim) + value_dim, weight, bias, q,
+                           k, v, batch, seq_len, key_dim, value_dim, width, cu_seqlens, n_seqs, activation, nullptr,
+                           stream);
 }
 
 extern "C" int fd_packed_conv_strided_fwd(const void* x, int64_t x_row_stride, const void* weight, const void* bias,
                                           void* q, void* k, void* v, int batch, int seq_len, int key_dim,
                                           int value_dim, int width, const int32_t* cu_seqlens, int n_seqs,
                                           int activation, void* stream) {
-  return packed_conv_entry(x, x_row_stride, weight, bias, q, k, v, batch, seq_len, key_dim, value_dim, width,
-                           cu_seqlens, n_seqs, activation, stream);
+  return packed_conv_entry("fd_packed_conv_fwd", x, x_row_stride, weight, bias, q, k, v, batch, seq_len, key_dim,
+                           value_dim, width, cu_seqlens, n_seqs, activation, nullptr, stream);
+}
+
+extern "C" int fd_packed_conv_gate_fwd(const void* x, int64_t x_row_stride, const void* weight, void* q, void* k,
+                                       void* v, int batch, int seq_len, int key_dim, int value_dim, int width,
+                                       const int32_t* cu_seqlens, int n_seqs, const void* hidden_states,
+                                       int64_t hidden_row_stride, const void* gate_weight, int hidden,
+                                       const void* a_log, int a_log_dtype, const void* dt_bias, int dt_bias_dtype,
+                                       float* g, void* beta, int heads, void* stream) {
+  const char* who = "fd_packed_conv_gate_fwd";
+  const int64_t rows = static_cast<int64_t>(batch) * seq_len;
+  const int rc = fd_gate::gate_proj_check(who, hidden_states, hidden_row_stride, gate_weight, hidden, a_log,
+                                          a_log_dtype, dt_bias, dt_bias_dtype, g, beta, rows, heads);
+  if (rc != FD_OK) return rc;
+  const GateSpec gate{{static_cast<const uint16_t*>(hidden_states), hidden_row_stride,
+                       static_cast<const uint16_t*>(gate_weight), hidden, a_log, dt_bias, g,
+                       static_cast<uint16_t*>(beta), nullptr, rows},
+                      a_log_dtype, dt_bias_dtype, heads};
+  return packed_conv_entry(who, x, x_row_stride, weight, nullptr, q, k, v, batch, seq_len, key_dim, value_dim, width,
+                           cu_seqlens, n_seqs, FD_ACT_SILU, &gate, stream);
 }

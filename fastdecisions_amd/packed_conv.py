@@ -10,6 +10,11 @@ Mirrors ref: src/decider/packed_conv.py:
   gated delta rule -> gated RMSNorm -> ``out_proj``; falls back to the original
   method for caches, training, grad, non-CUDA/non-bf16 inputs and other
   geometries (ref: :27-38).  The reference also requires T == 2048; any T works here;
+* ``packed_conv_gates(x, weight, hidden_states, gate_weight, a_log, dt_bias,
+  cu_seqlens=None) -> (q, k, v, g, beta)`` — the conv and the combined a|b gate
+  projection + gate transform in one launch (no counterpart in the reference;
+  bit-identical to ``packed_conv`` followed by ``fastdecisions::gate_proj``);
+  the patched forward uses it when the combined projections are installed;
 * ``install_packed_conv(core)`` — binds it on every ``Qwen3_5GatedDeltaNet``
   and returns the count (ref: :65-75).
 
@@ -27,7 +32,7 @@ from types import MethodType
 import torch
 import torch.nn.functional as F
 
-from .packed_conv_kernel import prep_qkv
+from .packed_conv_kernel import prep_qkv, prep_qkv_gates
 
 
 @torch.library.custom_op("fastdecisions::packed_conv", mutates_args=(), device_types="cuda")
@@ -53,6 +58,24 @@ def _packed_conv_varlen_fake(x, weight, cu_seqlens):
     batch, seq, channels = x.shape
     shape = (batch, seq, channels // 3 // 128, 128)
     return tuple(x.new_empty(shape) for _ in range(3))
+
+
+@torch.library.custom_op("fastdecisions::packed_conv_gates", mutates_args=(), device_types="cuda")
+def packed_conv_gates(x: torch.Tensor, weight: torch.Tensor, hidden_states: torch.Tensor, gate_weight: torch.Tensor,
+                      a_log: torch.Tensor, dt_bias: torch.Tensor,
+                      cu_seqlens: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                                                      torch.Tensor, torch.Tensor]:
+    """``packed_conv`` and ``fastdecisions::gate_proj`` of one layer in one launch."""
+    return prep_qkv_gates(x, weight, hidden_states, gate_weight, a_log, dt_bias, cu_seqlens=cu_seqlens)
+
+
+@packed_conv_gates.register_fake
+def _packed_conv_gates_fake(x, weight, hidden_states, gate_weight, a_log, dt_bias, cu_seqlens=None):
+    batch, seq, channels = x.shape
+    shape = (batch, seq, channels // 3 // 128, 128)
+    gates = (batch, seq, gate_weight.shape[0] // 2)
+    return (*(x.new_empty(shape) for _ in range(3)), x.new_empty(gates, dtype=torch.float32),
+            x.new_empty(gates, dtype=torch.bfloat16))
 
 
 def _segments(kwargs):
@@ -92,17 +115,19 @@ def _forward(self, hidden_states, cache_params=None, attention_mask=None, **kwar
     else:
         mixed = self.in_proj_qkv(hidden_states)
     cu_seqlens = kwargs.get("cu_seq_lens_q")
-    if cu_seqlens is not None:
+    fused_gates = combined and _gate_proj_fits(self, hidden_states)
+    if fused_gates:
+        # the conv and the a|b projection + gate transform in one launch
+        query, key, value, g, beta = packed_conv_gates(mixed, self.conv1d.weight, hidden_states,
+                                                       self._combined_gate_weight, self.A_log, self.dt_bias,
+                                                       cu_seqlens)
+    elif cu_seqlens is not None:
         query, key, value = packed_conv_varlen(mixed, self.conv1d.weight, cu_seqlens)
     else:
         query, key, value = packed_conv(mixed, self.conv1d.weight)
     if combined:
         z = proj[..., c0:c1].view(batch, seq, -1, self.head_v_dim)
-        if _gate_proj_fits(self, hidden_states):
-            # the a|b projection and the gate transform in one kernel
-            from .combined_gates import gate_proj_op
-            g, beta = gate_proj_op(hidden_states, self._combined_gate_weight, self.A_log, self.dt_bias)
-        else:
+        if not fused_gates:
             from .combined_gates import unpack_gate_op
             ab = F.linear(hidden_states, self._combined_gate_weight)
             g, beta = unpack_gate_op(ab, self.A_log, self.dt_bias)

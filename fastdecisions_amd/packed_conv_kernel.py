@@ -23,18 +23,8 @@ from . import _lib
 _ACTIVATIONS = {"silu": _lib.FD_ACT_SILU, None: _lib.FD_ACT_NONE}
 
 
-def prep_qkv(
-    input_qkv: torch.Tensor,
-    weight: torch.Tensor,
-    bias: torch.Tensor | None = None,
-    *,
-    key_dim: int | None = None,
-    value_dim: int | None = None,
-    head_k_dim: int = 128,
-    head_v_dim: int = 128,
-    activation: str | None = "silu",
-    cu_seqlens: torch.Tensor | None = None,
-):
+def _check_conv(input_qkv, weight, bias, key_dim, value_dim, head_k_dim, head_v_dim, activation, cu_seqlens):
+    """prep_qkv's validation; returns (B, T, key_dim, value_dim, row_stride, width, cu_ptr, n_seqs)."""
     if not input_qkv.is_cuda:
         raise ValueError("input_qkv must be on CUDA")
     if input_qkv.ndim != 3:
@@ -91,14 +81,73 @@ def prep_qkv(
             raise ValueError("cu_seqlens must be a contiguous int32 vector [n_seqs + 1] on input_qkv's device")
         n_seqs = cu_seqlens.numel() - 1
         cu_ptr = cu_seqlens.data_ptr()
+    return B, T, key_dim, value_dim, row_stride, width, cu_ptr, n_seqs
 
+
+def _alloc_qkv(input_qkv, B, T, key_dim, value_dim, head_k_dim, head_v_dim):
+    q = torch.empty((B, T, key_dim // head_k_dim, head_k_dim), device=input_qkv.device, dtype=input_qkv.dtype)
+    k = torch.empty_like(q)
+    v = torch.empty((B, T, value_dim // head_v_dim, head_v_dim), device=input_qkv.device, dtype=input_qkv.dtype)
+    return q, k, v
+
+
+def prep_qkv(
+    input_qkv: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    *,
+    key_dim: int | None = None,
+    value_dim: int | None = None,
+    head_k_dim: int = 128,
+    head_v_dim: int = 128,
+    activation: str | None = "silu",
+    cu_seqlens: torch.Tensor | None = None,
+):
+    B, T, key_dim, value_dim, row_stride, width, cu_ptr, n_seqs = _check_conv(
+        input_qkv, weight, bias, key_dim, value_dim, head_k_dim, head_v_dim, activation, cu_seqlens)
     with torch.cuda.device(input_qkv.device):
-        q = torch.empty((B, T, key_dim // head_k_dim, head_k_dim), device=input_qkv.device, dtype=input_qkv.dtype)
-        k = torch.empty_like(q)
-        v = torch.empty((B, T, value_dim // head_v_dim, head_v_dim), device=input_qkv.device, dtype=input_qkv.dtype)
+        q, k, v = _alloc_qkv(input_qkv, B, T, key_dim, value_dim, head_k_dim, head_v_dim)
         lib = _lib.lib()
         _lib.check("fd_packed_conv_strided_fwd", lib.fd_packed_conv_strided_fwd(
             input_qkv.data_ptr(), row_stride, weight.data_ptr(), _lib.ptr(bias), q.data_ptr(), k.data_ptr(),
             v.data_ptr(), B, T, key_dim, value_dim, width, cu_ptr, n_seqs, _ACTIVATIONS[activation],
             _lib.stream_handle(input_qkv.device)))
     return q, k, v
+
+
+def prep_qkv_gates(
+    input_qkv: torch.Tensor,
+    weight: torch.Tensor,
+    hidden_states: torch.Tensor,
+    gate_weight: torch.Tensor,
+    a_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    *,
+    key_dim: int | None = None,
+    value_dim: int | None = None,
+    head_k_dim: int = 128,
+    head_v_dim: int = 128,
+    cu_seqlens: torch.Tensor | None = None,
+):
+    """``prep_qkv(input_qkv, weight)`` (SiLU, no bias) and
+    ``gate_projection(hidden_states, gate_weight, a_log, dt_bias)`` of one layer
+    in one launch (``fd_packed_conv_gate_fwd``): returns ``(q, k, v, decay, beta)``,
+    bit-identical to the two calls made one after the other.  Each part takes the
+    arguments, and raises the errors, of its own function."""
+    B, T, key_dim, value_dim, row_stride, width, cu_ptr, n_seqs = _check_conv(
+        input_qkv, weight, None, key_dim, value_dim, head_k_dim, head_v_dim, "silu", cu_seqlens)
+    from .unpack_gate_transform_kernel import _PARAM_DTYPES, _check_gate_projection
+    gB, gT, hidden, H = _check_gate_projection(hidden_states, gate_weight, a_log, dt_bias)
+    if (gB, gT) != (B, T) or hidden_states.device != input_qkv.device:
+        raise ValueError("hidden_states must be [B, T, hidden] with input_qkv's B and T, on its device")
+    with torch.cuda.device(input_qkv.device):
+        q, k, v = _alloc_qkv(input_qkv, B, T, key_dim, value_dim, head_k_dim, head_v_dim)
+        decay = torch.empty((B, T, H), device=input_qkv.device, dtype=torch.float32)
+        beta = torch.empty((B, T, H), device=input_qkv.device, dtype=torch.bfloat16)
+        _lib.check("fd_packed_conv_gate_fwd", _lib.lib().fd_packed_conv_gate_fwd(
+            input_qkv.data_ptr(), row_stride, weight.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), B, T,
+            key_dim, value_dim, width, cu_ptr, n_seqs, hidden_states.data_ptr(), hidden_states.stride(1),
+            gate_weight.data_ptr(), hidden, a_log.data_ptr(), _PARAM_DTYPES[a_log.dtype], dt_bias.data_ptr(),
+            _PARAM_DTYPES[dt_bias.dtype], decay.data_ptr(), beta.data_ptr(), H,
+            _lib.stream_handle(input_qkv.device)))
+    return q, k, v, decay, beta

@@ -75,8 +75,8 @@ def unpack_gate(combined: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tens
     return gate_transform(combined[..., :H], combined[..., H:], a_log, dt_bias)
 
 
-def gate_projection(x: torch.Tensor, weight: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor,
-                    ab: torch.Tensor | None = None):
+def _check_gate_projection(x, weight, a_log, dt_bias):
+    """gate_projection's checks of x, weight and the parameters; returns (B, T, hidden, H)."""
     if not x.is_cuda or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or weight.device != x.device:
         raise ValueError("x and weight must be CUDA BF16 on one device")
     if x.ndim != 3 or weight.ndim != 2 or weight.shape[1] != x.shape[2] or weight.shape[0] % 2:
@@ -85,9 +85,15 @@ def gate_projection(x: torch.Tensor, weight: torch.Tensor, a_log: torch.Tensor, 
     H = weight.shape[0] // 2
     if B < 1 or T < 1:
         raise ValueError("B and T must be positive")
-    if x.stride(2) != 1 or x.stride(0) != T * x.stride(1) or not weight.is_contiguous():
+    if x.stride(2) != 1 or (B > 1 and x.stride(0) != T * x.stride(1)) or not weight.is_contiguous():
         raise ValueError("x must be row-contiguous [B, T, hidden] and weight contiguous")
     _check_params(a_log, dt_bias, H, x.device)
+    return B, T, hidden, H
+
+
+def gate_projection(x: torch.Tensor, weight: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor,
+                    ab: torch.Tensor | None = None):
+    B, T, hidden, H = _check_gate_projection(x, weight, a_log, dt_bias)
     if ab is not None and (ab.shape != (B, T, 2 * H) or ab.dtype != torch.bfloat16 or not ab.is_contiguous()
                            or ab.device != x.device):
         raise ValueError("ab must be a contiguous BF16 [B, T, 2H] tensor on x's device")

@@ -33,6 +33,7 @@
  *   fd_gate_proj_fwd    the combined a|b gate projection fused with the gate transform
  *                       replaces F.linear(x, cat(W_a, W_b)) + unpack_gate
  *                       (ref: src/decider/combined_gates.py:19-43, packed_conv.py:45-53)
+ *   fd_packed_conv_gate_fwd  fd_packed_conv_strided_fwd and fd_gate_proj_fwd of one layer in one launch
  *
  * Conventions shared by every entry point:
  *   - every tensor pointer is a device pointer; bf16 tensors are passed as raw
@@ -58,7 +59,7 @@ extern "C" {
 #define FD_API
 #endif
 
-#define FD_ABI_VERSION 9
+#define FD_ABI_VERSION 10
 
 #define FD_OK 0
 #define FD_ERR_INVALID_ARGUMENT (-1) /* shape, size, stride or flag out of range */
@@ -186,6 +187,32 @@ FD_API int fd_packed_conv_strided_fwd(const void* x, int64_t x_row_stride, const
                                       int seq_len, int key_dim, int value_dim, int width,
                                       const int32_t* cu_seqlens, int n_seqs, int activation,
                                       void* stream);
+
+/*
+ * fd_packed_conv_strided_fwd (SiLU, no bias) and fd_gate_proj_fwd of the same
+ * Gated-DeltaNet layer in one launch.  The two are independent; the gate
+ * projection alone is a small latency-bound launch, so here its workgroups run
+ * beside the conv's instead of after them.  No counterpart in the reference:
+ * it stands for its prep_qkv (ref: src/decider/packed_conv_kernel.py:194-232)
+ * followed by the combined gate projection and unpack_gate
+ * (ref: src/decider/combined_gates.py:19-43,
+ *  ref: src/decider/unpack_gate_transform_kernel.py:94-133).
+ *
+ *   x .. n_seqs          as fd_packed_conv_strided_fwd (activation SiLU, bias NULL);
+ *   hidden_states        token r at hidden_states + r*hidden_row_stride, [hidden] bf16
+ *                        (batch*seq_len tokens: the layer input the a|b projection reads)
+ *   gate_weight .. heads as fd_gate_proj_fwd (ab not written)
+ *
+ * q, k, v, g and beta are bit-identical to fd_packed_conv_strided_fwd followed
+ * by fd_gate_proj_fwd.  Limits: the union of both.
+ */
+FD_API int fd_packed_conv_gate_fwd(const void* x, int64_t x_row_stride, const void* weight, void* q,
+                                   void* k, void* v, int batch, int seq_len, int key_dim,
+                                   int value_dim, int width, const int32_t* cu_seqlens, int n_seqs,
+                                   const void* hidden_states, int64_t hidden_row_stride,
+                                   const void* gate_weight, int hidden, const void* a_log,
+                                   int a_log_dtype, const void* dt_bias, int dt_bias_dtype, float* g,
+                                   void* beta, int heads, void* stream);
 
 /*
  * Fused residual add + RMSNorm over rows of `width` features.
