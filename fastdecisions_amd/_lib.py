@@ -88,6 +88,11 @@ SIGNATURES = {
         ctypes.c_int,
         [_c_void_p, ctypes.c_int64, _c_void_p, ctypes.c_int64, ctypes.c_int, _c_void_p],
     ),
+    "fd_silu_mul_split_fwd": (
+        ctypes.c_int,
+        [_c_void_p, ctypes.c_int64, ctypes.c_int, _c_void_p, ctypes.c_int64, ctypes.c_int, _c_void_p,
+         ctypes.c_int64, _c_void_p],
+    ),
     "fd_gate_proj_fwd": (
         ctypes.c_int,
         [_c_void_p, ctypes.c_int64, _c_void_p, ctypes.c_int, _c_void_p, ctypes.c_int, _c_void_p, ctypes.c_int,

@@ -14,6 +14,9 @@
 // (transformers Qwen3_5MLP) on a combined [rows, 2*width] gate|up projection:
 //   out = bf16(bf16(silu(gate)) * up)
 // HBM-bound, 16-byte loads and stores, one thread per 8 features.
+// fd_silu_mul_split_fwd does the same when the features come from two
+// gate|up projections (features [0, width1) from the first, the rest from the
+// second), writing one [rows, width1 + width2] output.
 #include "fd_common.h"
 
 namespace {
@@ -76,15 +79,22 @@ __global__ __launch_bounds__(kThreads) void gated_rmsnorm_kernel(const uint16_t*
   if (valid) *reinterpret_cast<uint4*>(out + r * kWidth + ln * 8) = pack8(y);
 }
 
-// one 8-feature piece per thread; blockIdx.y is the row, so no index division
-__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __restrict__ gu, int64_t gu_stride,
-                                                            uint16_t* __restrict__ out, int width) {
+// one 8-feature piece per thread; blockIdx.y is the row, so no index division.
+// Output features [0, w1) come from gu1 (gate at column f, up at w1 + f), the
+// rest from gu2 (gate at f - w1, up at w2 + f - w1).
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __restrict__ gu1, int64_t stride1, int w1,
+                                                            const uint16_t* __restrict__ gu2, int64_t stride2, int w2,
+                                                            uint16_t* __restrict__ out) {
   const int c = blockIdx.x * kThreads + threadIdx.x;  // piece within the row
+  const int width = w1 + w2;
   if (c * 8 >= width) return;
   const int64_t r = blockIdx.y;
+  const bool first = c * 8 < w1;
+  const uint16_t* src = first ? gu1 + r * stride1 + c * 8 : gu2 + r * stride2 + (c * 8 - w1);
+  const int up = first ? w1 : w2;
   float g[8], u[8], s[8], y[8];
-  unpack8(*reinterpret_cast<const uint4*>(gu + r * gu_stride + c * 8), g);
-  unpack8(*reinterpret_cast<const uint4*>(gu + r * gu_stride + width + c * 8), u);
+  unpack8(*reinterpret_cast<const uint4*>(src), g);
+  unpack8(*reinterpret_cast<const uint4*>(src + up), u);
 #pragma unroll
   for (int e = 0; e < 8; ++e) s[e] = g[e] / (1.0f + expf(-g[e]));
   unpack8(pack8(s), s);  // act_fn's bf16 output
@@ -135,25 +145,48 @@ extern "C" FD_API int fd_gated_rmsnorm_fwd(const void* x, const void* gate, int6
   return fd_check_launch("fd_gated_rmsnorm_fwd");
 }
 
-extern "C" FD_API int fd_silu_mul_fwd(const void* gate_up, int64_t row_stride, void* out, int64_t rows, int width,
-                                      void* stream) {
-  FD_REQUIRE(gate_up && out, FD_ERR_INVALID_ARGUMENT, "fd_silu_mul_fwd: pointers must be non-null");
-  FD_REQUIRE(rows >= 0 && width > 0 && width % 8 == 0 && row_stride >= 2LL * width && row_stride % 8 == 0,
+namespace {
+
+int silu_mul_entry(const char* who, const void* gate_up1, int64_t row_stride1, int width1, const void* gate_up2,
+                   int64_t row_stride2, int width2, void* out, int64_t rows, void* stream) {
+  FD_REQUIRE(gate_up1 && out && (width2 == 0 || gate_up2), FD_ERR_INVALID_ARGUMENT,
+             "%s: pointers must be non-null", who);
+  FD_REQUIRE(rows >= 0 && width1 > 0 && width1 % 8 == 0 && row_stride1 >= 2LL * width1 && row_stride1 % 8 == 0,
              FD_ERR_INVALID_ARGUMENT,
-             "fd_silu_mul_fwd: width a positive multiple of 8 and row_stride a multiple of 8 >= 2*width");
-  FD_REQUIRE(fd_aligned16(gate_up) && fd_aligned16(out), FD_ERR_ALIGNMENT,
-             "fd_silu_mul_fwd: gate_up and out must be 16-byte aligned");
+             "%s: width a positive multiple of 8 and row_stride a multiple of 8 >= 2*width", who);
+  FD_REQUIRE(width2 >= 0 && width2 % 8 == 0 && (width2 == 0 || (row_stride2 >= 2LL * width2 && row_stride2 % 8 == 0)),
+             FD_ERR_INVALID_ARGUMENT,
+             "%s: width2 a multiple of 8 >= 0 and row_stride2 a multiple of 8 >= 2*width2", who);
+  FD_REQUIRE(fd_aligned16(gate_up1) && fd_aligned16(out) && (width2 == 0 || fd_aligned16(gate_up2)),
+             FD_ERR_ALIGNMENT, "%s: gate_up and out must be 16-byte aligned", who);
   if (rows == 0) return FD_OK;
+  const int64_t width = static_cast<int64_t>(width1) + width2;
   FD_REQUIRE(rows <= 65535 * 1024LL && width <= (1 << 28), FD_ERR_INVALID_ARGUMENT,
-             "fd_silu_mul_fwd: problem too large");
+             "%s: problem too large", who);
   const int64_t pieces = width / 8;
   const unsigned bx = static_cast<unsigned>((pieces + kThreads - 1) / kThreads);
+  const uint16_t* g1 = static_cast<const uint16_t*>(gate_up1);
+  const uint16_t* g2 = static_cast<const uint16_t*>(gate_up2);
   // rows beyond the grid's y limit run in slabs of 65535
   for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
     const unsigned by = static_cast<unsigned>(rows - r0 < 65535 ? rows - r0 : 65535);
     hipLaunchKernelGGL(silu_mul_kernel, dim3(bx, by), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
-                       static_cast<const uint16_t*>(gate_up) + r0 * row_stride, row_stride,
-                       static_cast<uint16_t*>(out) + r0 * width, width);
+                       g1 + r0 * row_stride1, row_stride1, width1, width2 ? g2 + r0 * row_stride2 : g2, row_stride2,
+                       width2, static_cast<uint16_t*>(out) + r0 * width);
   }
-  return fd_check_launch("fd_silu_mul_fwd");
+  return fd_check_launch(who);
+}
+
+}  // namespace
+
+extern "C" FD_API int fd_silu_mul_fwd(const void* gate_up, int64_t row_stride, void* out, int64_t rows, int width,
+                                      void* stream) {
+  return silu_mul_entry("fd_silu_mul_fwd", gate_up, row_stride, width, nullptr, 0, 0, out, rows, stream);
+}
+
+extern "C" FD_API int fd_silu_mul_split_fwd(const void* gate_up1, int64_t row_stride1, int width1,
+                                            const void* gate_up2, int64_t row_stride2, int width2, void* out,
+                                            int64_t rows, void* stream) {
+  return silu_mul_entry("fd_silu_mul_split_fwd", gate_up1, row_stride1, width1, gate_up2, row_stride2, width2, out,
+                        rows, stream);
 }

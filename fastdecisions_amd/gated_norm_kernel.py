@@ -63,3 +63,24 @@ def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
         _lib.check("fd_silu_mul_fwd", _lib.lib().fd_silu_mul_fwd(
             gate_up.data_ptr(), gate_up.shape[-1], out.data_ptr(), rows, width, _lib.stream_handle(gate_up.device)))
     return out
+
+
+def silu_mul_split(gate_up1: torch.Tensor, gate_up2: torch.Tensor) -> torch.Tensor:
+    """``silu_mul`` over two gate|up projections ``[..., 2*I1]`` and ``[..., 2*I2]``
+    (``fd_silu_mul_split_fwd``): returns ``[..., I1 + I2]``, features ``[0, I1)``
+    from the first, each computed exactly as ``silu_mul`` computes it."""
+    for t in (gate_up1, gate_up2):
+        if not t.is_cuda or t.dtype != torch.bfloat16 or t.shape[-1] % 16:
+            raise ValueError("gate_up must be CUDA BF16 [..., 2I] with I a multiple of 8")
+        if not t.is_contiguous() or t.data_ptr() % 16:
+            raise ValueError("gate_up must be contiguous and 16-byte aligned")
+    if gate_up1.shape[:-1] != gate_up2.shape[:-1] or gate_up1.device != gate_up2.device:
+        raise ValueError("gate_up1 and gate_up2 must have the same leading shape and device")
+    w1, w2 = gate_up1.shape[-1] // 2, gate_up2.shape[-1] // 2
+    rows = gate_up1.numel() // gate_up1.shape[-1]
+    with torch.cuda.device(gate_up1.device):
+        out = torch.empty((*gate_up1.shape[:-1], w1 + w2), device=gate_up1.device, dtype=torch.bfloat16)
+        _lib.check("fd_silu_mul_split_fwd", _lib.lib().fd_silu_mul_split_fwd(
+            gate_up1.data_ptr(), gate_up1.shape[-1], w1, gate_up2.data_ptr(), gate_up2.shape[-1], w2, out.data_ptr(),
+            rows, _lib.stream_handle(gate_up1.device)))
+    return out

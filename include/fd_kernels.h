@@ -27,6 +27,7 @@
  *                       (ref: src/decider/slot_projection.py:6-21, src/decider/engine.py:48-56)
  *   fd_gated_rmsnorm_fwd   gated RMSNorm of the delta rule's output (transformers Qwen3_5RMSNormGated)
  *   fd_silu_mul_fwd     the MLP's silu(gate) * up on a combined gate|up projection
+ *   fd_silu_mul_split_fwd  the same on two gate|up projections (the MLP's GEMM split in two)
  *   fd_gate_transform_fwd  gate transform (decay g and beta) of the Gated-DeltaNet layers
  *                       replaces unpack_gate(combined, a_log, dt_bias)
  *                       (ref: src/decider/unpack_gate_transform_kernel.py:94-133, kernel :51-91)
@@ -59,7 +60,7 @@ extern "C" {
 #define FD_API
 #endif
 
-#define FD_ABI_VERSION 10
+#define FD_ABI_VERSION 11
 
 #define FD_OK 0
 #define FD_ERR_INVALID_ARGUMENT (-1) /* shape, size, stride or flag out of range */
@@ -384,6 +385,20 @@ FD_API int fd_gated_rmsnorm_fwd(const void* x, const void* gate, int64_t gate_to
  */
 FD_API int fd_silu_mul_fwd(const void* gate_up, int64_t row_stride, void* out, int64_t rows, int width,
                            void* stream);
+
+/*
+ * fd_silu_mul_fwd over two gate|up projections: output features [0, width1) come
+ * from gate_up1 (gate in its columns [0, width1), up in [width1, 2*width1)), the
+ * next width2 from gate_up2 likewise; out [rows, width1 + width2] contiguous.
+ * Each feature is computed exactly as fd_silu_mul_fwd computes it.  No
+ * counterpart in the reference: the MLP's combined gate|up GEMM runs as two
+ * GEMMs whose widths hipBLASLt tiles better (transformers Qwen3_5MLP).
+ * width2 == 0 (gate_up2 unused) is fd_silu_mul_fwd.
+ * Limits: widths multiples of 8; 16-byte aligned pointers, row strides multiples of 8.
+ */
+FD_API int fd_silu_mul_split_fwd(const void* gate_up1, int64_t row_stride1, int width1,
+                                 const void* gate_up2, int64_t row_stride2, int width2, void* out,
+                                 int64_t rows, void* stream);
 
 #ifdef __cplusplus
 }

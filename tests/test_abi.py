@@ -25,7 +25,8 @@ def test_header_declares_the_expected_entry_points():
                                     "fd_gate_transform_fwd", "fd_gqa_gated_fwd", "fd_attn_prologue_fwd",
                                     "fd_slot_readout_fwd", "fd_gated_rmsnorm_fwd", "fd_silu_mul_fwd",
                                     "fd_packed_conv_strided_fwd", "fd_gated_delta_norm_fwd",
-                                    "fd_gate_proj_fwd", "fd_packed_conv_gate_fwd"}
+                                    "fd_gate_proj_fwd", "fd_packed_conv_gate_fwd",
+                                    "fd_silu_mul_split_fwd"}
 
 
 def test_library_exports_every_declared_symbol_and_nothing_else():

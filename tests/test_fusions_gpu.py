@@ -65,3 +65,52 @@ def test_decider_sizes_vs_eager_on_gpu():
         # the gated norm rounds three times after the reduction: a normalised value one ulp
         # apart (another fp32 summation order) can end two ulps apart
         assert u.max() <= (2 if name == "gated norm" else 1) and (u == 0).mean() > 0.999, name
+
+
+@pytest.mark.parametrize("rows,i1,i2", [(2048, 4096, 2048), (37, 24, 8), (5, 64, 0)])
+def test_silu_mul_split_equals_one_projection(rows, i1, i2):
+    """fd_silu_mul_split_fwd on two gate|up halves gives silu_mul's bits on the joined projection
+    (an empty second projection is the single-projection case)."""
+    from fastdecisions_amd.gated_norm_kernel import silu_mul, silu_mul_split
+    announce(f"silu_mul_split rows={rows} widths {i1}+{i2}")
+    gen = torch.Generator().manual_seed(rows + i1)
+    g1, u1 = (torch.randn((2, rows, i1), generator=gen) * 3).to(torch.bfloat16).cuda()
+    g2, u2 = (torch.randn((2, rows, i2), generator=gen) * 3).to(torch.bfloat16).cuda()
+    split = silu_mul_split(torch.cat((g1, u1), -1), torch.cat((g2, u2), -1))
+    joined = silu_mul(torch.cat((g1, g2, u1, u2), -1))
+    torch.cuda.synchronize()
+    assert split.shape == (rows, i1 + i2)
+    assert torch.equal(split.view(torch.int16), joined.view(torch.int16))
+
+
+def test_split_mlp_matches_eager_mlp():
+    """The installed MLP (two gate|up GEMMs + fd_silu_mul_split_fwd) against the eager Qwen3_5MLP."""
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as mq
+    from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5TextConfig
+    from fastdecisions_amd.layer_fusions import install_mlp_fusion
+    announce("split MLP 2048 tokens, hidden 2048, intermediate 6144")
+    torch.manual_seed(3)
+    cfg = Qwen3_5TextConfig(hidden_size=2048, intermediate_size=6144, hidden_act="silu")
+    mlp = mq.Qwen3_5MLP(cfg, 6144).to(torch.bfloat16).cuda()
+    with torch.no_grad():
+        for p in mlp.parameters():
+            p.normal_(0, 0.02)
+    x = torch.randn((1, 2048, 2048), dtype=torch.bfloat16, device="cuda")
+    with torch.no_grad():
+        eager = mlp(x)
+        assert install_mlp_fusion(torch.nn.ModuleList([mlp])) == 1
+        assert mlp._fd_gate_up_weight.shape == (8192, 2048) and mlp._fd_gate_up_weight2.shape == (4096, 2048)
+        ours = mlp(x)
+        # float64 evaluation of the same bf16 weights and input
+        x64 = x.double()
+        g64 = x64 @ mlp.gate_proj.weight.double().t()
+        u64 = x64 @ mlp.up_proj.weight.double().t()
+        ref = (g64 * torch.sigmoid(g64) * u64) @ mlp.down_proj.weight.double().t()
+    torch.cuda.synchronize()
+    # the GEMMs sum in another order than the eager gate and up GEMMs, so the bits differ;
+    # the bar is accuracy: no worse than the eager module against float64
+    e_ours, e_eager = (ours.double() - ref).abs(), (eager.double() - ref).abs()
+    print(f"split MLP vs float64: max {e_ours.max().item():.3e} rms {e_ours.pow(2).mean().sqrt().item():.3e}; "
+          f"eager max {e_eager.max().item():.3e} rms {e_eager.pow(2).mean().sqrt().item():.3e}")
+    assert e_ours.max() <= 1.5 * e_eager.max()
+    assert e_ours.pow(2).mean() <= 1.1 ** 2 * e_eager.pow(2).mean()

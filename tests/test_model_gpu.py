@@ -47,6 +47,7 @@ def _uninstall(model):
             m.forward = m._fd_mlp_original_forward
             delattr(m, "_fd_mlp_original_forward")
             del m._buffers["_fd_gate_up_weight"]
+            m._buffers.pop("_fd_gate_up_weight2", None)
 
 
 def test_install_counts_and_fallback(full_model):
