@@ -23,7 +23,8 @@
 //      l2norm, cumsum, the Gram and q.k tiles on bf16 MFMA (the normalised q/k
 //      are bf16 values, so these products are exact before fp32 accumulation),
 //      then u and w as the solutions of (I + L) x = rhs by forward substitution,
-//      one right-hand-side column per thread (256 columns: 128 of u, 128 of w).
+//      one right-hand-side column per thread (256 columns: 128 of u, 128 of w),
+//      in four 16-row blocks; each finished block is stored while the next runs.
 //   3. gd_state_kernel — one workgroup per (request, value head, 16 value
 //      columns): the only sequential part.  Each state column evolves on its
 //      own, so the 128 value columns split over 8 workgroups.  The state slice
@@ -238,8 +239,6 @@ constexpr int kPrepG = kPrepL + kC * kRowF * 4;             // fp32 [64]  gc
 constexpr int kPrepB = kPrepG + kC * 4;                     // fp32 [64]  beta
 constexpr int kPrepBG = kPrepB + kC * 4;                    // fp32 [64]  beta e^gc
 constexpr int kPrepBytes = kPrepBG + kC * 4;
-constexpr int kRowT = kD + 4;    // fp32 row stride of the u / w staging tiles (reuse the q/k/v/L area)
-static_assert(2 * kC * kRowT * 4 <= kPrepG, "u and w staging tiles must fit below the g / beta vectors");
 
 // One workgroup per (chunk, value head).  u = T (beta v) and w = T (beta e^gc k)
 // are the solutions of (I + L) x = rhs; thread j < 128 solves for column j of
@@ -383,6 +382,8 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
   }
   __syncthreads();  // every wave has read its right-hand sides: the q/k/v tiles are free
   float* wl = reinterpret_cast<float*>(smem) + wv * (48 * 64);  // 12 KiB per wave
+  uint16_t* gw = a.w + hc * 3 * kC * kD;
+  float* gu = a.u + hc * kC * kD;
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     const int b0 = 16 * b;
@@ -397,10 +398,41 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
           if (i0 + e > m) x[i0 + e] = fmaf(-lv[e], xm, x[i0 + e]);
       }
     }
-    if (b == 3) break;
     // X_block (16 rows of the wave's 64 columns) -> LDS [16][64]
 #pragma unroll
     for (int k = 0; k < 16; ++k) wl[k * 64 + l] = x[b0 + k];
+    // These 16 rows of u or w are final: store them now, in the state pass's
+    // operand order, so the writes drain while the later blocks run.
+    if (is_w) {
+      // w piece (row 16b + lane%16, columns 32c + 8(lane/16) .. +7) as three exact bf16 planes;
+      // this wave holds the column groups c = 2(wv-2), 2(wv-2)+1
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch) {
+        const int q = (b << 8) | ((2 * (wv - 2) + ch) << 6) | l;
+        const float* src_row = wl + (l & 15) * 64 + 32 * ch + 8 * (l >> 4);
+        const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(src_row);
+        const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(src_row + 4);
+        const float va[4] = {v0[0], v0[1], v0[2], v0[3]};
+        const float vb[4] = {v1[0], v1[1], v1[2], v1[3]};
+        uint2 ha, ma, la, hb, mb, lb;
+        split3x4(va, ha, ma, la);
+        split3x4(vb, hb, mb, lb);
+        *reinterpret_cast<uint4*>(gw + q * 8) = make_uint4(ha.x, ha.y, hb.x, hb.y);
+        *reinterpret_cast<uint4*>(gw + kC * kD + q * 8) = make_uint4(ma.x, ma.y, mb.x, mb.y);
+        *reinterpret_cast<uint4*>(gw + 2 * kC * kD + q * 8) = make_uint4(la.x, la.y, lb.x, lb.y);
+      }
+    } else {
+      // u piece (rows 16b + 4(lane/16) .. +3, column 16g + lane%16) in fp32;
+      // this wave holds the column groups g = 4wv .. 4wv+3
+#pragma unroll
+      for (int cg = 0; cg < 4; ++cg) {
+        const int q = ((4 * wv + cg) << 8) | (b << 6) | l;
+        const float* src_col = wl + 4 * (l >> 4) * 64 + 16 * cg + (l & 15);
+        const f32x4_t v = {src_col[0], src_col[64], src_col[128], src_col[192]};
+        *reinterpret_cast<f32x4_t*>(gu + q * 4) = v;
+      }
+    }
+    if (b == 3) break;
     // C[rest rows][64 columns] = L[rest, block] X_block: rest row tile rt (16 rows), column tile t
     constexpr int kMaxRt = 3;
     const int nrt = 3 - b;
@@ -435,16 +467,6 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
 #pragma unroll
     for (int i = b0 + 16; i < kC; ++i) x[i] = x[i] - wl[(i - b0 - 16) * 64 + l];
   }
-  // u and w through LDS (the q/k/v/L tiles are dead after this barrier), then
-  // out in the state pass's operand order with 16-byte stores
-  __syncthreads();
-  float* tU = reinterpret_cast<float*>(smem);   // [64][kRowT] u
-  float* tW = tU + kC * kRowT;                  // [64][kRowT] w
-  {
-    float* dst = (is_w ? tW : tU) + j;
-#pragma unroll
-    for (int i = 0; i < kC; ++i) dst[i * kRowT] = x[i];
-  }
   if (is_w) {
     // normalised k^T in the state pass's operand order: row dk = j, the 8 tokens
     // 32st + 8g4 .. +7 of lane 16g4 + (j % 16) (16 lanes write 256 B contiguous)
@@ -458,36 +480,6 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
         *reinterpret_cast<uint4*>(kt + ((((kwv * 2 + km) * 2 + st) * 64) + 16 * g + kc16) * 8) =
             make_uint4(kbits[i], kbits[i + 1], kbits[i + 2], kbits[i + 3]);
       }
-  }
-  __syncthreads();
-  uint16_t* gw = a.w + hc * 3 * kC * kD;
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int q = tid + kThreads * it;  // (wv, st, lane) of one 8-value piece
-    const int lane = q & 63;
-    const int row = 16 * (q >> 8) + (lane & 15);
-    const int col = 32 * ((q >> 6) & 3) + 8 * (lane >> 4);
-    const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(tW + row * kRowT + col);
-    const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(tW + row * kRowT + col + 4);
-    const float va[4] = {v0[0], v0[1], v0[2], v0[3]};
-    const float vb[4] = {v1[0], v1[1], v1[2], v1[3]};
-    uint2 ha, ma, la, hb, mb, lb;
-    split3x4(va, ha, ma, la);
-    split3x4(vb, hb, mb, lb);
-    *reinterpret_cast<uint4*>(gw + q * 8) = make_uint4(ha.x, ha.y, hb.x, hb.y);
-    *reinterpret_cast<uint4*>(gw + kC * kD + q * 8) = make_uint4(ma.x, ma.y, mb.x, mb.y);
-    *reinterpret_cast<uint4*>(gw + 2 * kC * kD + q * 8) = make_uint4(la.x, la.y, lb.x, lb.y);
-  }
-  float* gu = a.u + hc * kC * kD;
-#pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    const int q = tid + kThreads * it;  // (js, wv, lane) of one 4-value piece
-    const int lane = q & 63;
-    const int row = 16 * ((q >> 6) & 3) + 4 * (lane >> 4);
-    const int col = 16 * (q >> 8) + (lane & 15);
-    const f32x4_t v = {tU[row * kRowT + col], tU[(row + 1) * kRowT + col], tU[(row + 2) * kRowT + col],
-                       tU[(row + 3) * kRowT + col]};
-    *reinterpret_cast<f32x4_t*>(gu + q * 4) = v;
   }
 }
 
