@@ -36,6 +36,7 @@ struct PrologueArgs {
   uint16_t* k_out;
   int64_t rows;  // tokens * (q_heads + kv_heads)
   int hq, hkv, rot, w_f32, gain_offset;
+  int w_vec;  // both gain vectors 16-byte aligned: each lane loads its 8 gains as vectors
   float eps;
 };
 
@@ -69,12 +70,32 @@ __global__ __launch_bounds__(kThreads) void attn_prologue_kernel(PrologueArgs a)
   s = s + __shfl_xor(s, 1);
   const float inv = 1.0f / __builtin_sqrtf(s / static_cast<float>(kD) + a.eps);
   const void* w = isq ? a.q_w : a.k_w;
+  float gw[8];
+  if (a.w_vec) {
+    if (a.w_f32) {
+      const float4 g0 = *reinterpret_cast<const float4*>(static_cast<const float*>(w) + ln * 8);
+      const float4 g1 = *reinterpret_cast<const float4*>(static_cast<const float*>(w) + ln * 8 + 4);
+      gw[0] = g0.x; gw[1] = g0.y; gw[2] = g0.z; gw[3] = g0.w;
+      gw[4] = g1.x; gw[5] = g1.y; gw[6] = g1.z; gw[7] = g1.w;
+    } else {
+      const uint4 gr = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(w) + ln * 8);
+      const uint32_t gd[4] = {gr.x, gr.y, gr.z, gr.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        gw[2 * i] = fd_lo(gd[i]);
+        gw[2 * i + 1] = fd_hi(gd[i]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      gw[e] = a.w_f32 ? static_cast<const float*>(w)[ln * 8 + e]
+                      : fd_bf16_to_f32(static_cast<const uint16_t*>(w)[ln * 8 + e]);
+  }
   float y[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    float g = a.w_f32 ? static_cast<const float*>(w)[ln * 8 + e]
-                      : fd_bf16_to_f32(static_cast<const uint16_t*>(w)[ln * 8 + e]);
-    if (a.gain_offset) g = 1.0f + g;
+    const float g = a.gain_offset ? 1.0f + gw[e] : gw[e];
     y[e] = bf16r((x[e] * inv) * g);
   }
   if (a.rot > 0) {
@@ -160,6 +181,7 @@ extern "C" FD_API int fd_attn_prologue_fwd(const void* q_in, int64_t q_token_str
   a.rot = rotary_dim;
   a.w_f32 = weight_dtype == FD_DTYPE_F32;
   a.gain_offset = gain_offset != 0;
+  a.w_vec = fd_aligned16(q_weight) && fd_aligned16(k_weight);
   a.eps = eps;
   hipLaunchKernelGGL(attn_prologue_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), a);
