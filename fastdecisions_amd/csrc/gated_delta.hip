@@ -85,6 +85,7 @@ struct GdArgs {
   int64_t z_ts, z_hs;
   const void* nw;  // [128] norm weight, bf16 or fp32 (nw_f32)
   int nw_f32;
+  int nw_vec;      // nw 16-byte aligned: each lane loads its 8 weights as vectors
   float norm_eps;
 };
 
@@ -805,6 +806,21 @@ __global__ __launch_bounds__(kThreads) void gd_out_kernel(GdArgs a) {
   //   out = bf16(y2 * z / (1 + exp(-z)))
   __syncthreads();
   const int ln = tid & 15;
+  // this lane's 8 norm weights, as fp32 values
+  float nwv[8];
+  if (a.nw_vec && a.nw_f32) {
+    const float4 w0 = *reinterpret_cast<const float4*>(static_cast<const float*>(a.nw) + ln * 8);
+    const float4 w1 = *reinterpret_cast<const float4*>(static_cast<const float*>(a.nw) + ln * 8 + 4);
+    nwv[0] = w0.x; nwv[1] = w0.y; nwv[2] = w0.z; nwv[3] = w0.w;
+    nwv[4] = w1.x; nwv[5] = w1.y; nwv[6] = w1.z; nwv[7] = w1.w;
+  } else if (a.nw_vec) {
+    unpack8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.nw) + ln * 8), nwv);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      nwv[e] = a.nw_f32 ? static_cast<const float*>(a.nw)[ln * 8 + e]
+                        : fd_bf16_to_f32(static_cast<const uint16_t*>(a.nw)[ln * 8 + e]);
+  }
 #pragma unroll
   for (int it = 0; it < kC / 16; ++it) {
     const int t = it * 16 + (tid >> 4);
@@ -820,8 +836,7 @@ __global__ __launch_bounds__(kThreads) void gd_out_kernel(GdArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float yn = bf16r(xv[e] * inv);
-      const float gw = a.nw_f32 ? static_cast<const float*>(a.nw)[ln * 8 + e] * yn
-                                : bf16r(fd_bf16_to_f32(static_cast<const uint16_t*>(a.nw)[ln * 8 + e]) * yn);
+      const float gw = a.nw_f32 ? nwv[e] * yn : bf16r(nwv[e] * yn);
       y[e] = gw * act[it][e];
     }
     if (t < L) *reinterpret_cast<uint4*>(a.o + static_cast<size_t>(r0 + t) * o_row + h * kD + ln * 8) = pack8(y);
@@ -970,6 +985,7 @@ int gd_run(const void* q, const void* k, const void* v, const float* g, const vo
   a.z_hs = norm ? norm->z_hs : 0;
   a.nw = norm ? norm->w : nullptr;
   a.nw_f32 = norm ? norm->w_dtype == FD_DTYPE_F32 : 0;
+  a.nw_vec = norm ? fd_aligned16(norm->w) : 0;
   a.norm_eps = norm ? norm->eps : 0.0f;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
