@@ -160,6 +160,30 @@ def test_gate_transform_argument_errors():
     assert call(rows=0) == _lib.FD_OK
 
 
+def test_joined_launch_argument_errors():
+    from fastdecisions_amd import _lib
+    lib = _lib.lib()
+    f = 1 << 20
+    conv_gate = lambda **kw: lib.fd_packed_conv_gate_fwd(
+        f, 6144, f, f, f, f, kw.get("B", 1), 16, 2048, 2048, kw.get("W", 4), None, 0,
+        kw.get("hs", f), 2048, f, kw.get("hidden", 2048), f, 1, f, 1, f, f, kw.get("heads", 16), None)
+    assert conv_gate(heads=12) == _lib.FD_ERR_UNSUPPORTED
+    assert "heads must be" in _err(lib) and "fd_packed_conv_gate_fwd" in _err(lib)
+    assert conv_gate(hidden=1536) == _lib.FD_ERR_UNSUPPORTED
+    assert conv_gate(W=5) == _lib.FD_ERR_UNSUPPORTED
+    assert conv_gate(hs=f + 8) == _lib.FD_ERR_ALIGNMENT
+    assert conv_gate(B=0) == _lib.FD_OK  # no tokens: nothing to launch
+    split = lambda **kw: lib.fd_silu_mul_split_fwd(
+        f, kw.get("s1", 8192), kw.get("w1", 4096), kw.get("g2", f), kw.get("s2", 4096), kw.get("w2", 2048),
+        kw.get("out", f), kw.get("rows", 2048), None)
+    assert split(w1=12) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert "fd_silu_mul_split_fwd" in _err(lib)
+    assert split(g2=None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert split(s2=4000) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert split(out=f + 4) == _lib.FD_ERR_ALIGNMENT
+    assert split(rows=0) == _lib.FD_OK
+
+
 def test_python_wrappers_keep_the_reference_errors_on_cpu_tensors():
     from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
     from fastdecisions_amd.packed_conv_kernel import prep_qkv
