@@ -686,7 +686,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 
 // ---------------------------------------------------------------------------
 // 4. per-chunk output: o = scale e^{gc} (q S) + A v'
-__global__ __launch_bounds__(kThreads) void gd_out_kernel(GdArgs a) {
+// output pass: 8 wavefronts, wavefront wv owns the 16 value columns 16wv .. +15
+constexpr int kOutThreads = 512;
+constexpr int kOutRows = kOutThreads / 16;  // rows one 16-lanes-per-row sweep covers
+
+__global__ __launch_bounds__(kOutThreads, 2) void gd_out_kernel(GdArgs a) {
   const int h = blockIdx.x % a.hv;
   const int c = blockIdx.x / a.hv;
   int r0, L;
@@ -708,22 +712,22 @@ __global__ __launch_bounds__(kThreads) void gd_out_kernel(GdArgs a) {
   const uint16_t* gq = a.qn + hc * kC * kD;
   const float* gaq = a.aq + hc * kC * kC;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = (tid >> 4) + 16 * i;
+  for (int i = 0; i < kC * 16 / kOutThreads; ++i) {
+    const int row = (tid >> 4) + (kOutThreads / 16) * i;
     *reinterpret_cast<uint4*>(sQ + row * kRowK + (tid & 15) * 8) =
         *reinterpret_cast<const uint4*>(gq + row * kD + (tid & 15) * 8);
-    const int idx = 4 * tid + 1024 * i;
+    const int idx = 4 * tid + 4 * kOutThreads * i;
     *reinterpret_cast<f32x4_t*>(sA + (idx >> 6) * kRowF + (idx & 63)) = *reinterpret_cast<const f32x4_t*>(gaq + idx);
   }
   if (wv == 0) sG[l] = a.gc[hc * 3 * kC + l];  // e^{gc_t}
   // the norm epilogue's gate rows and their silu(z) = z / (1 + exp(-z)), computed now so that the
-  // loads and the VALU work overlap the MFMA phase (16 lanes per row, row it * 16 + tid / 16;
+  // loads and the VALU work overlap the MFMA phase (16 lanes per row, row it * kOutRows + tid / 16;
   // rows past the chunk's end use row L - 1)
-  float act[kC / 16][8];
+  float act[kC / kOutRows][8];
   if (a.z != nullptr) {
 #pragma unroll
-    for (int it = 0; it < kC / 16; ++it) {
-      const int t = it * 16 + (tid >> 4);
+    for (int it = 0; it < kC / kOutRows; ++it) {
+      const int t = it * kOutRows + (tid >> 4);
       const int tc = t < L ? t : L - 1;
       float zv[8];
       unpack8(*reinterpret_cast<const uint4*>(a.z + static_cast<int64_t>(r0 + tc) * a.z_ts + h * a.z_hs +
@@ -749,9 +753,8 @@ __global__ __launch_bounds__(kThreads) void gd_out_kernel(GdArgs a) {
     mid = make_uint4(ma.x, ma.y, mb.x, mb.y);
     lo = make_uint4(la.x, la.y, lb.x, lb.y);
   };
-#pragma unroll 1
-  for (int nn = 0; nn < 2; ++nn) {
-    const int n = 2 * wv + nn;  // 16 value columns
+  {
+    const int n = wv;  // 16 value columns
     // B operands: S[32s + 8g4 .. +7][16n + c16] and v'[32s + 8g4 .. +7][16n + c16], stored in
     // this order by the state pass (each lane reads 32 B, a wavefront 2 KiB contiguous)
     uint4 bS[3][4], bN[3][2];
@@ -822,8 +825,8 @@ __global__ __launch_bounds__(kThreads) void gd_out_kernel(GdArgs a) {
                         : fd_bf16_to_f32(static_cast<const uint16_t*>(a.nw)[ln * 8 + e]);
   }
 #pragma unroll
-  for (int it = 0; it < kC / 16; ++it) {
-    const int t = it * 16 + (tid >> 4);
+  for (int it = 0; it < kC / kOutRows; ++it) {
+    const int t = it * kOutRows + (tid >> 4);
     const int tc = t < L ? t : L - 1;  // rows past the chunk's end compute on row L - 1 and store nothing
     float xv[8], y[8];
     unpack8(*reinterpret_cast<const uint4*>(sO + tc * kRowK + ln * 8), xv);
@@ -997,7 +1000,7 @@ int gd_run(const void* q, const void* k, const void* v, const float* g, const vo
   hipLaunchKernelGGL(gd_state_kernel, dim3(static_cast<unsigned>(nseq * v_heads * kSlices)), dim3(kThreads), 0, s,
                      a);
   if (nc > 0) {
-    hipLaunchKernelGGL(gd_out_kernel, dim3(static_cast<unsigned>(nc * v_heads)), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(gd_out_kernel, dim3(static_cast<unsigned>(nc * v_heads)), dim3(kOutThreads), 0, s, a);
   }
   return fd_check_launch("fd_gated_delta_fwd");
 }
