@@ -51,33 +51,8 @@ __device__ __forceinline__ uint32_t fd_pack2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
-// e^t for the SiLU, branch-free: t is first clamped to [-20, 89] (v_med3);
-// Cody–Waite reduction t = k*ln2 + r with ln2 split into a head of 16
-// significant bits (so k*head is exact) and a tail; degree-7 Taylor polynomial
-// of e^r on |r| <= ln2/2 in Horner form; exact scaling by 2^k (v_ldexp, k in
-// [-29, 129]: no subnormal result, overflow to +inf).  Error < 2 ulp on
-// [-20, 88.7]; identical bits on CPU and GPU since every step is one IEEE op.
-// The clamp changes nothing the SiLU can see: below -17.4, 1 + e^t == 1 in
-// fp32, and above 88.73 e^t is +inf either way.
-__device__ __forceinline__ float fd_exp_silu(float t) {
-  const float kLog2e = 1.44269502162933349609375f;
-  const float kLn2Hi = 0.693145751953125f;         // 0x3f317200
-  const float kLn2Lo = 1.428606765330187045e-06f;  // ln2 - kLn2Hi
-  t = __builtin_amdgcn_fmed3f(t, -20.0f, 89.0f);
-  const float k = __builtin_rintf(t * kLog2e);
-  float r = __builtin_fmaf(-k, kLn2Hi, t);
-  r = __builtin_fmaf(-k, kLn2Lo, r);
-  float p = 1.0f / 5040.0f;
-  p = __builtin_fmaf(p, r, 1.0f / 720.0f);
-  p = __builtin_fmaf(p, r, 1.0f / 120.0f);
-  p = __builtin_fmaf(p, r, 1.0f / 24.0f);
-  p = __builtin_fmaf(p, r, 1.0f / 6.0f);
-  p = __builtin_fmaf(p, r, 0.5f);
-  p = __builtin_fmaf(p, r, 1.0f);
-  p = __builtin_fmaf(p, r, 1.0f);
-  return __builtin_ldexpf(p, static_cast<int>(k));
-}
-
-// SiLU as the reference writes it: y / (1 + exp(-y)), correctly rounded division.
-// A NaN y gives NaN whatever the clamped exponential returns.
-__device__ __forceinline__ float fd_silu(float y) { return y / (1.0f + fd_exp_silu(-y)); }
+// SiLU exactly as PyTorch's GPU kernel evaluates it in fp32: y / (1 + expf(-y))
+// with the device expf and the correctly rounded IEEE division (no fast-math).
+// Measured on the MI355X: torch.nn.functional.silu on fp32 equals this
+// expression bit for bit on every one of 25M conv outputs.
+__device__ __forceinline__ float fd_silu(float y) { return y / (1.0f + expf(-y)); }

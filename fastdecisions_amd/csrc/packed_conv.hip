@@ -17,11 +17,18 @@
 // XCD receives one contiguous range of runs; the halo rows a run re-reads
 // were loaded by its predecessor into the same XCD's L2.
 //
-// fp32 sequence per output (the CPU restatement reproduces it bit for bit):
-//   acc = w[W-1]*x[t]; acc = fma(w[0], x[t-W+1], acc); ...; acc = fma(w[W-2], x[t-1], acc)
-//   (+ bias), then y = acc / (1 + exp(-acc)) for SiLU, one bf16 rounding.
-// The tap order is the reference's (ref: :139-177); a product of two bf16
-// values is exact in fp32, so each fma equals the multiply-then-add there.
+// Arithmetic per output, chosen to equal PyTorch's fp32 GPU path
+// (silu(conv1d(x.float(), w.float())) then one cast) bit for bit:
+//   y = fp32(exact sum of the W products w[j]*x[t-W+1+j]): the products of two
+//       bf16 values are exact, and their sum is accumulated in fp64 from +0 in
+//       tap order, which is exact for any 4 such products short of an
+//       exponent spread beyond 2^37; one rounding to fp32 (MIOpen's
+//       depthwise conv accumulates in fp64 and rounds once: measured equal on
+//       every output of the config-2 tensor, where every fp32 tap order
+//       differs on 0.3 % of them);
+//   (+ bias, one fp32 add), then y / (1 + expf(-y)) for SiLU, one bf16 rounding.
+// The taps are the reference's (ref: :139-177): w[W-1] multiplies x[t], w[j]
+// multiplies x[t-W+1+j], taps before the sequence start are zero.
 #include "fd_common.h"
 #include "gate_proj_body.h"
 
@@ -29,23 +36,22 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kNumXcd = 8;
+constexpr int kCh = 4;  // channels per thread: one 8-byte vector of bf16
 
-struct Vec8 {
-  float v[8];
+struct Vec4 {
+  float v[kCh];
 };
 
-__device__ __forceinline__ Vec8 unpack8(uint4 raw) {
-  uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-  Vec8 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    r.v[2 * i] = fd_lo(w[i]);
-    r.v[2 * i + 1] = fd_hi(w[i]);
-  }
+__device__ __forceinline__ Vec4 unpack4(uint2 raw) {
+  Vec4 r;
+  r.v[0] = fd_lo(raw.x);
+  r.v[1] = fd_hi(raw.x);
+  r.v[2] = fd_lo(raw.y);
+  r.v[3] = fd_hi(raw.y);
   return r;
 }
 
-__device__ __forceinline__ uint4 load16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ uint2 load8(const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); }
 
 // Grid: 1-D, n_col * n_runs_padded blocks (a multiple of 8).  Linear block b
 // runs on XCD b % 8; logical block L = (b % 8) * (nblocks / 8) + b / 8, so the
@@ -80,36 +86,42 @@ __device__ __forceinline__ void conv_block(int lin, int nblocks, const ConvArgs&
   const int C = 2 * key_dim + value_dim;
   const int logical = (lin % kNumXcd) * (nblocks / kNumXcd) + lin / kNumXcd;
   const int run = logical / n_col;
-  const int chunk = (logical % n_col) * kThreads + threadIdx.x;  // 8-channel chunk
-  if (run >= n_runs || chunk * 8 >= C) return;
-  const int c0 = chunk * 8;
+  const int chunk = (logical % n_col) * kThreads + threadIdx.x;  // kCh-channel chunk
+  if (run >= n_runs || chunk * kCh >= C) return;
+  const int c0 = chunk * kCh;
   const int r0 = run * RUN;
 
-  // Per-channel taps (tap WIDTH-1 multiplies the current token) and bias.
-  float wt[WIDTH][8];
+  // Per-channel taps in fp64 (exact: every bf16 value is a double); tap
+  // WIDTH-1 multiplies the current token.
+  double wd[WIDTH][kCh];
   if (WIDTH == 4) {
-    const uint4* wp = reinterpret_cast<const uint4*>(w + c0 * 4);  // 8 channels x 4 taps = 64 B
+    const uint4* wp = reinterpret_cast<const uint4*>(w + c0 * 4);  // 4 channels x 4 taps = 32 B
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      Vec8 t = unpack8(wp[i]);  // channels 2i, 2i+1, taps 0..3 each
+    for (int i = 0; i < 2; ++i) {
+      const uint4 t = wp[i];  // channels 2i, 2i+1, taps 0..3 each
+      const uint32_t u[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        wt[j][2 * i] = t.v[j];
-        wt[j][2 * i + 1] = t.v[4 + j];
+      for (int j = 0; j < 2; ++j) {
+        wd[2 * j][2 * i] = fd_lo(u[j]);
+        wd[2 * j + 1][2 * i] = fd_hi(u[j]);
+        wd[2 * j][2 * i + 1] = fd_lo(u[2 + j]);
+        wd[2 * j + 1][2 * i + 1] = fd_hi(u[2 + j]);
       }
     }
   } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int e = 0; e < kCh; ++e) {
 #pragma unroll
-      for (int j = 0; j < WIDTH; ++j) wt[j][e] = fd_bf16_to_f32(w[(c0 + e) * WIDTH + j]);
+      for (int j = 0; j < WIDTH; ++j) wd[j][e] = fd_bf16_to_f32(w[(c0 + e) * WIDTH + j]);
     }
   }
-  Vec8 bs;
-  if (HAS_BIAS) bs = unpack8(load16(bias + c0));
+  Vec4 bs;
+  if (HAS_BIAS) bs = unpack4(load8(bias + c0));
 
   // Sequence containing r0: [seg_start, seg_end).  For varlen, seg is the
-  // largest index in [0, n_seqs) with cu_seqlens[seg] <= r0.
+  // largest index in [0, n_seqs) with cu_seqlens[seg] <= r0; the offsets are
+  // clamped to [0, total_rows] so a malformed table cannot move an access
+  // outside x or the outputs.
   int seg = 0, seg_start, seg_end;
   if (cu_seqlens != nullptr) {
     int lo = 0, hi = n_seqs;
@@ -118,27 +130,11 @@ __device__ __forceinline__ void conv_block(int lin, int nblocks, const ConvArgs&
       if (cu_seqlens[mid] <= r0) lo = mid; else hi = mid;
     }
     seg = lo;
-    seg_start = cu_seqlens[seg];
-    seg_end = cu_seqlens[seg + 1];
+    seg_start = min(max(cu_seqlens[seg], 0), total_rows);
+    seg_end = min(max(cu_seqlens[seg + 1], 0), total_rows);
   } else {
     seg_start = (r0 / seq_len) * seq_len;
     seg_end = seg_start + seq_len;
-  }
-
-  // Issue every load of the run up front: WIDTH-1 halo rows + RUN rows.
-  const int r_end = min(r0 + RUN, total_rows);
-  uint4 halo[WIDTH > 1 ? WIDTH - 1 : 1];
-  const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
-#pragma unroll
-  for (int j = 0; j < WIDTH - 1; ++j) {
-    const int r = r0 - (WIDTH - 1) + j;
-    halo[j] = (r >= seg_start && r >= 0) ? load16(x + static_cast<int64_t>(r) * x_row + c0) : zero;
-  }
-  uint4 cur[RUN];
-#pragma unroll
-  for (int i = 0; i < RUN; ++i) {
-    const int r = r0 + i;
-    cur[i] = (r < r_end) ? load16(x + static_cast<int64_t>(r) * x_row + c0) : zero;
   }
 
   uint16_t* dst;
@@ -150,47 +146,79 @@ __device__ __forceinline__ void conv_block(int lin, int nblocks, const ConvArgs&
   } else {
     dst = v; dst_stride = value_dim; dst_c = c0 - 2 * key_dim;
   }
+  const uint16_t* __restrict__ xc = x + c0;
 
-  Vec8 win[WIDTH > 1 ? WIDTH - 1 : 1];
+  // One output: the W taps of row r (window values in xw, zero before the
+  // row's sequence start), bias, activation; returns the fp32 result.
+  auto tap_sum = [&](const double (&xw)[WIDTH], int e) {
+    // from +0, so an exact zero sum is +0 whatever the signs of the products
+    double acc = 0.0;
 #pragma unroll
-  for (int j = 0; j < WIDTH - 1; ++j) win[j] = unpack8(halo[j]);
+    for (int j = 0; j < WIDTH; ++j) acc = __builtin_fma(wd[j][e], xw[j], acc);
+    float t = static_cast<float>(acc);
+    if (HAS_BIAS) t = t + bs.v[e];
+    return SILU ? fd_silu(t) : t;
+  };
 
+  if (r0 + RUN <= seg_end && r0 + RUN <= total_rows) {
+    // The whole run lies in one sequence (the usual case).  Every load is
+    // issued up front: WIDTH-1 halo rows (zero before the sequence start) +
+    // RUN rows; every index below is static after unrolling.
+    uint2 raw[WIDTH - 1 + RUN];
 #pragma unroll
-  for (int i = 0; i < RUN; ++i) {
-    const int r = r0 + i;
-    if (r >= r_end) break;
-    if (r >= seg_end) {  // first token of the next sequence: restart the window
-      if (cu_seqlens != nullptr) {
-        while (seg + 1 < n_seqs && cu_seqlens[seg + 1] <= r) ++seg;
-        seg_end = cu_seqlens[seg + 1];
-      } else {
-        seg_end = (r / seq_len) * seq_len + seq_len;
-      }
-#pragma unroll
-      for (int j = 0; j < WIDTH - 1; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) win[j].v[e] = 0.0f;
+    for (int m = 0; m < WIDTH - 1 + RUN; ++m) {
+      const int r = r0 - (WIDTH - 1) + m;
+      raw[m] = (m >= WIDTH - 1 || r >= seg_start) ? load8(xc + static_cast<int64_t>(r) * x_row) : make_uint2(0u, 0u);
     }
-    const Vec8 xc = unpack8(cur[i]);
-    uint32_t o[4];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      float y2[2];
+    for (int i = 0; i < RUN; ++i) {
+      float y[kCh];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int e = 2 * p + h;
-        float acc = wt[WIDTH - 1][e] * xc.v[e];
+      for (int e = 0; e < kCh; ++e) {
+        double xw[WIDTH];
 #pragma unroll
-        for (int j = 0; j < WIDTH - 1; ++j) acc = __builtin_fmaf(wt[j][e], win[j].v[e], acc);
-        if (HAS_BIAS) acc = acc + bs.v[e];
-        y2[h] = SILU ? fd_silu(acc) : acc;
+        for (int j = 0; j < WIDTH; ++j) {
+          const uint2 u = raw[i + j];
+          xw[j] = (e & 1) ? fd_hi(e < 2 ? u.x : u.y) : fd_lo(e < 2 ? u.x : u.y);
+        }
+        y[e] = tap_sum(xw, e);
       }
-      o[p] = fd_pack2(y2[0], y2[1]);
+      *reinterpret_cast<uint2*>(dst + static_cast<int64_t>(r0 + i) * dst_stride + dst_c) =
+          make_uint2(fd_pack2(y[0], y[1]), fd_pack2(y[2], y[3]));
     }
-    *reinterpret_cast<uint4*>(dst + static_cast<int64_t>(r) * dst_stride + dst_c) = make_uint4(o[0], o[1], o[2], o[3]);
+  } else {
+    // A sequence starts inside the run, or the run passes the last row: one
+    // row at a time, with the window re-read (from L1/L2).
+    int start = seg_start;
+#pragma unroll 1
+    for (int r = r0; r < min(r0 + RUN, total_rows); ++r) {
+      if (r >= seg_end) {  // first token of the next sequence
+        if (cu_seqlens != nullptr) {
+          while (seg + 1 < n_seqs && cu_seqlens[seg + 1] <= r) ++seg;
+          start = min(max(cu_seqlens[seg], 0), total_rows);
+          seg_end = min(max(cu_seqlens[seg + 1], 0), total_rows);
+        } else {
+          start = (r / seq_len) * seq_len;
+          seg_end = start + seq_len;
+        }
+      }
+      Vec4 xv[WIDTH];
 #pragma unroll
-    for (int j = 0; j + 1 < WIDTH - 1; ++j) win[j] = win[j + 1];
-    if (WIDTH > 1) win[WIDTH > 1 ? WIDTH - 2 : 0] = xc;
+      for (int j = 0; j < WIDTH; ++j) {
+        const int src = r - (WIDTH - 1) + j;
+        xv[j] = unpack4(src >= start ? load8(xc + static_cast<int64_t>(src) * x_row) : make_uint2(0u, 0u));
+      }
+      float y[kCh];
+#pragma unroll
+      for (int e = 0; e < kCh; ++e) {
+        double xw[WIDTH];
+#pragma unroll
+        for (int j = 0; j < WIDTH; ++j) xw[j] = xv[j].v[e];
+        y[e] = tap_sum(xw, e);
+      }
+      *reinterpret_cast<uint2*>(dst + static_cast<int64_t>(r) * dst_stride + dst_c) =
+          make_uint2(fd_pack2(y[0], y[1]), fd_pack2(y[2], y[3]));
+    }
   }
 }
 
@@ -243,7 +271,7 @@ int launch_run(const char* who, const void* x, int64_t x_row, const void* w, con
                void* v, int total_rows, int seq_len, int key_dim, int value_dim, const int32_t* cu, int n_seqs,
                int act, const GateSpec* gate, hipStream_t stream) {
   const int C = 2 * key_dim + value_dim;
-  const int chunks = C / 8;
+  const int chunks = C / kCh;
   const int n_runs = (total_rows + RUN - 1) / RUN;
   const int n_col = (chunks + kThreads - 1) / kThreads;
   int64_t nblocks = static_cast<int64_t>(n_col) * n_runs;

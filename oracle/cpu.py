@@ -22,8 +22,8 @@ def _lib() -> ctypes.CDLL:
             _build.build()
         lib = ctypes.CDLL(str(_LIB_PATH))
         p = ctypes.c_void_p
-        lib.fd_oracle_exp_silu.restype = ctypes.c_float
-        lib.fd_oracle_exp_silu.argtypes = [ctypes.c_float]
+        lib.fd_oracle_conv_taps.restype = None
+        lib.fd_oracle_conv_taps.argtypes = [p, p, p, p, ctypes.c_int64, ctypes.c_int]
         lib.fd_oracle_silu.restype = ctypes.c_float
         lib.fd_oracle_silu.argtypes = [ctypes.c_float]
         lib.fd_oracle_f32_to_bf16.restype = ctypes.c_uint16
@@ -59,13 +59,8 @@ def f32_to_bf16(x: np.ndarray) -> np.ndarray:
     return r
 
 
-def exp_silu(t: float) -> float:
-    """The fp32 e^t of the conv's SiLU (t clamped to [-20, 89], Cody–Waite + degree-7 Taylor)."""
-    return _lib().fd_oracle_exp_silu(float(t))
-
-
 def silu(y: float) -> float:
-    """The conv's fp32 SiLU, y / (1 + e^-y)."""
+    """The conv's fp32 SiLU, y / (1 + expf(-y)) with the C library's expf."""
     return _lib().fd_oracle_silu(float(y))
 
 
@@ -102,6 +97,19 @@ def packed_conv(x_bits: np.ndarray, w_bits: np.ndarray, bias_bits: np.ndarray | 
     if rc != 0:
         raise ValueError("oracle packed_conv rejected its arguments")
     return q, k, v
+
+
+def conv_taps(x_windows: np.ndarray, w_bits: np.ndarray, bias_bits: np.ndarray | None = None) -> np.ndarray:
+    """fp32 pre-activation of independent conv outputs: x_windows [n, W] (oldest row first)
+    and w_bits [n, W] bf16 bits, bias_bits [n] or None.  The same arithmetic as packed_conv."""
+    xw = np.ascontiguousarray(x_windows, dtype=np.uint16)
+    w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    n, width = xw.shape
+    assert w.shape == (n, width) and 1 <= width <= 4
+    bias = None if bias_bits is None else np.ascontiguousarray(bias_bits, dtype=np.uint16)
+    out = np.empty(n, np.float32)
+    _lib().fd_oracle_conv_taps(_ptr(xw), _ptr(w), _ptr(bias), _ptr(out), n, width)
+    return out
 
 
 def packed_conv_f64(x_bits: np.ndarray, w_bits: np.ndarray, bias_bits=None, *, key_dim=None, value_dim=None,

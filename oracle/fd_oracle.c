@@ -6,9 +6,10 @@
  * Plain-C restatement, in fp32 with every operation rounded where written
  * (build with -ffp-contract=off), of:
  *   - the packed causal depthwise conv1d + SiLU with head-split store
- *     (ref: src/decider/packed_conv_kernel.py:128-191: tap order :139-177,
+ *     (ref: src/decider/packed_conv_kernel.py:128-191: taps :139-177,
  *      zero taps before the sequence start :128-176, SiLU :178-182,
- *      q/k/v split :184-191);
+ *      q/k/v split :184-191), with the tap sum rounded once to fp32 as
+ *      PyTorch's fp32 GPU conv1d rounds it (BASELINE config 2's definition);
  *   - the attention prologue (per-head RMSNorm of q / k, partial rotary
  *     embedding; ref: experiments/native_gqa/bench_native_gqa_model.py:47-53);
  *   - the fused residual add + RMSNorm (ref: src/decider/residual_rms_baseline.py:48-85
@@ -53,33 +54,38 @@ uint16_t fd_oracle_f32_to_bf16(float f) {
   return (uint16_t)(u >> 16);
 }
 
-/* e^t as the conv's SiLU computes it: t clamped to [-20, 89]; Cody–Waite
- * reduction t = k ln2 + r with ln2 split into a head of 16 significant bits and
- * a tail; degree-7 Taylor polynomial of e^r in Horner form; exact scaling by
- * 2^k (k in [-29, 129]).  Every step is one IEEE fp32 operation.  The clamp is
- * invisible to the SiLU: below -17.4, 1 + e^t == 1 in fp32; above 88.73, e^t
- * overflows to +inf either way. */
-float fd_oracle_exp_silu(float t) {
-  const float log2e = 1.44269502162933349609375f;
-  const float ln2_hi = 0.693145751953125f;
-  const float ln2_lo = 1.428606765330187045e-06f;
-  t = fminf(fmaxf(t, -20.0f), 89.0f);
-  float k = rintf(t * log2e);
-  float r = fmaf(-k, ln2_hi, t);
-  r = fmaf(-k, ln2_lo, r);
-  float p = 1.0f / 5040.0f;
-  p = fmaf(p, r, 1.0f / 720.0f);
-  p = fmaf(p, r, 1.0f / 120.0f);
-  p = fmaf(p, r, 1.0f / 24.0f);
-  p = fmaf(p, r, 1.0f / 6.0f);
-  p = fmaf(p, r, 0.5f);
-  p = fmaf(p, r, 1.0f);
-  p = fmaf(p, r, 1.0f);
-  return ldexpf(p, (int)k);
+/* SiLU as PyTorch's fp32 kernel writes it and the reference restates it,
+ * y / (1 + expf(-y)) (ref: src/decider/packed_conv_kernel.py:178-182), with the
+ * C library's expf.  The device expf the GPU kernel calls is a different
+ * approximation (within 1 fp32 ulp), so on rare inputs the two SiLUs land on
+ * neighbouring bf16 values; the GPU tests bound that, and compare the kernel
+ * bit for bit with torch's own GPU silu instead. */
+float fd_oracle_silu(float y) { return y / (1.0f + expf(-y)); }
+
+/* One conv output before the activation: the exact sum of the taps
+ * w[j] * x[j] (x[0] is the oldest row; zeros stand for rows before the
+ * sequence start), rounded once to fp32, then + bias in fp32.  Each product of
+ * two bf16 values is exact in double, and so is their running sum (unless the
+ * products span more than 2^37).  Accumulated from +0 in tap order, so an
+ * exact zero is +0. */
+static float conv_taps_f32(const double* xv, const uint16_t* w, int width, const uint16_t* bias) {
+  double acc = 0.0;
+  for (int j = 0; j < width; ++j) acc = fma((double)bf16_to_f32(w[j]), xv[j], acc);
+  float t = (float)acc;
+  if (bias) t = t + bf16_to_f32(*bias);
+  return t;
 }
 
-/* SiLU as the reference writes it, y / (1 + exp(-y)) (ref: src/decider/packed_conv_kernel.py:178-182). */
-float fd_oracle_silu(float y) { return y / (1.0f + fd_oracle_exp_silu(-y)); }
+/* conv_taps_f32 over n independent windows: xwin [n, width] and w [n, width]
+ * bf16 bits, bias [n] or NULL; out [n] fp32. */
+void fd_oracle_conv_taps(const uint16_t* xwin, const uint16_t* w, const uint16_t* bias, float* out, int64_t n,
+                         int width) {
+  for (int64_t i = 0; i < n; ++i) {
+    double xv[4];
+    for (int j = 0; j < width && j < 4; ++j) xv[j] = (double)bf16_to_f32(xwin[(size_t)i * width + j]);
+    out[i] = conv_taps_f32(xv, w + (size_t)i * width, width, bias ? bias + i : NULL);
+  }
+}
 
 /* Packed causal depthwise conv1d + activation, token-major [B, T, C] input,
  * C = 2*key_dim + value_dim, weight [C, width], optional bias [C].
@@ -101,16 +107,13 @@ int fd_oracle_packed_conv(const uint16_t* x, const uint16_t* w, const uint16_t* 
       start = (r / seq_len) * seq_len;
     }
     for (int c = 0; c < C; ++c) {
-      float wt[4];
-      for (int j = 0; j < width; ++j) wt[j] = bf16_to_f32(w[(size_t)c * width + j]);
-      float acc = wt[width - 1] * bf16_to_f32(x[(size_t)r * C + c]);
-      for (int j = 0; j < width - 1; ++j) {
+      double xv[4];
+      for (int j = 0; j < width; ++j) {
         const int64_t src = r - (width - 1) + j;
-        const float xv = src >= start ? bf16_to_f32(x[(size_t)src * C + c]) : 0.0f;
-        acc = fmaf(wt[j], xv, acc);
+        xv[j] = src >= start ? (double)bf16_to_f32(x[(size_t)src * C + c]) : 0.0;
       }
-      if (bias) acc = acc + bf16_to_f32(bias[c]);
-      const float y = activation == 1 ? fd_oracle_silu(acc) : acc;
+      const float t = conv_taps_f32(xv, w + (size_t)c * width, width, bias ? bias + c : NULL);
+      const float y = activation == 1 ? fd_oracle_silu(t) : t;
       const uint16_t h = fd_oracle_f32_to_bf16(y);
       if (c < key_dim)
         q[(size_t)r * key_dim + c] = h;

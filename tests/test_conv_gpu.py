@@ -1,10 +1,12 @@
 """GPU parity of the packed causal conv1d + SiLU kernel (fd_packed_conv_fwd).
 
-Bar: bit-exact vs the oracle's documented fp32 sequence everywhere; against
-fp32 torch ``conv1d`` + SiLU then cast the mismatch count
-is reported and every mismatch is <= 1 bf16 ulp (or an absolute error below
-2^-20 where the tap sum cancels to ~0).  The reference's four unit tests
-(ref: experiments/packed_conv/check_packed_output_conv.py:48-95) run at full size.
+Bar: bit-exact against PyTorch's own fp32 GPU path,
+``silu(conv1d(x.float(), w.float(), bias.float()))`` then one bf16 cast, run per
+request for varlen inputs, on every case below.  The CPU oracle is the semantic
+pin: it computes the same exact tap sum but the C library's expf, so it agrees
+to within one bf16 ulp, on all but a few elements per million.  The reference's
+four unit tests (ref: experiments/packed_conv/check_packed_output_conv.py:48-95)
+run at full size.
 """
 from __future__ import annotations
 
@@ -23,14 +25,40 @@ def cat_bits(q, k, v):
     return np.concatenate([to_bits(t).reshape(B, T, -1) for t in (q, k, v)], axis=-1)
 
 
-def torch_fp32_conv(x, w):
+def torch_gpu_conv(x, w, bias=None, cu=None, act="silu"):
+    """PyTorch's fp32 GPU conv1d (+ SiLU), one bf16 cast; each request of a varlen batch alone.
+    Returns bf16 bits [B, T, C]."""
     C = x.shape[-1]
     W = w.reshape(C, -1).shape[1]
-    y = F.conv1d(x.float().transpose(1, 2), w.reshape(C, 1, W).float(), padding=W - 1, groups=C)[..., :x.shape[1]]
-    return F.silu(y).transpose(1, 2).to(torch.bfloat16)
+
+    def one(xs):
+        y = F.conv1d(xs.float().transpose(1, 2), w.reshape(C, 1, W).float(),
+                     None if bias is None else bias.float(), padding=W - 1, groups=C)[..., :xs.shape[1]]
+        return (F.silu(y) if act == "silu" else y).transpose(1, 2).to(torch.bfloat16)
+
+    if cu is None:
+        out = one(x)
+    else:
+        cu = [int(c) for c in cu]
+        out = torch.cat([one(x[:, a:b]) for a, b in zip(cu[:-1], cu[1:]) if b > a], dim=1)
+    return to_bits(out)
+
+
+def check(got, x, w, oracle, bias=None, cu=None, act="silu", key_dim=None, value_dim=None):
+    """got == torch's GPU result bit for bit; within one bf16 ulp of the CPU oracle."""
+    want = torch_gpu_conv(x, w, bias, cu, act)
+    assert np.array_equal(got, want), f"{int((got != want).sum())} of {got.size} differ from torch"
+    orc = np.concatenate(oracle.packed_conv(to_bits(x), to_bits(w), None if bias is None else to_bits(bias),
+                                            key_dim=key_dim, value_dim=value_dim,
+                                            cu_seqlens=None if cu is None else np.asarray(cu, np.int32),
+                                            activation=act), axis=-1)
+    d = ulp_diff(got, orc)
+    assert d.max() <= 1 and (d != 0).sum() <= max(4, got.size // 200_000), int((d != 0).sum())
+    return int((d != 0).sum())
 
 
 def test_golden_fixtures(golden, oracle):
+    """The CPU-torch golden vectors (tests/golden/conv.npz); small shapes, so exact everywhere."""
     from fastdecisions_amd.packed_conv_kernel import prep_qkv
     d = golden("conv")
     announce("conv golden batch")
@@ -51,24 +79,42 @@ def test_golden_fixtures(golden, oracle):
     assert np.array_equal(cat_bits(q, k, v), d["dec_y_fp32"])
 
 
+def test_torch_gpu_golden(golden):
+    """tests/golden/conv_torch_gpu.npz (torch's fp32 GPU conv + SiLU at config 2, written on an
+    MI355X): each fixture element, rebuilt as a 4-row window of its own channel, comes out as
+    torch's bf16, without and with a bias."""
+    from fastdecisions_amd.packed_conv_kernel import prep_qkv
+    d = golden("conv_torch_gpu")
+    for tag, bias in (("conv", None), ("bias", "bias_bias")):
+        announce(f"conv torch-gpu golden {tag}")
+        n = d[f"{tag}_x"].shape[0]
+        C = -(-n // 24) * 24
+        x = np.zeros((1, 4, C), np.uint16)
+        x[0, :, :n] = d[f"{tag}_x"].T
+        w = np.zeros((C, 4), np.uint16)
+        w[:n] = d[f"{tag}_w"]
+        b = None
+        if bias is not None:
+            b = np.zeros(C, np.uint16)
+            b[:n] = d[bias]
+        q, k, v = prep_qkv(from_bits(x), from_bits(w), None if b is None else from_bits(b),
+                           head_k_dim=8, head_v_dim=8)
+        torch.cuda.synchronize()
+        got = cat_bits(q, k, v)[0, 3, :n]
+        assert np.array_equal(got, d[f"{tag}_out"]), int((got != d[f"{tag}_out"]).sum())
+
+
 def test_config2_full_size(oracle):
-    """B=1, T=2048, C=6144, W=4, x ~ N(0,1), w ~ N(0, 0.25), bias 0, bf16."""
+    """B=1, T=2048, C=6144, W=4, x ~ N(0,1), w ~ N(0, 0.25), bias 0, bf16:
+    bit-exact against fp32 torch conv1d + SiLU on the GPU, then cast."""
     from fastdecisions_amd.packed_conv_kernel import prep_qkv
     announce("conv config2 [1,2048,6144]")
     x = seeded((1, 2048, 6144), 100).cuda()
     w = seeded((6144, 4), 101, 0.25).cuda()
     q, k, v = prep_qkv(x, w)
     torch.cuda.synchronize()
-    got = cat_bits(q, k, v)
-    want = np.concatenate(oracle.packed_conv(to_bits(x), to_bits(w)), axis=-1)
-    assert np.array_equal(got, want)
-    ref = to_bits(torch_fp32_conv(x, w))
-    diff = ulp_diff(got, ref)
-    tiny = np.abs(oracle.bf16_to_f32(got) - oracle.bf16_to_f32(ref)) < 2.0 ** -20
-    print(f"config2: vs torch fp32 conv1d+SiLU: {int((diff != 0).sum())} of {diff.size} differ; "
-          f"max {int(diff.max())} ulp")
-    assert ((diff <= 1) | tiny).all()
-    assert (diff != 0).mean() < 1e-4
+    n = check(cat_bits(q, k, v), x, w, oracle)
+    print(f"config2: 0 of {x.numel()} differ from torch fp32 conv1d+SiLU; {n} differ from the CPU oracle by 1 ulp")
 
 
 @pytest.mark.parametrize("batch", [1, 2, 4])
@@ -83,8 +129,7 @@ def test_reference_random_batches_and_weight_shapes(oracle, batch, weight_shape)
     torch.cuda.synchronize()
     for t in (q, k, v):
         assert t.shape == (batch, 2048, 16, 128) and t.is_contiguous() and t.dtype == torch.bfloat16
-    want = np.concatenate(oracle.packed_conv(to_bits(x), to_bits(w)), axis=-1)
-    assert np.array_equal(cat_bits(q, k, v), want)
+    check(cat_bits(q, k, v), x, w, oracle)
     # the reference's own tolerance vs its fp64 oracle
     exact = torch.from_numpy(oracle.bf16_to_f32(oracle.packed_conv_f64(to_bits(x), to_bits(w))))
     got = torch.from_numpy(oracle.bf16_to_f32(cat_bits(q, k, v)))
@@ -107,9 +152,8 @@ def test_reference_each_tap_and_batch_boundaries(oracle):
         w = w.cuda()
         q, k, v = prep_qkv(x, w)
         torch.cuda.synchronize()
-        want = np.concatenate(oracle.packed_conv(to_bits(x), to_bits(w)), axis=-1)
         got = cat_bits(q, k, v)
-        assert np.array_equal(got, want)
+        check(got, x, w, oracle)
         assert not (oracle.bf16_to_f32(got[1]) > 1.0).any()
 
 
@@ -141,8 +185,7 @@ def test_reference_graph_replay_with_changed_input(oracle):
         x.copy_(seeded((1, 2048, 6144), seed, 0.5).cuda())
         graph.replay()
         torch.cuda.synchronize()
-        want = np.concatenate(oracle.packed_conv(to_bits(x), to_bits(w)), axis=-1)
-        assert np.array_equal(cat_bits(*outputs), want)
+        check(cat_bits(*outputs), x, w, oracle)
 
 
 def test_varlen_requests_never_leak(oracle):
@@ -159,8 +202,7 @@ def test_varlen_requests_never_leak(oracle):
     q, k, v = prep_qkv(x, w, cu_seqlens=torch.from_numpy(cu).cuda())
     torch.cuda.synchronize()
     got = cat_bits(q, k, v)
-    want = np.concatenate(oracle.packed_conv(to_bits(x), to_bits(w), cu_seqlens=cu), axis=-1)
-    assert np.array_equal(got, want)
+    check(got, x, w, oracle, cu=cu)
     for a, b in zip(cu[:-1], cu[1:]):
         if b > a:
             qa, ka, va = prep_qkv(x[:, a:b].contiguous(), w)
@@ -180,9 +222,7 @@ def test_widths_bias_activation_and_ragged_T(oracle, width, act):
     q, k, v = prep_qkv(x, w, bias, key_dim=kd, value_dim=vd, head_k_dim=32, head_v_dim=64, activation=act)
     torch.cuda.synchronize()
     assert q.shape == (B, T, 2, 32) and v.shape == (B, T, 2, 64)
-    want = np.concatenate(oracle.packed_conv(to_bits(x), to_bits(w), to_bits(bias), key_dim=kd, value_dim=vd,
-                                             activation=act), axis=-1)
-    assert np.array_equal(cat_bits(q, k, v), want)
+    check(cat_bits(q, k, v), x, w, oracle, bias=bias, act=act, key_dim=kd, value_dim=vd)
 
 
 def test_wrapper_rejects_bad_inputs():
