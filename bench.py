@@ -130,22 +130,26 @@ def summary(us: list[float]) -> dict:
 
 # --------------------------------------------------------------------------- kernels
 
-def bench_gqa(samples: int, only: bool = False) -> dict:
+def _gqa_inputs(B, Hq, Hkv, T, D, seed=0):
+    """The decider layout: q and v token-major [B, T, H, D] viewed head-major, k head-major;
+    N(0, 1)/sqrt(D) as BASELINE config 1, cast to bf16."""
     import torch
-    import torch.nn.functional as F
-    from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
-    B, Hq, Hkv, T, D = 1, 16, 4, 2048, 128
-    g = torch.Generator().manual_seed(0)
-    # decider layout: q and v are token-major [B, T, H, D] viewed head-major, k head-major
+    g = torch.Generator().manual_seed(seed)
     q = (torch.randn((B, T, Hq, D), generator=g) / D ** 0.5).to(torch.bfloat16).cuda().permute(0, 2, 1, 3)
     k = (torch.randn((B, Hkv, T, D), generator=g) / D ** 0.5).to(torch.bfloat16).cuda()
     v = (torch.randn((B, T, Hkv, D), generator=g) / D ** 0.5).to(torch.bfloat16).cuda().permute(0, 2, 1, 3)
+    return q, k, v
+
+
+def _gqa_case(B, Hq, Hkv, T, D, samples: int, eager: bool) -> dict:
+    """HIP GQA (and, with `eager`, SDPA enable_gqa / repeat_kv) on one shape; per-launch µs."""
+    import torch.nn.functional as F
+    from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
+    q, k, v = _gqa_inputs(B, Hq, Hkv, T, D)
     flops = 4 * B * Hq * D * T * T / 2
-    bytes_ = 2 * (q.numel() + k.numel() + v.numel() + q.numel())
     reps = 10  # launches per graph: per-launch time excludes the graph launch gap
     graphs = {"hip": graph_of([lambda: native_gqa_attention(q, k, v)] * reps)}
-    backend = None
-    if not only:
+    if eager:
         def sdpa_gqa():
             return F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
 
@@ -155,17 +159,28 @@ def bench_gqa(samples: int, only: bool = False) -> dict:
             return F.scaled_dot_product_attention(q, kr, vr, is_causal=True)
         graphs["eager_sdpa_enable_gqa"] = graph_of([sdpa_gqa] * reps)
         graphs["eager_sdpa_repeat_kv"] = graph_of([sdpa_repeat] * reps)
-        backend = _sdpa_backend(q, k, v)
     times = time_graphs(graphs, {k_: reps for k_ in graphs}, samples, 2)
     res = {name: summary(t) for name, t in times.items()}
     us = res["hip"]["median_us"]
-    out = dict(config="B=1 T=2048 Hq=16 Hkv=4 D=128 bf16", bound="mfma", flops=flops, bytes=bytes_,
-               hip=res["hip"], tflops=flops / us / 1e6, peak_tflops=MFMA_BF16_PEAK_TFLOPS,
+    out = dict(config=f"B={B} T={T} Hq={Hq} Hkv={Hkv} D={D} bf16", flops=flops,
+               bytes=2 * (2 * q.numel() + k.numel() + v.numel()), hip=res["hip"], tflops=flops / us / 1e6,
                frac=flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS)
-    if not only:
+    if eager:
         base = min(res["eager_sdpa_enable_gqa"]["median_us"], res["eager_sdpa_repeat_kv"]["median_us"])
         out.update(eager_sdpa_enable_gqa=res["eager_sdpa_enable_gqa"], eager_sdpa_repeat_kv=res["eager_sdpa_repeat_kv"],
-                   sdpa_backend=backend, speedup_vs_best_eager=base / us)
+                   sdpa_backend=_sdpa_backend(q, k, v), speedup_vs_best_eager=base / us)
+    return out
+
+
+def bench_gqa(samples: int, only: bool = False) -> dict:
+    """The BASELINE GQA kernel config (B=1 T=2048 16/4x128, the roofline line), plus the shapes the
+    reference's isolated benchmark sweeps (B = 2, 4; ref: experiments/native_gqa/bench_native_gqa.py:43-61)
+    and the decider-2b checkpoint's real attention shape (8/2x256)."""
+    out = _gqa_case(1, 16, 4, 2048, 128, samples, eager=not only)
+    out.update(bound="mfma", peak_tflops=MFMA_BF16_PEAK_TFLOPS)
+    if not only:
+        out["other_shapes"] = [_gqa_case(B, Hq, Hkv, 2048, D, max(10, samples // 3), eager=True)
+                               for B, Hq, Hkv, D in ((2, 16, 4, 128), (4, 16, 4, 128), (1, 8, 2, 256))]
     return out
 
 
@@ -409,16 +424,22 @@ def cpu_baseline() -> dict:
     torch.set_num_threads(threads)
     info = reference_cpu.cpu_info()
     t0 = time.time()
-    fwd = reference_cpu.decider_forward_sample(layers=4, seq_len=2048, warmup=1, runs=3)
-    gqa = reference_cpu.gqa_config1()
-    conv = reference_cpu.conv_config2()
-    norm = reference_cpu.rmsnorm_config3()
+    # BASELINE's CPU protocol: 3 warm-ups, median of 10.  The full 28-layer forward takes ~5 s
+    # per run, so 13 runs of it do not fit a bench run of a few minutes: the sample is one
+    # period of the 3:1 layer interleave (layers 0-3), extrapolated x7 to the 28 layers.
+    fwd = reference_cpu.decider_forward_sample(layers=4, seq_len=2048, warmup=3, runs=10)
+    gqa = reference_cpu.gqa_config1(warmup=3, runs=10)
+    conv = reference_cpu.conv_config2(warmup=3, runs=10)
+    norm = reference_cpu.rmsnorm_config3(warmup=3, runs=10)
     log(f"cpu baseline took {time.time() - t0:.1f}s")
     return dict(value=fwd["scaled_forward_ms"], unit="ms", cores=torch.get_num_threads(), kind="port",
                 sample=("eager fp32 PyTorch forward of the decider-2b-shaped model (transformers Qwen3.5 layers: "
                         "SDPA, F.conv1d, eager RMSNorm, torch gated-delta rule) at B=1 T=2048 over layers 0-3 "
-                        f"(3 DeltaNet + 1 GQA), median of 3 runs = {fwd['sample_ms']:.1f} ms, scaled x7 to 28 layers"),
-                cpu_model=info["cpu_model"], cores_visible=info["cores_visible"],
+                        f"(3 DeltaNet + 1 GQA), 3 warm-ups, median of 10 runs = {fwd['sample_ms']:.1f} ms, "
+                        "scaled x7 to 28 layers"),
+                extrapolated=True, sampled_layers=fwd["layers"], total_layers=28, sample_ms=fwd["sample_ms"],
+                warmup=3, runs=10, cpu_model=info["cpu_model"], cpu_id=info["cpu_id"],
+                cores_visible=info["cores_visible"], torch_threads=torch.get_num_threads(),
                 gqa_config1_ms=gqa, conv_config2_ms=conv, rmsnorm_config3_ms=norm)
 
 

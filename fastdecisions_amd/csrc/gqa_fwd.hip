@@ -167,8 +167,9 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
 
   int seq_start, seq_end, bidx;
   if (a.cu != nullptr) {
-    seq_start = a.cu[sidx];
-    seq_end = a.cu[sidx + 1];
+    // clamped to [0, T], so a malformed offset table cannot move an access outside q/k/v/o
+    seq_start = min(max(a.cu[sidx], 0), a.seq_len);
+    seq_end = min(max(a.cu[sidx + 1], seq_start), a.seq_len);
     bidx = 0;
   } else {
     seq_start = 0;

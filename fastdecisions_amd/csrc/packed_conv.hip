@@ -309,9 +309,11 @@ int launch_run(const char* who, const void* x, int64_t x_row, const void* w, con
 #ifndef FD_CONV_RUN
 #define FD_CONV_RUN 4
 #endif
-// Tokens per thread: 4 gives 6 wavefronts per SIMD at B=1, T=2048, C=6144
-// (balanced over the 1024 SIMDs; the exact SiLU makes the kernel VALU-heavy,
-// so occupancy matters more than the 3/4 halo re-read, which hits L2).
+// Tokens per thread: 4 gives 12 wavefronts per SIMD-round at B=1, T=2048,
+// C=6144; 2 was 14 % slower, 8 and 16 no faster (measured).  The kernel is
+// VALU-bound: about 39 VALU instructions per output (the exact SiLU's expf and
+// IEEE division are about 25 of them), so the 3/4 halo re-read, which hits L2,
+// costs less than longer runs would save.
 constexpr int kRun = FD_CONV_RUN;
 
 int packed_conv_entry(const char* who, const void* x, int64_t x_row_stride, const void* weight, const void* bias,

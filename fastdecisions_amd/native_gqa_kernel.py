@@ -10,7 +10,9 @@ current stream without synchronisation.
 Differences, all widenings: head_dim 64/128/256 (the reference accepts only
 256, ref: :132-133), an optional ``scale`` (default ``D**-0.5`` as ref: :168),
 packed variable-length batches through ``cu_seqlens``/``max_seqlen``
-(B == 1, T = total tokens), with causal masking inside each request, and an
+(B == 1, T = total tokens; ``max_seqlen`` must be at least the longest
+request, whose rows past it would otherwise stay unwritten), with causal
+masking inside each request, and an
 optional output ``gate`` (logical ``[B, Hq, T, D]`` like the output): the
 attention layer's ``output * sigmoid(gate)`` applied in the kernel's store
 (``fd_gqa_gated_fwd``; ref: experiments/native_gqa/bench_native_gqa_model.py:54-55).

@@ -23,7 +23,8 @@ window at every request start.  The gated delta rule runs on the HIP kernels
 (``fastdecisions::gated_delta_rule``, per-request states from ``cu_seqlens``)
 once ``install_gated_delta_rule`` has switched the layer; otherwise it runs
 transformers' torch form, which ignores ``cu_seqlens``, once per request
-(``fd_segments``), so no state crosses a request boundary either way.
+(``fd_segments``, or the boundaries read back from ``cu_seq_lens_q`` when a
+caller passes only that), so no state crosses a request boundary either way.
 """
 from __future__ import annotations
 
@@ -79,9 +80,20 @@ def _packed_conv_gates_fake(x, weight, hidden_states, gate_weight, a_log, dt_bia
 
 
 def _segments(kwargs):
-    """Host-side request boundaries of a packed batch (a list of (start, end)), or None."""
+    """Host-side request boundaries of a packed batch (a list of (start, end)), or None.
+
+    They come from ``fd_segments`` when the caller passes them (the decider model
+    does, so graph capture never synchronises); a caller that passes only
+    ``cu_seq_lens_q`` gets them from one device-to-host copy of it, so the torch
+    delta rule below still runs once per request."""
     bounds = kwargs.get("fd_segments")
-    return None if bounds is None else list(bounds)
+    if bounds is not None:
+        return list(bounds)
+    cu = kwargs.get("cu_seq_lens_q")
+    if cu is None:
+        return None
+    c = [int(v) for v in cu.tolist()]
+    return list(zip(c[:-1], c[1:]))
 
 
 def _gate_proj_fits(self, hidden_states) -> bool:
@@ -143,13 +155,13 @@ def _forward(self, hidden_states, cache_params=None, attention_mask=None, **kwar
         a = self.in_proj_a(hidden_states)
         beta = b.sigmoid()
         g = -self.A_log.float().exp() * F.softplus(a.float() + self.dt_bias)
-    segments = _segments(kwargs)
     if getattr(self, "_fd_gated_delta", False) and getattr(self, "_fd_gated_norm", False):
         # the delta rule with the gated RMSNorm in its output pass (one kernel sequence)
         from .gated_delta import gated_delta_rule_norm
         core_attn_out = gated_delta_rule_norm(query, key, value, g, beta, z, self.norm.weight,
                                               float(self.norm.variance_epsilon), cu_seqlens)
         return self.out_proj(core_attn_out.reshape(batch, seq, -1))
+    segments = None if getattr(self, "_fd_gated_delta", False) else _segments(kwargs)
     if getattr(self, "_fd_gated_delta", False):
         from .gated_delta import gated_delta_rule
         core_attn_out = gated_delta_rule(query, key, value, g, beta, cu_seqlens)

@@ -95,7 +95,10 @@ FD_API const char* fd_last_error(void);
  * Varlen: with cu_seqlens != NULL (device int32[n_seqs + 1], non-decreasing,
  * cu_seqlens[0] == 0, cu_seqlens[n_seqs] == seq_len), batch must be 1 and the
  * T axis holds n_seqs packed requests; masking is causal within each request
- * and no request sees another.  max_seqlen (host) bounds the longest request.
+ * and no request sees another.  max_seqlen (host) must be at least the longest
+ * request: it sets the number of query tiles per request, so the rows of a
+ * longer request past max_seqlen are not written.  Offsets are clamped to
+ * [0, seq_len] on the device.
  *
  * Limits: head_dim in {64, 128, 256}; q_heads % kv_heads == 0; every base
  * pointer and every non-unit stride keeps 16-byte alignment.

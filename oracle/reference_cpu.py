@@ -26,15 +26,24 @@ import torch.nn.functional as F
 
 
 def cpu_info() -> dict:
-    model = platform.processor() or ""
+    """The host CPU as /proc/cpuinfo names it (the first processor's ``model name``, family,
+    model and stepping), with the cores this process may run on and torch's thread count."""
+    fields = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
+            if ":" not in line:
+                if fields:
+                    break  # end of the first processor's block
+                continue
+            key, val = (p.strip() for p in line.split(":", 1))
+            if key in ("model name", "cpu family", "model", "stepping", "vendor_id"):
+                fields.setdefault(key, val)
     except OSError:
         pass
-    return dict(cores_visible=len(os.sched_getaffinity(0)), torch_threads=torch.get_num_threads(), cpu_model=model)
+    return dict(cores_visible=len(os.sched_getaffinity(0)), torch_threads=torch.get_num_threads(),
+                cpu_model=fields.get("model name", platform.processor() or "unknown"),
+                cpu_id=" ".join(f"{k}={fields[k]}" for k in ("vendor_id", "cpu family", "model", "stepping")
+                                if k in fields))
 
 
 def _median_ms(fn, warmup: int, runs: int) -> float:
@@ -91,10 +100,12 @@ def rmsnorm_config3(warmup: int = 3, runs: int = 10) -> float:
 
 
 @torch.no_grad()
-def decider_forward_sample(layers: int = 4, seq_len: int = 2048, warmup: int = 1, runs: int = 3) -> dict:
+def decider_forward_sample(layers: int = 4, seq_len: int = 2048, warmup: int = 3, runs: int = 10) -> dict:
     """Eager fp32 forward of the first ``layers`` decoder layers (3 Gated-DeltaNet + 1 GQA
-    for 4) of the decider-2b-shaped model, plus embedding, final norm and readout; the
-    per-layer time is scaled to 28 layers (21 linear-attention + 7 full-attention)."""
+    for 4: one period of the 3:1 interleave) of the decider-2b-shaped model, plus
+    embedding, final norm and readout; median of ``runs`` after ``warmup``.  The time is
+    scaled to 28 layers (21 linear-attention + 7 full-attention), which counts the
+    embedding, final norm and readout 7 times (a few ms of the sample)."""
     from dataclasses import replace
 
     from fastdecisions_amd.model import DECIDER_2B_SHAPED, build_decider, synthetic_ids

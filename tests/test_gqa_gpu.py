@@ -57,6 +57,36 @@ def test_golden_fixtures(golden, oracle):
     assert np.abs(o.float().cpu().numpy() - want).max() <= ATOL
 
 
+def config1_inputs():
+    """q [1,16,1024,128], k and v [1,4,1024,128], fp32 N(0,1)/sqrt(128) drawn in the
+    order q, k, v from one generator seeded 0 (as oracle/reference_cpu.py:gqa_config1 times it)."""
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn((1, 16, 1024, 128), generator=g) / 128 ** 0.5
+    k = torch.randn((1, 4, 1024, 128), generator=g) / 128 ** 0.5
+    v = torch.randn((1, 4, 1024, 128), generator=g) / 128 ** 0.5
+    return q, k, v
+
+
+def test_config1_recipe_through_the_kernel(oracle):
+    """BASELINE config 1's exact inputs, cast to bf16, through native_gqa_attention: within 2e-2 of fp32
+    MATH SDPA on the bf16 inputs and of the fp64 oracle; and within the bf16 input-rounding error of
+    the fp32 reference path itself (SDPA on the fp32 inputs, the CPU baseline's computation)."""
+    from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
+    announce("gqa config1 B=1 T=1024 16/4x128 seed 0")
+    q32, k32, v32 = config1_inputs()
+    q, k, v = (t.to(torch.bfloat16).cuda() for t in (q32, k32, v32))
+    o = native_gqa_attention(q, k, v)
+    torch.cuda.synchronize()
+    err_sdpa = (o.float() - sdpa_fp32(q, k, v)).abs().max().item()
+    want = oracle.gqa_attention(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy())
+    err_oracle = float(np.abs(o.float().cpu().numpy() - want).max())
+    ref32 = sdpa_fp32(q32.cuda(), k32.cuda(), v32.cuda())
+    err_fp32_path = (o.float() - ref32).abs().max().item()
+    print(f"gqa config1: max abs err vs fp32 SDPA (bf16 inputs) {err_sdpa:.3e}, vs fp64 oracle {err_oracle:.3e}, "
+          f"vs the fp32-input reference {err_fp32_path:.3e}")
+    assert err_sdpa <= ATOL and err_oracle <= ATOL and err_fp32_path <= ATOL
+
+
 @pytest.mark.parametrize("recipe", ["config1_scaled", "reference_bench_unscaled"])
 def test_decider_shape_T2048(recipe, oracle):
     """B=1, T=2048, 16 q / 4 kv heads, D=128 bf16 (the BASELINE GQA kernel config)."""

@@ -83,3 +83,13 @@ def test_read_slots_matches_oracle_readout(golden):
     assert decisions(probs) == d["choice"].tolist()
     _, p = oracle.decide(d["logits"].astype(np.float32), d["nopts"])
     assert np.allclose(probs.numpy(), p, atol=1e-6)
+
+
+def test_request_segments_come_from_cu_seqlens_when_not_given():
+    """The torch delta-rule fallback of the patched Gated-DeltaNet runs once per request: with only
+    cu_seq_lens_q passed, the boundaries are read back from it; fd_segments wins when both are given."""
+    from fastdecisions_amd.packed_conv import _segments
+    cu = torch.tensor([0, 3, 3, 10], dtype=torch.int32)
+    assert _segments({"cu_seq_lens_q": cu}) == [(0, 3), (3, 3), (3, 10)]
+    assert _segments({"cu_seq_lens_q": cu, "fd_segments": ((0, 10),)}) == [(0, 10)]
+    assert _segments({}) is None
