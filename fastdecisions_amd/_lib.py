@@ -117,6 +117,12 @@ SIGNATURES = {
          ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
          ctypes.c_float, ctypes.c_int, ctypes.c_int, _c_void_p, ctypes.c_int, _c_void_p],
     ),
+    "fd_gated_delta_fwd_noalloc": (
+        ctypes.c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+         ctypes.c_float, ctypes.c_int, ctypes.c_int, _c_void_p, ctypes.c_int, _c_void_p],
+    ),
     "fd_gated_delta_norm_fwd": (
         ctypes.c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, ctypes.c_int64, ctypes.c_int64,

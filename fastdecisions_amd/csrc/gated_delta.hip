@@ -38,6 +38,8 @@
 // operands are loaded (one wavefront load = 1-2 KiB contiguous).  The MFMA
 // lane layout (v_mfma_f32_16x16x32_bf16): lane l supplies A[l%16][8(l/16)+j]
 // and B[8(l/16)+j][l%16] for j = 0..7 of each 32-step; D[4(l/16)+r][l%16].
+#include <mutex>
+
 #include "fd_common.h"
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -1007,6 +1009,52 @@ int gd_run(const void* q, const void* k, const void* v, const float* g, const vo
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Static device scratch of fd_gated_delta_fwd_noalloc: the workspace of callers
+// that cannot allocate (HIP graph capture, serving loops).  Every GPU the
+// library runs on holds its own copy for the life of the process.  Host code
+// never passes `scratch` itself to a kernel (in host code the name is a
+// host-side stand-in, not a device address): it uses the address that
+// hipGetSymbolAddress returns once per device.
+static __device__ __align__(256) unsigned char scratch[FD_GD_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device `stream` belongs to (the current
+// device for the null stream), looked up on that device's first call.
+int scratch_address(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (stream != nullptr) {
+    FD_REQUIRE(hipStreamGetDevice(stream, &dev) == hipSuccess, FD_ERR_LAUNCH,
+               "fd_gated_delta_fwd_noalloc: cannot query the stream's device");
+  } else {
+    FD_REQUIRE(hipGetDevice(&dev) == hipSuccess, FD_ERR_LAUNCH, "fd_gated_delta_fwd_noalloc: no current device");
+  }
+  FD_REQUIRE(dev >= 0 && dev < kMaxDevices, FD_ERR_UNSUPPORTED, "fd_gated_delta_fwd_noalloc: device %d out of range",
+             dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    FD_REQUIRE(hipGetDevice(&cur) == hipSuccess, FD_ERR_LAUNCH, "fd_gated_delta_fwd_noalloc: no current device");
+    if (cur != dev) FD_REQUIRE(hipSetDevice(dev) == hipSuccess, FD_ERR_LAUNCH,
+                               "fd_gated_delta_fwd_noalloc: cannot select device %d", dev);
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    FD_REQUIRE(err == hipSuccess && p != nullptr, FD_ERR_LAUNCH,
+               "fd_gated_delta_fwd_noalloc: hipGetSymbolAddress of the scratch failed: %s", hipGetErrorString(err));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FD_OK;
+}
+
+}  // namespace
+
 extern "C" FD_API int fd_gated_delta_fwd(const void* q, const void* k, const void* v, const float* g,
                                          const void* beta, void* out, const float* initial_state,
                                          float* final_state, void* workspace, int64_t workspace_bytes, int batch,
@@ -1041,4 +1089,28 @@ extern "C" FD_API int fd_gated_delta_norm_fwd(const void* q, const void* k, cons
   return gd_run(q, k, v, g, beta, out, initial_state, final_state, workspace, workspace_bytes, batch, seq_len,
                 k_heads, v_heads, head_k_dim, head_v_dim, scale, beta_dtype, l2norm_qk, cu_seqlens, n_seqs, stream,
                 &norm);
+}
+
+extern "C" FD_API int fd_gated_delta_fwd_noalloc(const void* q, const void* k, const void* v, const float* g,
+                                                 const void* beta, void* out, const float* initial_state,
+                                                 float* final_state, int batch, int seq_len, int k_heads,
+                                                 int v_heads, int head_k_dim, int head_v_dim, float scale,
+                                                 int beta_dtype, int l2norm_qk, const int32_t* cu_seqlens,
+                                                 int n_seqs, void* stream) {
+  const int64_t need = fd_gated_delta_workspace_bytes(batch, seq_len, v_heads, head_k_dim, head_v_dim,
+                                                      cu_seqlens != nullptr ? n_seqs : 0);
+  if (need < 0) {
+    return fd_set_error(static_cast<int>(need), "fd_gated_delta_fwd_noalloc: unsupported sizes (batch %d, seq_len %d, "
+                        "v_heads %d, head dims %d/%d, n_seqs %d)", batch, seq_len, v_heads, head_k_dim, head_v_dim,
+                        n_seqs);
+  }
+  FD_REQUIRE(need <= FD_GD_SCRATCH_BYTES, FD_ERR_UNSUPPORTED,
+             "fd_gated_delta_fwd_noalloc: these sizes need %lld bytes of workspace, more than the %lld-byte "
+             "static scratch (call fd_gated_delta_fwd with a workspace instead)",
+             static_cast<long long>(need), static_cast<long long>(FD_GD_SCRATCH_BYTES));
+  void* ws = nullptr;
+  const int rc = scratch_address(static_cast<hipStream_t>(stream), &ws);
+  if (rc != FD_OK) return rc;
+  return gd_run(q, k, v, g, beta, out, initial_state, final_state, ws, FD_GD_SCRATCH_BYTES, batch, seq_len, k_heads,
+                v_heads, head_k_dim, head_v_dim, scale, beta_dtype, l2norm_qk, cu_seqlens, n_seqs, stream, nullptr);
 }

@@ -278,6 +278,32 @@ FD_API int fd_gated_delta_fwd(const void* q, const void* k, const void* v, const
                               int head_v_dim, float scale, int beta_dtype, int l2norm_qk,
                               const int32_t* cu_seqlens, int n_seqs, void* stream);
 
+/* Bytes of the static device scratch fd_gated_delta_fwd_noalloc works in (128 MiB). */
+#define FD_GD_SCRATCH_BYTES 134217728LL
+
+/*
+ * fd_gated_delta_fwd without a workspace argument: the work runs in a static
+ * device array of FD_GD_SCRATCH_BYTES that the library holds on every GPU it
+ * runs on until the process ends, and the call allocates no memory.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The caller still passes inputs and outputs.
+ *
+ * Limit: fd_gated_delta_workspace_bytes of the same sizes must not exceed
+ * FD_GD_SCRATCH_BYTES (the decider's B=1, T=2048, 16-value-head call needs
+ * about 113 MiB), else FD_ERR_UNSUPPORTED.  Every call on one GPU shares that
+ * GPU's scratch: calls that overlap on one GPU (other streams, other threads)
+ * race and must be serialised by the caller.  The scratch needs no clearing:
+ * each call writes every byte it reads.  The first call on a device looks the
+ * scratch's address up with that device current (the stream's device).
+ * Other arguments, results and limits as fd_gated_delta_fwd.
+ */
+FD_API int fd_gated_delta_fwd_noalloc(const void* q, const void* k, const void* v, const float* g,
+                                      const void* beta, void* out, const float* initial_state,
+                                      float* final_state, int batch, int seq_len, int k_heads, int v_heads,
+                                      int head_k_dim, int head_v_dim, float scale, int beta_dtype,
+                                      int l2norm_qk, const int32_t* cu_seqlens, int n_seqs, void* stream);
+
 /*
  * fd_gated_delta_fwd followed by the layer's gated RMSNorm (transformers
  * Qwen3_5RMSNormGated, the call after the delta rule at ref: src/decider/packed_conv.py:60-61),

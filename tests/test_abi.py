@@ -26,7 +26,7 @@ def test_header_declares_the_expected_entry_points():
                                     "fd_slot_readout_fwd", "fd_gated_rmsnorm_fwd", "fd_silu_mul_fwd",
                                     "fd_packed_conv_strided_fwd", "fd_gated_delta_norm_fwd",
                                     "fd_gate_proj_fwd", "fd_packed_conv_gate_fwd",
-                                    "fd_silu_mul_split_fwd"}
+                                    "fd_silu_mul_split_fwd", "fd_gated_delta_fwd_noalloc"}
 
 
 def test_library_exports_every_declared_symbol_and_nothing_else():
@@ -142,6 +142,21 @@ def test_gated_delta_argument_errors():
     assert call(scale=0.0) == _lib.FD_ERR_INVALID_ARGUMENT
     assert call(work=None) == _lib.FD_ERR_INVALID_ARGUMENT
     assert call(B=0, ws=0) == _lib.FD_OK  # empty batch: nothing to launch
+
+
+def test_noalloc_delta_rule_rejects_sizes_beyond_its_static_scratch():
+    """fd_gated_delta_fwd_noalloc checks its sizes against the static scratch before any HIP call."""
+    from fastdecisions_amd import _lib
+    lib = _lib.lib()
+    f = ctypes.c_void_p(256)  # never dereferenced: the size checks come first
+    scale = ctypes.c_float(128 ** -0.5)
+    assert lib.fd_gated_delta_workspace_bytes(1, 2048, 16, 128, 128, 0) <= 134217728  # the decider call fits
+    rc = lib.fd_gated_delta_fwd_noalloc(f, f, f, f, f, f, None, None, 1, 4096, 16, 16, 128, 128, scale,
+                                        _lib.FD_DTYPE_BF16, 1, None, 0, None)
+    assert rc == _lib.FD_ERR_UNSUPPORTED and b"static scratch" in lib.fd_last_error()
+    rc = lib.fd_gated_delta_fwd_noalloc(f, f, f, f, f, f, None, None, 1, 64, 16, 16, 64, 128, scale,
+                                        _lib.FD_DTYPE_BF16, 1, None, 0, None)
+    assert rc == _lib.FD_ERR_UNSUPPORTED
 
 
 def test_gate_transform_argument_errors():
