@@ -330,6 +330,7 @@ def bench_forward(args) -> dict:
     import torch
     from fastdecisions_amd.engine import Engine, margins, read_slots
     from fastdecisions_amd.model import DECIDER_2B_SHAPED, build_decider, install_hip_kernels
+    from fastdecisions_amd.numerics import compare, fp32_copy, merge
     from fastdecisions_amd.workloads import config4_request
     t0 = time.time()
     model = build_decider(DECIDER_2B_SHAPED, seed=args.seed, device="cuda")
@@ -338,11 +339,29 @@ def bench_forward(args) -> dict:
     log(f"model built in {time.time() - t0:.1f}s; capturing the eager (reference PyTorch path) graph")
     eager_engine = Engine(model)
     ref = eager_engine.logits_all(ids).clone()
+    # model-level numerics against the fp32 forward of the same bf16 weights, on the config-4
+    # request and 7 more seeded requests (outside the timed region)
+    num_reqs = [req] + [config4_request(DECIDER_2B_SHAPED.vocab_size, seed=s) for s in range(2, 9)]
+    m32 = fp32_copy(model)
+    with torch.no_grad():
+        num_fp32 = [m32(r.ids[None].cuda()).cpu() for r in num_reqs]
+    del m32
+    torch.cuda.empty_cache()
+    num_eager = [eager_engine.logits_all(r.ids[None].cuda()).cpu() for r in num_reqs]
     counts = install_hip_kernels(model)
     log(f"installed HIP kernels {counts}; capturing the HIP graph")
     hip_engine = Engine(model)
+    num_hip = [hip_engine.logits_all(r.ids[None].cuda()).cpu() for r in num_reqs]
     got = hip_engine.logits_all(ids).clone()
     torch.cuda.synchronize()
+
+    def merged(new, old):
+        return merge([compare(n, o, [0] * len(r.slots), r.slots, r.nopts) for n, o, r in zip(new, old, num_reqs)])
+    numerics = dict(requests=len(num_reqs), slots_per_request=4, letters_per_slot=4,
+                    reference="fp32 forward of the same bf16 weights",
+                    tolerance="logits |new-old| > 0.05 + 0.02|old| counted as outside; probabilities rtol .02 atol .005",
+                    eager_bf16_vs_fp32=merged(num_eager, num_fp32), hip_bf16_vs_fp32=merged(num_hip, num_fp32),
+                    hip_vs_eager=merged(num_hip, num_eager))
     rows = [0] * len(req.slots)
     d_ref = read_slots(ref, rows, req.slots, req.nopts).argmax(-1).tolist()
     d_got = read_slots(got, rows, req.slots, req.nopts).argmax(-1).tolist()
@@ -388,7 +407,7 @@ def bench_forward(args) -> dict:
         slot_only_median_ms=statistics.median(slot_ms), decisions_slot_only=d_slots,
         decisions_eager=d_ref, decisions_hip=d_got, decisions_identical=d_ref == d_got == d_slots,
         slot_margins=[round(m, 4) for m in margins(ref, rows, req.slots, req.nopts)],
-        max_abs_logit_diff=float((got - ref).abs().max()), patched=counts)
+        max_abs_logit_diff=float((got - ref).abs().max()), numerics=numerics, patched=counts)
 
 
 def forward_only(args) -> dict:

@@ -131,7 +131,8 @@ def test_config5_packed_varlen_decisions_identical(full_model):
                   f"max|dlogit|={np.abs(got_slots[i] - ref[i][0]).max():.4f}")
             assert np.array_equal(want, have)
             assert np.array_equal(want, alone)
-            # packing must not change a request's logits beyond bf16 noise
-            assert np.abs(got_slots[i] - alone_hip[i][0]).max() < 0.25
+            # packing must not change a request's logits: measured identical; bound at the
+            # reference's logit atol
+            assert np.abs(got_slots[i] - alone_hip[i][0]).max() <= 0.05
     finally:
         _uninstall(full_model)
