@@ -38,14 +38,15 @@ SIGNATURES = {
         ctypes.c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64_4, _i64_4, _i64_4, _i64_4,
          ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
-         _c_void_p, ctypes.c_int, ctypes.c_int, _c_void_p],
+         _c_void_p, ctypes.c_int, ctypes.c_int, _c_void_p, ctypes.c_int64, _c_void_p],
     ),
     "fd_gqa_gated_fwd": (
         ctypes.c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64_4, _i64_4, _i64_4, _i64_4, _i64_4,
          ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
-         _c_void_p, ctypes.c_int, ctypes.c_int, _c_void_p],
+         _c_void_p, ctypes.c_int, ctypes.c_int, _c_void_p, ctypes.c_int64, _c_void_p],
     ),
+    "fd_gqa_workspace_bytes": (ctypes.c_int64, [ctypes.c_int] * 7),
     "fd_attn_prologue_fwd": (
         ctypes.c_int,
         [_c_void_p, ctypes.c_int64, ctypes.c_int64, _c_void_p, ctypes.c_int64, ctypes.c_int64,

@@ -54,6 +54,29 @@ __global__ __launch_bounds__(kThreads) void attn_prologue_kernel(PrologueArgs a)
   const bool isq = hh < a.hq;
   const uint16_t* src = isq ? a.q_in + t * a.q_ts + hh * a.q_hs : a.k_in + t * a.k_ts + (hh - a.hq) * a.k_hs;
   const uint4 raw = *reinterpret_cast<const uint4*>(src + ln * 8);
+  // The gains and the rotary tables do not depend on the row's values: their
+  // loads go out with the row's, so the norm waits for one round of latency.
+  const bool rot_lane = a.rot > 0 && ln < (a.rot >> 3);
+  uint4 cr = make_uint4(0u, 0u, 0u, 0u), sr = cr;
+  if (rot_lane) {
+    cr = *reinterpret_cast<const uint4*>(a.cos + t * a.rot + ln * 8);
+    sr = *reinterpret_cast<const uint4*>(a.sin + t * a.rot + ln * 8);
+  }
+  // Both gain vectors are loaded and the lane's is selected by value: a per-lane
+  // choice of pointer would become the address of a kernel-argument field and
+  // cost a dependent load round trip.
+  uint4 gr0 = make_uint4(0u, 0u, 0u, 0u), gr1 = gr0;
+  if (a.w_vec) {
+    const int gstep = a.w_f32 ? 32 : 16;  // bytes of 8 gains
+    const unsigned char* qw = static_cast<const unsigned char*>(a.q_w) + ln * gstep;
+    const unsigned char* kw = static_cast<const unsigned char*>(a.k_w) + ln * gstep;
+    const uint4 q0 = *reinterpret_cast<const uint4*>(qw), k0 = *reinterpret_cast<const uint4*>(kw);
+    gr0 = isq ? q0 : k0;
+    if (a.w_f32) {
+      const uint4 q1 = *reinterpret_cast<const uint4*>(qw + 16), k1 = *reinterpret_cast<const uint4*>(kw + 16);
+      gr1 = isq ? q1 : k1;
+    }
+  }
   const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
   float x[8];
 #pragma unroll
@@ -69,17 +92,15 @@ __global__ __launch_bounds__(kThreads) void attn_prologue_kernel(PrologueArgs a)
   s = s + __shfl_xor(s, 2);
   s = s + __shfl_xor(s, 1);
   const float inv = 1.0f / __builtin_sqrtf(s / static_cast<float>(kD) + a.eps);
-  const void* w = isq ? a.q_w : a.k_w;
   float gw[8];
   if (a.w_vec) {
     if (a.w_f32) {
-      const float4 g0 = *reinterpret_cast<const float4*>(static_cast<const float*>(w) + ln * 8);
-      const float4 g1 = *reinterpret_cast<const float4*>(static_cast<const float*>(w) + ln * 8 + 4);
-      gw[0] = g0.x; gw[1] = g0.y; gw[2] = g0.z; gw[3] = g0.w;
-      gw[4] = g1.x; gw[5] = g1.y; gw[6] = g1.z; gw[7] = g1.w;
+      gw[0] = __uint_as_float(gr0.x); gw[1] = __uint_as_float(gr0.y);
+      gw[2] = __uint_as_float(gr0.z); gw[3] = __uint_as_float(gr0.w);
+      gw[4] = __uint_as_float(gr1.x); gw[5] = __uint_as_float(gr1.y);
+      gw[6] = __uint_as_float(gr1.z); gw[7] = __uint_as_float(gr1.w);
     } else {
-      const uint4 gr = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(w) + ln * 8);
-      const uint32_t gd[4] = {gr.x, gr.y, gr.z, gr.w};
+      const uint32_t gd[4] = {gr0.x, gr0.y, gr0.z, gr0.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         gw[2 * i] = fd_lo(gd[i]);
@@ -87,6 +108,7 @@ __global__ __launch_bounds__(kThreads) void attn_prologue_kernel(PrologueArgs a)
       }
     }
   } else {
+    const void* w = isq ? a.q_w : a.k_w;
 #pragma unroll
     for (int e = 0; e < 8; ++e)
       gw[e] = a.w_f32 ? static_cast<const float*>(w)[ln * 8 + e]
@@ -104,10 +126,8 @@ __global__ __launch_bounds__(kThreads) void attn_prologue_kernel(PrologueArgs a)
     float p[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(y[e], half_lanes);
-    if (ln < (a.rot >> 3)) {
+    if (rot_lane) {
       const bool first_half = ln < half_lanes;
-      const uint4 cr = *reinterpret_cast<const uint4*>(a.cos + t * a.rot + ln * 8);
-      const uint4 sr = *reinterpret_cast<const uint4*>(a.sin + t * a.rot + ln * 8);
       const uint32_t cw[4] = {cr.x, cr.y, cr.z, cr.w};
       const uint32_t sw[4] = {sr.x, sr.y, sr.z, sr.w};
 #pragma unroll

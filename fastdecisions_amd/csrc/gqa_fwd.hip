@@ -42,6 +42,8 @@
 //   sequence have the most keys) and mapped so that each XCD receives a
 //   contiguous range of (head group, query tile) items, keeping a KV head's
 //   tiles in one L2.
+#include <algorithm>
+
 #include "fd_common.h"
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -55,12 +57,34 @@ namespace {
 constexpr int kBlockM = 32;  // queries per wavefront
 constexpr int kBlockN = 64;  // keys per LDS tile
 constexpr int kNumXcd = 8;
+constexpr int kMaxUnits = 768;  // work units per group of a split launch (kernel-argument table)
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 
+// The fields the work-item decode reads come first: a workgroup's first
+// scalar loads of its arguments then share cache lines.
 struct GqaArgs {
+  int n_items;    // work items (workgroups with work)
+  int n_qtiles;   // query tiles per (sequence, head group)
+  int n_hgroups;  // q_heads / hpw
+  int hpw;        // query heads per workgroup
+  int qpw;        // 32-query blocks per workgroup (hpw * qpw == 4)
+  int q_heads, kv_heads, seq_len;
+  // Key split of the long query tiles (padded batches with fewer work items
+  // than CUs): the n_split longest tiles of every (sequence, head group) run as
+  // two items over the two halves of their key tiles, each writing its
+  // unnormalised (o, running max, denominator) to `part`; gqa_combine_kernel
+  // merges them.
+  int n_split;    // 0: no split
+  int n_groups;   // sequences * head groups
+  int n_units;    // work units per group: n_qtiles + n_split
+  int n_pad;      // n_units rounded up to a multiple of xcd_per_group
+  int xcd_per_group;
+  float scale_log2;
+  const int32_t* cu;
+  int n_seqs;
   const uint16_t* q;
   const uint16_t* k;
   const uint16_t* v;
@@ -68,15 +92,9 @@ struct GqaArgs {
   int64_t qs[4], ks[4], vs[4], os[4];
   const uint16_t* gate;  // output gate (fd_gqa_gated_fwd) or null
   int64_t gs[4];
-  int q_heads, kv_heads, seq_len;
-  float scale_log2;
-  const int32_t* cu;
-  int n_seqs;
-  int hpw;        // query heads per workgroup
-  int qpw;        // 32-query blocks per workgroup (hpw * qpw == 4)
-  int n_qtiles;   // query tiles per (sequence, head group)
-  int n_hgroups;  // q_heads / hpw
-  int n_items;    // n_qtiles * n_hgroups * sequences
+  float* part;    // [n_groups][n_split][2][4 slots][64 lanes][D/2 + 2]
+  // units of a group, longest first: 4 * query tile + (part + 1), part -1 = whole tile
+  uint16_t units[kMaxUnits];
 };
 
 // KSPLIT = wavefronts per (head, query block): each takes 64/KSPLIT keys of a tile.
@@ -141,6 +159,45 @@ __device__ __forceinline__ float half_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Workspace slot of one (head, query block) slot x lane of a split tile's half.
+template <int D>
+__device__ __forceinline__ float* part_slot(const GqaArgs& a, int group, int qtile, int part, int w4, int lane) {
+  const size_t tile = static_cast<size_t>(group) * a.n_split + (a.n_qtiles - 1 - qtile);
+  return a.part + ((tile * 2 + part) * 4 * 64 + w4 * 64 + lane) * (D / 2 + 2);
+}
+
+// Normalised store of a lane's query row (the O^T accumulator: dims
+// 32 db + 8 r4 + 4 half + 0..3), with the optional output gate
+// bf16(o) * bf16(sigmoid(gate)), each product rounded to bf16 as the eager ops do.
+template <int D>
+__device__ __forceinline__ void store_rows(const GqaArgs& a, const f32x16_t (&o)[D / 32], float inv, bool qvalid,
+                                           uint16_t* orow, const uint16_t* grow, int half) {
+  if (!qvalid) return;
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) {
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int d = db * 32 + r4 * 8 + half * 4;
+      f32x4_t v4 = {o[db][r4 * 4 + 0] * inv, o[db][r4 * 4 + 1] * inv, o[db][r4 * 4 + 2] * inv,
+                    o[db][r4 * 4 + 3] * inv};
+      bf16x4_t ob = __builtin_convertvector(v4, bf16x4_t);
+      if (grow != nullptr) {
+        const bf16x4_t gb = *reinterpret_cast<const bf16x4_t*>(grow + d);
+        const f32x4_t gf = __builtin_convertvector(gb, f32x4_t);
+        const f32x4_t of = __builtin_convertvector(ob, f32x4_t);
+        f32x4_t sg, pr;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sg[e] = 1.0f / (1.0f + expf(-gf[e]));
+        const f32x4_t sgr = __builtin_convertvector(__builtin_convertvector(sg, bf16x4_t), f32x4_t);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pr[e] = of[e] * sgr[e];
+        ob = __builtin_convertvector(pr, bf16x4_t);
+      }
+      *reinterpret_cast<bf16x4_t*>(orow + d) = ob;
+    }
+  }
+}
+
 template <int D, int KSPLIT>
 __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
   using C = Cfg<D, KSPLIT>;
@@ -155,15 +212,34 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
   const int col = lane & 31;   // query within the wavefront's block
   const int half = lane >> 5;
 
-  // ---- work item: XCD-contiguous renumbering, longest tile first
+  // ---- work item
   const int nb = gridDim.x;
   const int b = blockIdx.x;
-  const int item = (nb % kNumXcd == 0) ? (b % kNumXcd) * (nb / kNumXcd) + b / kNumXcd : b;
-  if (item >= a.n_items) return;
-  const int j = item % a.n_qtiles;
-  const int hg = (item / a.n_qtiles) % a.n_hgroups;
-  const int sidx = item / (a.n_qtiles * a.n_hgroups);
-  const int qtile = a.n_qtiles - 1 - j;
+  int qtile, wgroup, part = -1;
+  if (a.n_split > 0) {
+    // Key split.  Block b runs on XCD b % 8; each group (one KV head's query
+    // heads of one sequence) goes to xcd_per_group XCDs, which take every
+    // xcd_per_group-th unit of its longest-first list in turn: each XCD's L2
+    // holds one KV head, and every XCD gets an equal share of long and short
+    // units, started longest first.
+    const int L = (b % kNumXcd) * (nb / kNumXcd) + b / kNumXcd;
+    wgroup = L / a.n_pad;
+    const int p = L % a.n_pad;
+    const int chunk = a.n_pad / a.xcd_per_group;
+    const int u = __builtin_amdgcn_readfirstlane((p % chunk) * a.xcd_per_group + p / chunk);
+    if (wgroup >= a.n_groups || u >= a.n_units) return;
+    const int code = a.units[u];  // uniform index: a scalar load
+    qtile = code >> 2;
+    part = (code & 3) - 1;
+  } else {
+    // XCD-contiguous renumbering, longest tile first
+    const int item = (nb % kNumXcd == 0) ? (b % kNumXcd) * (nb / kNumXcd) + b / kNumXcd : b;
+    if (item >= a.n_items) return;
+    qtile = a.n_qtiles - 1 - item % a.n_qtiles;
+    wgroup = item / a.n_qtiles;
+  }
+  const int hg = wgroup % a.n_hgroups;
+  const int sidx = wgroup / a.n_hgroups;
 
   int seq_start, seq_end, bidx;
   if (a.cu != nullptr) {
@@ -206,7 +282,10 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
   }
 
   const int kend = min(q0 + qspan, seq_end);
-  const int ntiles = (kend - seq_start + kBlockN - 1) / kBlockN;
+  const int nt_all = (kend - seq_start + kBlockN - 1) / kBlockN;
+  // key tiles [tb, tb + ntiles) of this item (a half of them for a split tile)
+  const int tb = part == 1 ? nt_all / 2 : 0;
+  const int ntiles = part == 0 ? nt_all / 2 : nt_all - tb;
 
   // ---- per-lane addressing, computed once.  LDS: [K stage 0..S-1][V stage
   // 0..S-1]; K and V reads each use one base register plus an immediate
@@ -274,7 +353,7 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
 
   // rows past the end of the sequence re-read its last row: finite data the mask discards
   auto issue_tile = [&](int t, int buf) {
-    const int ks0 = seq_start + t * kBlockN;
+    const int ks0 = seq_start + (tb + t) * kBlockN;
     unsigned char* kt = k_lds + buf * C::kTileBytes;
     unsigned char* vt = v_lds + buf * C::kTileBytes;
     const uint16_t* kg = kbase + ks0 * a.ks[2];
@@ -332,7 +411,7 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
   // the running max / denominator updated; returns the O rescale factor.
   // causal / end-of-sequence mask of tile t, on diagonal and tail tiles only
   auto mask = [&](int t, f32x16_t (&s)[C::kBlocks]) {
-    const int kb0 = seq_start + t * kBlockN + kh * C::kBlocks * 32;  // first key of this wavefront's part
+    const int kb0 = seq_start + (tb + t) * kBlockN + kh * C::kBlocks * 32;  // first key of this wavefront's part
     if (kb0 + C::kBlocks * 32 - 1 > qw0 || kb0 + C::kBlocks * 32 > seq_end) {
 #pragma unroll
       for (int bl = 0; bl < C::kBlocks; ++bl)
@@ -557,41 +636,66 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
     const float a0 = (m_run == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
     const float a1 = (m1 == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m1 - m);
     l_run = l_run * a0 + l1 * a1;
+    m_run = m;  // o and l_run are now relative to m
 #pragma unroll
     for (int db = 0; db < D / 32; ++db)
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * a0 + cmb[db * 16 + r] * a1;
   }
-  const float l_tot = half_sum(l_run);
-  const float inv = 1.0f / l_tot;
-  if (qvalid) {
-    uint16_t* orow = obase + qpos * a.os[2];
-    const uint16_t* grow = a.gate ? a.gate + bidx * a.gs[0] + qhead * a.gs[1] + qpos * a.gs[2] : nullptr;
+  if (part >= 0) {
+    // a half of a split tile: the unnormalised state goes to the workspace
+    float* dst = part_slot<D>(a, wgroup, qtile, part, w4, lane);
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db) {
+    for (int db = 0; db < D / 32; ++db)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int d = db * 32 + r4 * 8 + half * 4;
-        f32x4_t v4 = {o[db][r4 * 4 + 0] * inv, o[db][r4 * 4 + 1] * inv, o[db][r4 * 4 + 2] * inv,
-                      o[db][r4 * 4 + 3] * inv};
-        bf16x4_t ob = __builtin_convertvector(v4, bf16x4_t);
-        if (grow != nullptr) {
-          // output gate: bf16(o) * bf16(sigmoid(gate)), each product rounded to bf16 as the eager ops do
-          const bf16x4_t gb = *reinterpret_cast<const bf16x4_t*>(grow + d);
-          const f32x4_t gf = __builtin_convertvector(gb, f32x4_t);
-          const f32x4_t of = __builtin_convertvector(ob, f32x4_t);
-          f32x4_t sg, pr;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) sg[e] = 1.0f / (1.0f + expf(-gf[e]));
-          const f32x4_t sgr = __builtin_convertvector(__builtin_convertvector(sg, bf16x4_t), f32x4_t);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) pr[e] = of[e] * sgr[e];
-          ob = __builtin_convertvector(pr, bf16x4_t);
-        }
-        *reinterpret_cast<bf16x4_t*>(orow + d) = ob;
-      }
-    }
+      for (int r4 = 0; r4 < 4; ++r4)
+        *reinterpret_cast<f32x4_t*>(dst + db * 16 + r4 * 4) =
+            f32x4_t{o[db][r4 * 4], o[db][r4 * 4 + 1], o[db][r4 * 4 + 2], o[db][r4 * 4 + 3]};
+    dst[D / 2] = m_run;
+    dst[D / 2 + 1] = l_run;
+    return;
   }
+  const float l_tot = half_sum(l_run);
+  store_rows<D>(a, o, 1.0f / l_tot, qvalid, obase + qpos * a.os[2],
+                a.gate ? a.gate + bidx * a.gs[0] + qhead * a.gs[1] + qpos * a.gs[2] : nullptr, half);
+}
+
+// Merge of the two halves of every split tile (one wavefront per tile and
+// (head, query block) slot, lanes as in the main kernel): the same combine as
+// the in-workgroup merge of the key parts, then the normalised, optionally
+// gated store.
+template <int D>
+__global__ __launch_bounds__(64) void gqa_combine_kernel(GqaArgs a) {
+  const int lane = threadIdx.x;
+  const int w4 = blockIdx.x % 4;  // one wavefront per (split tile, slot): every CU takes a share
+  const int tile = blockIdx.x / 4;
+  const int group = tile / a.n_split;
+  const int qtile = a.n_qtiles - 1 - tile % a.n_split;
+  const int hg = group % a.n_hgroups;
+  const int bidx = group / a.n_hgroups;  // split tiles are padded batches only (no cu_seqlens)
+  const int qhead = hg * a.hpw + w4 % a.hpw;
+  const int qpos = qtile * kBlockM * a.qpw + (w4 / a.hpw) * kBlockM + (lane & 31);
+  const float* p0 = part_slot<D>(a, group, qtile, 0, w4, lane);
+  const float* p1 = part_slot<D>(a, group, qtile, 1, w4, lane);
+  const float m0 = p0[D / 2], l0 = p0[D / 2 + 1];
+  const float m1 = p1[D / 2], l1 = p1[D / 2 + 1];
+  const float m = fmaxf(m0, m1);
+  const float a0 = (m0 == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m0 - m);
+  const float a1 = (m1 == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m1 - m);
+  f32x16_t o[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(p0 + db * 16 + r4 * 4);
+      const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(p1 + db * 16 + r4 * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[db][r4 * 4 + e] = x0[e] * a0 + x1[e] * a1;
+    }
+  const float l_tot = half_sum(l0 * a0 + l1 * a1);
+  const bool qvalid = qpos < a.seq_len;
+  store_rows<D>(a, o, 1.0f / l_tot, qvalid, a.o + bidx * a.os[0] + qhead * a.os[1] + qpos * a.os[2],
+                a.gate ? a.gate + bidx * a.gs[0] + qhead * a.gs[1] + qpos * a.gs[2] : nullptr, lane >> 5);
 }
 
 int gcd_int(int x, int y) {
@@ -610,10 +714,72 @@ bool stride_ok(const int64_t s[4]) {
   return true;
 }
 
+// Work items below which a padded batch splits its long query tiles: fewer
+// than the 256 CUs of the MI355X, so CUs would idle (e.g. B=1, T=2048, 8/2
+// heads of 256).  At one item per CU (B=1, T=2048, 16/4 heads of 128) the
+// split measured no faster: every item carries about 5 us of fixed cost
+// (argument loads, the first tiles' latency, merge and store) against about
+// 1 us per 64-key tile, so the extra items cost what the balance saves.
+constexpr int64_t kSplitBelow = 256;
+
+// Query tiles of every (sequence, head group) that the key split halves, or 0.
+int split_tiles(int n_qtiles, int64_t items, bool varlen) {
+  if (varlen || items >= kSplitBelow || n_qtiles < 4 || n_qtiles + n_qtiles / 2 > kMaxUnits) return 0;
+  return n_qtiles / 2;
+}
+
+// The unit table of a split launch: whole tiles and halves of the n_split
+// longest, sorted by their key-tile count, longest first (the diagonal half
+// of a tile before the other), and the XCD sharing of the groups.
+void fill_units(GqaArgs& a, int qspan) {
+  struct U {
+    int len, code;
+  };
+  U list[kMaxUnits];
+  int n = 0;
+  for (int t = a.n_qtiles - 1; t >= 0; --t) {
+    const int nt = (std::min((t + 1) * qspan, a.seq_len) + kBlockN - 1) / kBlockN;
+    if (t >= a.n_qtiles - a.n_split) {
+      list[n++] = U{nt - nt / 2, 4 * t + 2};  // part 1: key tiles [nt/2, nt)
+      list[n++] = U{nt / 2, 4 * t + 1};       // part 0: key tiles [0, nt/2)
+    } else {
+      list[n++] = U{nt, 4 * t};
+    }
+  }
+  std::stable_sort(list, list + n, [](const U& x, const U& y) { return x.len > y.len; });
+  for (int i = 0; i < n; ++i) a.units[i] = static_cast<uint16_t>(list[i].code);
+  a.n_units = n;
+  a.xcd_per_group = (a.n_groups < kNumXcd && kNumXcd % a.n_groups == 0) ? kNumXcd / a.n_groups : 1;
+  a.n_pad = (n + a.xcd_per_group - 1) / a.xcd_per_group * a.xcd_per_group;
+}
+
+int64_t split_bytes(int64_t n_groups, int n_split, int head_dim) {
+  return n_groups * n_split * 2 * 4 * 64 * static_cast<int64_t>(head_dim / 2 + 2) * 4;
+}
+
+// Sizes shared by the launcher and fd_gqa_workspace_bytes.
+struct GqaShape {
+  int hpw, qpw, n_qtiles, n_hgroups, n_slots;
+  int64_t items;
+};
+GqaShape gqa_shape(int batch, int q_heads, int kv_heads, int seq_len, int n_seqs, int max_seqlen, bool varlen) {
+  GqaShape g;
+  const int group = q_heads / kv_heads;
+  g.hpw = gcd_int(group, 4);
+  g.qpw = 4 / g.hpw;
+  const int span_len = varlen ? max_seqlen : seq_len;
+  g.n_slots = varlen ? n_seqs : batch;
+  g.n_qtiles = (span_len + kBlockM * g.qpw - 1) / (kBlockM * g.qpw);
+  g.n_hgroups = q_heads / g.hpw;
+  g.items = static_cast<int64_t>(g.n_qtiles) * g.n_hgroups * g.n_slots;
+  return g;
+}
+
 int gqa_launch(const void* q, const void* k, const void* v, void* out, const int64_t q_strides[4],
                const int64_t k_strides[4], const int64_t v_strides[4], const int64_t out_strides[4],
                const void* gate, const int64_t gate_strides[4], int batch, int q_heads, int kv_heads, int seq_len,
-               int head_dim, float scale, const int32_t* cu_seqlens, int n_seqs, int max_seqlen, void* stream) {
+               int head_dim, float scale, const int32_t* cu_seqlens, int n_seqs, int max_seqlen, void* workspace,
+               int64_t workspace_bytes, void* stream) {
   FD_REQUIRE(q && k && v && out && q_strides && k_strides && v_strides && out_strides, FD_ERR_INVALID_ARGUMENT,
              "fd_gqa_fwd: tensor and stride pointers must be non-null");
   FD_REQUIRE(batch >= 0 && seq_len >= 0 && q_heads >= 1 && kv_heads >= 1, FD_ERR_INVALID_ARGUMENT,
@@ -646,7 +812,7 @@ int gqa_launch(const void* q, const void* k, const void* v, void* out, const int
   }
   if (n_slots == 0 || span_len == 0) return FD_OK;
 
-  const int group = q_heads / kv_heads;
+  const GqaShape g = gqa_shape(batch, q_heads, kv_heads, seq_len, n_seqs, max_seqlen, cu_seqlens != nullptr);
   GqaArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k);
@@ -666,12 +832,22 @@ int gqa_launch(const void* q, const void* k, const void* v, void* out, const int
   a.scale_log2 = scale * 1.4426950408889634f;
   a.cu = cu_seqlens;
   a.n_seqs = n_seqs;
-  a.hpw = gcd_int(group, 4);
-  a.qpw = 4 / a.hpw;
-  a.n_qtiles = (span_len + kBlockM * a.qpw - 1) / (kBlockM * a.qpw);
-  a.n_hgroups = q_heads / a.hpw;
-  const int64_t items = static_cast<int64_t>(a.n_qtiles) * a.n_hgroups * n_slots;
-  FD_REQUIRE(items < 2147483647LL, FD_ERR_INVALID_ARGUMENT, "fd_gqa_fwd: problem too large");
+  a.hpw = g.hpw;
+  a.qpw = g.qpw;
+  a.n_qtiles = g.n_qtiles;
+  a.n_hgroups = g.n_hgroups;
+  FD_REQUIRE(g.items < 2147483647LL / 2, FD_ERR_INVALID_ARGUMENT, "fd_gqa_fwd: problem too large");
+  a.n_groups = g.n_hgroups * g.n_slots;
+  a.n_split = split_tiles(g.n_qtiles, g.items, cu_seqlens != nullptr);
+  a.part = static_cast<float*>(workspace);
+  if (a.n_split > 0 && (workspace == nullptr || !fd_aligned16(workspace) ||
+                        workspace_bytes < split_bytes(a.n_groups, a.n_split, head_dim)))
+    a.n_split = 0;  // no room for the halves: every tile runs whole
+  int64_t items = g.items;
+  if (a.n_split > 0) {
+    fill_units(a, kBlockM * g.qpw);
+    items = static_cast<int64_t>(a.n_groups) * a.n_pad;
+  }
   a.n_items = static_cast<int>(items);
   const int nblocks = static_cast<int>((items + kNumXcd - 1) / kNumXcd * kNumXcd);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -687,6 +863,14 @@ int gqa_launch(const void* q, const void* k, const void* v, void* out, const int
       hipLaunchKernelGGL((gqa_fwd_kernel<256, 1>), grid, dim3(Cfg<256, 1>::kThreads), 0, s, a);
       break;
   }
+  if (a.n_split > 0) {
+    const dim3 cgrid(static_cast<unsigned>(a.n_groups * a.n_split * 4));
+    switch (head_dim) {
+      case 64: hipLaunchKernelGGL(gqa_combine_kernel<64>, cgrid, dim3(64), 0, s, a); break;
+      case 128: hipLaunchKernelGGL(gqa_combine_kernel<128>, cgrid, dim3(64), 0, s, a); break;
+      default: hipLaunchKernelGGL(gqa_combine_kernel<256>, cgrid, dim3(64), 0, s, a); break;
+    }
+  }
   return fd_check_launch("fd_gqa_fwd");
 }
 
@@ -695,20 +879,35 @@ int gqa_launch(const void* q, const void* k, const void* v, void* out, const int
 extern "C" int fd_gqa_fwd(const void* q, const void* k, const void* v, void* out, const int64_t q_strides[4],
                           const int64_t k_strides[4], const int64_t v_strides[4], const int64_t out_strides[4],
                           int batch, int q_heads, int kv_heads, int seq_len, int head_dim, float scale,
-                          const int32_t* cu_seqlens, int n_seqs, int max_seqlen, void* stream) {
+                          const int32_t* cu_seqlens, int n_seqs, int max_seqlen, void* workspace,
+                          int64_t workspace_bytes, void* stream) {
   return gqa_launch(q, k, v, out, q_strides, k_strides, v_strides, out_strides, nullptr, nullptr, batch, q_heads,
-                    kv_heads, seq_len, head_dim, scale, cu_seqlens, n_seqs, max_seqlen, stream);
+                    kv_heads, seq_len, head_dim, scale, cu_seqlens, n_seqs, max_seqlen, workspace, workspace_bytes,
+                    stream);
 }
 
 extern "C" int fd_gqa_gated_fwd(const void* q, const void* k, const void* v, const void* gate, void* out,
                                 const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4],
                                 const int64_t gate_strides[4], const int64_t out_strides[4], int batch,
                                 int q_heads, int kv_heads, int seq_len, int head_dim, float scale,
-                                const int32_t* cu_seqlens, int n_seqs, int max_seqlen, void* stream) {
+                                const int32_t* cu_seqlens, int n_seqs, int max_seqlen, void* workspace,
+                                int64_t workspace_bytes, void* stream) {
   FD_REQUIRE(gate && gate_strides, FD_ERR_INVALID_ARGUMENT, "fd_gqa_gated_fwd: gate and its strides must be non-null");
   FD_REQUIRE(fd_aligned16(gate) && gate_strides[3] == 1 && gate_strides[0] % 8 == 0 && gate_strides[1] % 8 == 0 &&
                  gate_strides[2] % 8 == 0,
              FD_ERR_ALIGNMENT, "fd_gqa_gated_fwd: gate must keep 16-byte rows with a unit innermost stride");
   return gqa_launch(q, k, v, out, q_strides, k_strides, v_strides, out_strides, gate, gate_strides, batch, q_heads,
-                    kv_heads, seq_len, head_dim, scale, cu_seqlens, n_seqs, max_seqlen, stream);
+                    kv_heads, seq_len, head_dim, scale, cu_seqlens, n_seqs, max_seqlen, workspace, workspace_bytes,
+                    stream);
+}
+
+extern "C" int64_t fd_gqa_workspace_bytes(int batch, int q_heads, int kv_heads, int seq_len, int head_dim,
+                                          int n_seqs, int max_seqlen) {
+  if (batch < 0 || seq_len < 0 || q_heads < 1 || kv_heads < 1 || q_heads % kv_heads != 0) return FD_ERR_INVALID_ARGUMENT;
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return FD_ERR_UNSUPPORTED;
+  const bool varlen = n_seqs > 0;
+  if (varlen && (batch != 1 || max_seqlen < 0 || max_seqlen > seq_len)) return FD_ERR_INVALID_ARGUMENT;
+  const GqaShape g = gqa_shape(batch, q_heads, kv_heads, seq_len, n_seqs, max_seqlen, varlen);
+  const int n_split = split_tiles(g.n_qtiles, g.items, varlen);
+  return n_split > 0 ? split_bytes(static_cast<int64_t>(g.n_hgroups) * g.n_slots, n_split, head_dim) : 0;
 }

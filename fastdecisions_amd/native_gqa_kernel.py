@@ -25,6 +25,20 @@ from . import _lib
 
 SUPPORTED_HEAD_DIMS = (64, 128, 256)
 
+_KEY_SPLIT = True
+
+
+def set_key_split(enabled: bool) -> bool:
+    """Turn the key split of long query tiles on (the default) or off; returns the previous setting.
+
+    With it, a padded batch with few work items (e.g. B=1, T=2048) runs the longest
+    query tiles as two halves of their key range, merged by a second launch
+    (fd_gqa_workspace_bytes).  Off, every tile runs whole, as packed varlen batches
+    always do: a request then gives bit-identical rows alone and packed."""
+    global _KEY_SPLIT
+    previous, _KEY_SPLIT = _KEY_SPLIT, bool(enabled)
+    return previous
+
 
 def native_gqa_attention(
     q: torch.Tensor,
@@ -94,16 +108,25 @@ def native_gqa_attention(
             (batch, seq_len, q_heads, head_dim), device=q.device, dtype=q.dtype
         ).permute(0, 2, 1, 3)
         lib = _lib.lib()
+        # workspace of the key split of long query tiles (0 bytes: the kernel runs unsplit)
+        nbytes = 0
+        if _KEY_SPLIT:
+            nbytes = lib.fd_gqa_workspace_bytes(batch, q_heads, kv_heads, seq_len, head_dim, n_seqs,
+                                                int(max_seqlen))
+            if nbytes < 0:
+                _lib.check("fd_gqa_workspace_bytes", nbytes)
+        work = torch.empty(nbytes, device=q.device, dtype=torch.uint8) if nbytes > 0 else None
+        ws = (None if work is None else work.data_ptr(), nbytes)
         if gate is None:
             _lib.check("fd_gqa_fwd", lib.fd_gqa_fwd(
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), output.data_ptr(),
                 _lib.strides4(q), _lib.strides4(k), _lib.strides4(v), _lib.strides4(output),
                 batch, q_heads, kv_heads, seq_len, head_dim, float(scale),
-                cu_ptr, n_seqs, int(max_seqlen), _lib.stream_handle(q.device)))
+                cu_ptr, n_seqs, int(max_seqlen), *ws, _lib.stream_handle(q.device)))
         else:
             _lib.check("fd_gqa_gated_fwd", lib.fd_gqa_gated_fwd(
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), gate.data_ptr(), output.data_ptr(),
                 _lib.strides4(q), _lib.strides4(k), _lib.strides4(v), _lib.strides4(gate), _lib.strides4(output),
                 batch, q_heads, kv_heads, seq_len, head_dim, float(scale),
-                cu_ptr, n_seqs, int(max_seqlen), _lib.stream_handle(q.device)))
+                cu_ptr, n_seqs, int(max_seqlen), *ws, _lib.stream_handle(q.device)))
     return output

@@ -60,7 +60,7 @@ extern "C" {
 #define FD_API
 #endif
 
-#define FD_ABI_VERSION 11
+#define FD_ABI_VERSION 12
 
 #define FD_OK 0
 #define FD_ERR_INVALID_ARGUMENT (-1) /* shape, size, stride or flag out of range */
@@ -100,6 +100,10 @@ FD_API const char* fd_last_error(void);
  * longer request past max_seqlen are not written.  Offsets are clamped to
  * [0, seq_len] on the device.
  *
+ * workspace / workspace_bytes: optional device memory (16-byte aligned) for
+ * the key split of long query tiles, see fd_gqa_workspace_bytes; NULL / 0 runs
+ * unsplit.  With a split the call enqueues two launches on `stream`.
+ *
  * Limits: head_dim in {64, 128, 256}; q_heads % kv_heads == 0; every base
  * pointer and every non-unit stride keeps 16-byte alignment.
  */
@@ -108,7 +112,24 @@ FD_API int fd_gqa_fwd(const void* q, const void* k, const void* v, void* out,
                const int64_t v_strides[4], const int64_t out_strides[4],
                int batch, int q_heads, int kv_heads, int seq_len, int head_dim,
                float scale, const int32_t* cu_seqlens, int n_seqs, int max_seqlen,
-               void* stream);
+               void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Bytes of device workspace with which fd_gqa_fwd / fd_gqa_gated_fwd split the
+ * key range of the long query tiles of these sizes (n_seqs = 0 for a padded
+ * batch), 0 when they run unsplit, or a negative FD_ERR_* code.
+ *
+ * Causal attention gives the query tiles near the end of a sequence up to
+ * twice the average work; when a padded batch has few work items (B=1,
+ * T=2048: one per CU), those tiles set the kernel's length.  With a workspace
+ * of at least this size the longest half of the tiles of every (sequence, head
+ * group) run as two work items over the two halves of their key tiles, and a
+ * second launch on the same stream merges the halves (their running maxima and
+ * denominators) and stores the rows.  A null or smaller workspace runs every
+ * tile whole: same results within rounding, no split.
+ */
+FD_API int64_t fd_gqa_workspace_bytes(int batch, int q_heads, int kv_heads, int seq_len, int head_dim,
+                                      int n_seqs, int max_seqlen);
 
 /*
  * fd_gqa_fwd followed by the attention layer's output gate, applied before the
@@ -124,7 +145,8 @@ FD_API int fd_gqa_gated_fwd(const void* q, const void* k, const void* v, const v
                             const int64_t v_strides[4], const int64_t gate_strides[4],
                             const int64_t out_strides[4], int batch, int q_heads, int kv_heads,
                             int seq_len, int head_dim, float scale, const int32_t* cu_seqlens,
-                            int n_seqs, int max_seqlen, void* stream);
+                            int n_seqs, int max_seqlen, void* workspace, int64_t workspace_bytes,
+                            void* stream);
 
 /*
  * Attention prologue: per-head RMSNorm of q and k over head_dim, then the

@@ -26,7 +26,8 @@ def test_header_declares_the_expected_entry_points():
                                     "fd_slot_readout_fwd", "fd_gated_rmsnorm_fwd", "fd_silu_mul_fwd",
                                     "fd_packed_conv_strided_fwd", "fd_gated_delta_norm_fwd",
                                     "fd_gate_proj_fwd", "fd_packed_conv_gate_fwd",
-                                    "fd_silu_mul_split_fwd", "fd_gated_delta_fwd_noalloc"}
+                                    "fd_silu_mul_split_fwd", "fd_gated_delta_fwd_noalloc",
+                                    "fd_gqa_workspace_bytes"}
 
 
 def test_library_exports_every_declared_symbol_and_nothing_else():
@@ -99,7 +100,7 @@ def test_gqa_argument_errors():
     bad_row = (ctypes.c_int64 * 4)(16 * 2048 * 128, 2048 * 128, 100, 1)
 
     def call(qs=good, Hq=16, Hkv=4, D=128, q=f, cu=None, n=0, mx=0, B=1, T=2048):
-        return lib.fd_gqa_fwd(q, f, f, f, qs, good, good, good, B, Hq, Hkv, T, D, 0.088, cu, n, mx, None)
+        return lib.fd_gqa_fwd(q, f, f, f, qs, good, good, good, B, Hq, Hkv, T, D, 0.088, cu, n, mx, None, 0, None)
 
     assert call(D=96) == _lib.FD_ERR_UNSUPPORTED
     assert call(Hq=15) == _lib.FD_ERR_INVALID_ARGUMENT

@@ -162,10 +162,15 @@ def test_varlen_equals_per_request():
     q, k, v = model_layout(1, 16, 4, T, 128, 1000)
     o = native_gqa_attention(q, k, v, cu_seqlens=torch.from_numpy(cu).cuda(), max_seqlen=max(lengths))
     torch.cuda.synchronize()
+    from fastdecisions_amd.native_gqa_kernel import set_key_split
     for a, b in zip(cu[:-1], cu[1:]):
         if b == a:
             continue
-        alone = native_gqa_attention(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b])
+        previous = set_key_split(False)  # whole tiles alone, as packed requests run them
+        try:
+            alone = native_gqa_attention(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b])
+        finally:
+            set_key_split(previous)
         ref = sdpa_fp32(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b])
         torch.cuda.synchronize()
         assert torch.equal(o[:, :, a:b], alone)  # same tiles relative to the request start
@@ -211,3 +216,43 @@ def test_wrapper_rejects_bad_inputs():
     kt = torch.zeros((1, 2, 128, 16), dtype=torch.bfloat16, device="cuda").transpose(2, 3)
     with pytest.raises(ValueError, match="contiguous"):
         native_gqa_attention(qt, kt, kt)
+
+
+@pytest.mark.parametrize("Hq,Hkv,T,D,gated", [(16, 4, 1024, 128, False), (16, 4, 1024, 128, True),
+                                               (8, 2, 2048, 256, False), (4, 4, 777, 64, False)])
+def test_key_split_equals_the_unsplit_kernel(Hq, Hkv, T, D, gated, oracle):
+    """Padded batches with fewer work items than CUs: with the workspace fd_gqa_workspace_bytes asks
+    for, the long query tiles run as two halves merged by a second launch; without it every tile runs
+    whole.  Both must agree to bf16 rounding (the merge order differs) and stay within the 2e-2 bar of
+    fp32 SDPA."""
+    import ctypes
+    from fastdecisions_amd import _lib
+    announce(f"gqa key split vs whole tiles B=1 T={T} {Hq}/{Hkv}x{D} gated={gated}")
+    lib = _lib.lib()
+    q, k, v = model_layout(1, Hq, Hkv, T, D, 1100 + D, D ** -0.5)
+    gate = seeded((1, T, Hq, D), 1200).cuda().permute(0, 2, 1, 3) if gated else None
+    nbytes = lib.fd_gqa_workspace_bytes(1, Hq, Hkv, T, D, 0, 0)
+    assert nbytes > 0
+    work = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    outs = []
+    for ws, wb in ((work.data_ptr(), nbytes), (None, 0)):
+        o = torch.empty((1, T, Hq, D), dtype=torch.bfloat16, device="cuda").permute(0, 2, 1, 3)
+        common = (1, Hq, Hkv, T, D, ctypes.c_float(D ** -0.5), None, 0, T, ws, wb,
+                  _lib.stream_handle(q.device))
+        if gated:
+            rc = lib.fd_gqa_gated_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), gate.data_ptr(), o.data_ptr(),
+                                      _lib.strides4(q), _lib.strides4(k), _lib.strides4(v), _lib.strides4(gate),
+                                      _lib.strides4(o), *common)
+        else:
+            rc = lib.fd_gqa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), _lib.strides4(q),
+                                _lib.strides4(k), _lib.strides4(v), _lib.strides4(o), *common)
+        _lib.check("fd_gqa_fwd", rc)
+        torch.cuda.synchronize()
+        outs.append(o.float())
+    split, whole = outs
+    diff = (split - whole).abs()
+    ulp = (whole.abs() * 2.0 ** -7).clamp_min(2.0 ** -14)  # one bf16 ulp of the value (and a floor)
+    print(f"split vs whole: max|diff| {diff.max().item():.3e}, {int((diff > 0).sum())} of {diff.numel()} differ")
+    assert (diff <= ulp).all()
+    if not gated:
+        assert (split - sdpa_fp32(q, k, v)).abs().max().item() <= ATOL

@@ -17,7 +17,8 @@ packed batch.  Bars:
   its two best letters exceeds ``CLEAR_MARGIN``, well above the bf16 noise
   both paths show against fp32 at the slots; closer slots are near-ties that
   either bf16 path can flip, and the test prints them;
-* packed requests equal the same requests run alone.
+* packed requests equal the same requests run alone (with whole query tiles,
+  as a packed batch runs them).
 """
 from __future__ import annotations
 
@@ -59,7 +60,12 @@ def runs():
         packed = model(ids, cu_seqlens=cu, segments=segments, max_seqlen=max_len).cpu()
         starts = [s for s, _ in segments]
         out["hip5_packed"] = [packed[:, s:e] for s, e in segments]
-        out["hip5_alone"] = [model(r.ids[None].cuda()).cpu() for r in c5]
+        from fastdecisions_amd.native_gqa_kernel import set_key_split
+        previous = set_key_split(False)  # whole query tiles, as the packed batch runs them
+        try:
+            out["hip5_alone"] = [model(r.ids[None].cuda()).cpu() for r in c5]
+        finally:
+            set_key_split(previous)
     torch.cuda.synchronize()
     del model
     torch.cuda.empty_cache()
