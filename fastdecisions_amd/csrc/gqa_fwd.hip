@@ -20,7 +20,9 @@
 //   are computed, one MFMA of that dependent chain after each of eight pieces
 //   of the softmax, so the VALU work issues while the MFMAs run; tiles t+2 and
 //   t+3 are in flight.  head_dim 256 (whose 4 stages would not fit the
-//   160 KiB LDS) runs tile by tile over 2 stages.
+//   160 KiB LDS) has one wavefront per SIMD walking 32-key blocks: the P·V of
+//   block j-1 and the scores of block j+1 are issued with the softmax of
+//   block j between their MFMAs, over 2-stage K and V rings.
 //   16-byte chunks are XOR-swizzled per row so that the MFMA operand reads
 //   below are bank-conflict free.
 // * The score tile is computed transposed, S^T = K · Q^T, with
@@ -43,6 +45,7 @@
 //   contiguous range of (head group, query tile) items, keeping a KV head's
 //   tiles in one L2.
 #include <algorithm>
+#include <type_traits>
 
 #include "fd_common.h"
 
@@ -109,8 +112,8 @@ struct Cfg {
   static constexpr int kStageBytes = 2 * kTileBytes;         // K tile + V tile
   // Pipelined loop (two wavefronts per (head, query block) and 4 stages in
   // LDS): the scores of tile t+1 are computed while tile t is finished, and
-  // tiles t+2, t+3 are in flight.  Otherwise a ring of 3 stages where they fit
-  // next to the merge area (tile t+2 in flight while tile t is consumed), else 2.
+  // tiles t+2, t+3 are in flight.  head_dim 256 (one wavefront per (head,
+  // query block)) has 2 stages, used as separate K and V rings.
   static constexpr bool kPipe = KSPLIT > 1 && 4 * kStageBytes <= 160 * 1024;
   static constexpr int kStages = kPipe ? 4 : 3 * kStageBytes <= 160 * 1024 ? 3 : 2;
   static constexpr int kCombineBytes = KSPLIT > 1 ? 4 * 64 * (D / 2 + 2) * 4 : 0;
@@ -274,11 +277,28 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
 
   // Q^T as MFMA B operand: lane supplies Q[qpos][16kk + 8*half + 0..7].
   bf16x8_t qf[D / 16];
+  if constexpr (D == 256 && KSPLIT == 1) {
+    // The head_dim-256 loop issues its copies and LDS reads as asm and counts
+    // them itself; the compiler, which does not see them, must not be left
+    // with loads of its own to wait for inside the loop.  So Q is read with
+    // asm too, before any copy, and the prologue's copy wait covers it.  Rows
+    // past the end read the last row and are zeroed after that wait.
+    typedef unsigned u32x4q_t __attribute__((ext_vector_type(4)));
+    const int qrow = qvalid ? qpos : seq_end - 1;
+    const uint16_t* qp = qbase + qrow * a.qs[2] + half * 8;
 #pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk) {
-    uint4 u = make_uint4(0u, 0u, 0u, 0u);
-    if (qvalid) u = *reinterpret_cast<const uint4*>(qbase + qpos * a.qs[2] + kk * 16 + half * 8);
-    qf[kk] = as_bf16x8(u);
+    for (int kk = 0; kk < D / 16; ++kk) {
+      u32x4q_t raw;
+      asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(raw) : "v"(qp), "i"(kk * 32) : "memory");
+      qf[kk] = __builtin_bit_cast(bf16x8_t, raw);
+    }
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+      uint4 u = make_uint4(0u, 0u, 0u, 0u);
+      if (qvalid) u = *reinterpret_cast<const uint4*>(qbase + qpos * a.qs[2] + kk * 16 + half * 8);
+      qf[kk] = as_bf16x8(u);
+    }
   }
 
   const int kend = min(q0 + qspan, seq_end);
@@ -407,8 +427,6 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
     }
   };
 
-  // Mask and online softmax of tile t (scores s): P as bf16 MFMA operands in pb,
-  // the running max / denominator updated; returns the O rescale factor.
   // causal / end-of-sequence mask of tile t, on diagonal and tail tiles only
   auto mask = [&](int t, f32x16_t (&s)[C::kBlocks]) {
     const int kb0 = seq_start + (tb + t) * kBlockN + kh * C::kBlocks * 32;  // first key of this wavefront's part
@@ -421,40 +439,6 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
           if (key > qpos || key >= seq_end) s[bl][r] = -__builtin_inff();
         }
     }
-  };
-
-  auto softmax = [&](int t, f32x16_t (&s)[C::kBlocks], bf16x8_t (&pb)[2 * C::kBlocks], bool& grow_any) {
-    mask(t, s);
-    // exp2 domain, lazily raised max
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int bl = 0; bl < C::kBlocks; ++bl)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[bl][r]);
-    mx = half_max(mx) * c;
-    const bool grow = mx > m_run + 8.0f;
-    const float m_new = grow ? mx : m_run;
-    const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-    const float m_sub = (m_new == -__builtin_inff()) ? 0.0f : m_new;  // fully masked so far: p = 0
-    m_run = m_new;
-    float psum = 0.0f;
-#pragma unroll
-    for (int bl = 0; bl < C::kBlocks; ++bl) {
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        f32x8_t pv;
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[bl][h2 * 8 + r], c, -m_sub));
-          psum += p;
-          pv[r] = p;
-        }
-        pb[bl * 2 + h2] = __builtin_convertvector(pv, bf16x8_t);
-      }
-    }
-    l_run = l_run * alpha + psum;
-    grow_any = __builtin_amdgcn_ballot_w64(grow) != 0;
-    return alpha;
   };
 
   // O = alpha O + V^T · P^T with V in stage BUF: the V^T A operand of each
@@ -572,49 +556,249 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
     if (t < ntiles) step(t, 0, sA, sB);
     if (t + 1 < ntiles) step(t + 1, 1, sB, sA);
     if (t + 2 < ntiles) step(t + 2, 2, sA, sB);
-  } else {
-    // Prologue: tiles 0 (and 1) in flight; wait for tile 0 only.
-    constexpr int kAhead = C::kStages - 1;  // prefetch distance in tiles
-    issue_tile(0, 0);
-    if (C::kStages == 3 && ntiles > 1) {
-      issue_tile(1, 1);
-      __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(kPerTile));
-    } else {
-      __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(0));
+  } else if constexpr (D == 256 && KSPLIT == 1) {
+    // head_dim 256: one wavefront per SIMD (4 per workgroup), each owning one
+    // head's 32 queries.  The wavefront walks the keys in 32-key blocks (block
+    // b = half b % 2 of tile b / 2) with its own online softmax per block.
+    // Block step j issues the 16 P·V MFMAs of block j-1 and the 16 score MFMAs
+    // of block j+1 alternately, and between them the softmax of block j, so
+    // the VALU work runs under the MFMAs.  K and V have 2-stage rings of whole
+    // tiles: K(u) is copied in step 2u-3 and read in steps 2u-1, 2u; V(u) is
+    // copied in step 2u-1 and read in steps 2u+1, 2u+2.  Copies and LDS
+    // operand reads are asm with explicit waits (see the Q loads).
+    constexpr int kKk = D / 16;   // 16 score MFMAs per block (and 16 P·V MFMAs)
+    constexpr int kWin = 4;       // MFMA pairs (three reads each) in flight
+    static_assert(C::kBlocks == 2 && C::kStages == 2, "head_dim 256 layout");
+    const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)smem));
+    // copy offsets: slot (i*4 + wave)*64 + lane -> row 8i + 2 wave + lane/32, chunk lane%32;
+    // the K swizzle depends on row & 15, i.e. on i & 1
+    const int crow = 2 * wave + (lane >> 5);
+    const int cchunk = lane & 31;
+    int ck_off[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) ck_off[e] = (cchunk ^ swz_k<CR>(8 * e + crow)) * 8;
+    const int cv_off = (cchunk ^ swz_v<CR>(crow)) * 8;
+    auto copy_tile = [&](int u, bool is_v) {
+      const uint32_t stage_base = lds0 + static_cast<uint32_t>(((is_v ? 2 : 0) + (u & 1)) * C::kTileBytes);
+      const int ks0 = seq_start + (tb + u) * kBlockN;
+      const uint16_t* g = is_v ? vbase + ks0 * a.vs[2] : kbase + ks0 * a.ks[2];
+      const int stride = static_cast<int>(is_v ? a.vs[2] : a.ks[2]);
+      const int last = seq_end - 1 - ks0;  // rows past the end re-read the last row: finite data the mask discards
+#pragma unroll
+      for (int i = 0; i < C::kLoads; ++i) {
+        const int r = min(8 * i + crow, last);
+        const int rel = r * stride + (is_v ? cv_off : ck_off[i & 1]);
+        const uint32_t lds = stage_base + static_cast<uint32_t>((i * C::kWaves + wave) * 1024);
+        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                     :: "v"(static_cast<uint32_t>(rel) * 2u), "s"(g), "s"(lds) : "memory", "m0");
+      }
+    };
+    // K operand (block bl of a tile, step kk): row bl*32 + sigma(col), logical chunk 2kk + half;
+    // chunk (16 hi + lo) ^ z = 16 hi + (lo ^ z): 8 lane offsets, the rest immediates
+    const int krow = sigma(col);
+    const int kz = swz_k<CR>(krow);
+    uint32_t kq[8];
+#pragma unroll
+    for (int k3 = 0; k3 < 8; ++k3) kq[k3] = lds0 + static_cast<uint32_t>(krow * CR * 16 + (((2 * k3 + half) ^ kz) * 16));
+    // V^T operand (O block db = 4 dh + d2, 16-key slice cs of the tile, half r2):
+    // row 16 cs + 8 (grp >> 1) + 4 r2 + li / 4, chunk 16 dh + 4 (d2 ^ (li / 4 & 3)) + c0
+    const int vrow = 8 * (grp >> 1) + (li >> 2);
+    const int vr = (li >> 2) & 3;
+    const int vc0 = 2 * (grp & 1) + ((li & 3) >> 1);
+    uint32_t vq[4];
+#pragma unroll
+    for (int d2 = 0; d2 < 4; ++d2)
+      vq[d2] = lds0 + static_cast<uint32_t>(2 * C::kTileBytes + vrow * CR * 16 + (4 * (d2 ^ vr) + vc0) * 16 + 8 * (li & 1));
+    typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+    typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+    const int nblk = 2 * ntiles;
+
+    // causal / end-of-sequence mask of block b, on diagonal and tail blocks only
+    auto mask_block = [&](int b, f32x16_t& s) {
+      const int kb0 = seq_start + tb * kBlockN + b * 32;
+      if (kb0 + 31 > qw0 || kb0 + 32 > seq_end) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb0 + (r >> 3) * 16 + half * 8 + (r & 7);
+          if (key > qpos || key >= seq_end) s[r] = -__builtin_inff();
+        }
+      }
+    };
+
+    // prologue: K0, K1, V0 in flight; scores of block 0 once K0 has landed
+    copy_tile(0, false);
+    if (ntiles > 1) copy_tile(1, false);
+    copy_tile(0, true);
+    if (ntiles > 1) __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(2 * C::kLoads));
+    else __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(C::kLoads));
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {  // the Q loads (older than every copy) have completed
+      asm volatile("" : "+v"(qf[kk]));
+      if (!qvalid) qf[kk] = bf16x8_t{};
     }
     __syncthreads();
+    f32x16_t S[2];   // scores of block b in S[b & 1]
+    bf16x8_t P[2][2];  // P of block b in P[b & 1] (two 16-key slices)
+    S[0] = f32x16_t{};
+#pragma unroll
+    for (int kk = 0; kk < kKk; ++kk) {
+      u32x4_t kf;
+      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(kf) : "v"(kq[kk & 7]), "i"(256 * (kk >> 3)) : "memory");
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kf) :: "memory");
+      S[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf), qf[kk], S[0], 0, 0, 0);
+    }
 
-    // One 64-key tile in LDS stage BUF (a constant after inlining where the
-    // loop is unrolled by the stage count).
-    auto tile_step = [&](int t, int BUF) {
-      const bool issued = t + kAhead < ntiles;
-      if (issued) issue_tile(t + kAhead, (BUF + kAhead) % C::kStages);
-      f32x16_t s[C::kBlocks];
-      scores(BUF, s);
-      bf16x8_t pb[2 * C::kBlocks];
-      bool grow_any;
-      const float alpha = softmax(t, s, pb, grow_any);
-      accumulate(BUF, pb, alpha, grow_any);
-      // tile t+1 must have landed (only tile t+kAhead may still be in flight);
-      // the barrier makes every thread's copies visible and frees stage BUF
-      if (C::kStages == 3 && issued)
-        __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(kPerTile));
-      else
+    // block step j: P·V of block j-1 (PV), softmax of block j (SM), scores of
+    // block j+1 (SC).  PAR = j & 1 picks the score and P registers; the LDS
+    // stage and half-tile offsets are added to the lane offsets once per step.
+    auto step = [&](auto PAR_C, auto PV_C, auto SM_C, auto SC_C, int j) {
+      constexpr int PAR = decltype(PAR_C)::value;
+      constexpr bool PV = decltype(PV_C)::value, SM = decltype(SM_C)::value, SC = decltype(SC_C)::value;
+      f32x16_t& ssm = S[PAR];             // block j
+      f32x16_t& ssc = S[PAR ^ 1];         // block j+1
+      bf16x8_t (&ppv)[2] = P[PAR ^ 1];    // block j-1
+      bf16x8_t (&psm)[2] = P[PAR];        // block j
+      // K of block j+1: tile (j+1)/2 in stage ((j+1)/2) & 1, half (j+1) & 1;
+      // V of block j-1: tile (j-1)/2, half (j-1) & 1 (its 16-key slices 2 half, 2 half + 1)
+      const uint32_t koff = static_cast<uint32_t>((((j + 1) >> 1) & 1) * C::kTileBytes + ((j + 1) & 1) * 16384);
+      const uint32_t voff = static_cast<uint32_t>((((j - 1) >> 1) & 1) * C::kTileBytes + ((j - 1) & 1) * 16384);
+      uint32_t kqs[8], vqs[4];
+      if constexpr (SC) {
+#pragma unroll
+        for (int k3 = 0; k3 < 8; ++k3) kqs[k3] = kq[k3] + koff;
+      }
+      if constexpr (PV) {
+#pragma unroll
+        for (int d2 = 0; d2 < 4; ++d2) vqs[d2] = vq[d2] + voff;
+      }
+      if (PAR == 1) {  // odd steps copy K((j+3)/2) and V((j+1)/2)
+        const int uk = (j + 3) >> 1, uv = (j + 1) >> 1;
+        if (uk < ntiles) copy_tile(uk, false);
+        if (uv < ntiles) copy_tile(uv, true);
+      }
+      float mx = -__builtin_inff(), alpha = 1.0f, m_sub = 0.0f, psum = 0.0f;
+      bool grow = false;
+      f32x8_t pv8[2];
+      auto piece = [&](int k) {
+        if constexpr (SM) {
+          if (k == 0) {
+            mask_block(j, ssm);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, ssm[r]);
+          } else if (k == 1) {
+            mx = half_max(mx) * c;
+            grow = mx > m_run + 8.0f;
+            const float m_new = grow ? mx : m_run;
+            alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+            m_sub = (m_new == -__builtin_inff()) ? 0.0f : m_new;  // fully masked so far: p = 0
+            m_run = m_new;
+          } else if (k < 6) {
+            const int r0 = 4 * (k - 2);
+#pragma unroll
+            for (int r = r0; r < r0 + 4; ++r) {
+              float p = __builtin_amdgcn_exp2f(__builtin_fmaf(ssm[r], c, -m_sub));
+              asm volatile("" : "+v"(p));
+              psum += p;
+              pv8[r >> 3][r & 7] = p;
+            }
+          } else if (k == 6) {
+            psm[0] = __builtin_convertvector(pv8[0], bf16x8_t);
+            psm[1] = __builtin_convertvector(pv8[1], bf16x8_t);
+            asm volatile("" : "+v"(psm[0]), "+v"(psm[1]));
+          } else if (k == 7) {
+            l_run = l_run * alpha + psum;
+            asm volatile("" : "+v"(l_run));
+          }
+        }
+      };
+      if constexpr (PV || SC) {
+        constexpr int per = (SC ? 1 : 0) + (PV ? 2 : 0);
+        u32x4_t kf[kWin];
+        u32x2_t vlo[kWin], vhi[kWin];
+        // pair i: score MFMA step kk = i, P·V MFMA m = i (O block m & 7, slice m >> 3)
+#define FD_R(I)                                                                                                 \
+  do {                                                                                                          \
+    const int i_ = (I), w_ = i_ % kWin;                                                                         \
+    if constexpr (SC)                                                                                           \
+      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(kf[w_]) : "v"(kqs[i_ & 7]), "i"(256 * (i_ >> 3))      \
+                   : "memory");                                                                                 \
+    if constexpr (PV) {                                                                                         \
+      const int db_ = i_ & 7, cs_ = i_ >> 3;                                                                    \
+      asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(vlo[w_])                                        \
+                   : "v"(vqs[db_ & 3]), "i"(256 * (db_ >> 2) + 8192 * cs_) : "memory");                         \
+      asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(vhi[w_])                                        \
+                   : "v"(vqs[db_ & 3]), "i"(256 * (db_ >> 2) + 8192 * cs_ + 2048) : "memory");                  \
+    }                                                                                                           \
+  } while (0)
+#pragma unroll
+        for (int i = 0; i < kWin; ++i) FD_R(i);
+        if constexpr (SC) ssc = f32x16_t{};
+#pragma unroll
+        for (int i = 0; i < kKk; ++i) {
+          const int w = i % kWin;
+          const int younger = per * min(kWin - 1, kKk - 1 - i);
+#define FD_W(N) asm volatile("s_waitcnt lgkmcnt(" #N ")" : "+v"(kf[w]), "+v"(vlo[w]), "+v"(vhi[w]) :: "memory")
+          switch (younger) {
+            case 12: FD_W(12); break;
+            case 9: FD_W(9); break;
+            case 8: FD_W(8); break;
+            case 6: FD_W(6); break;
+            case 4: FD_W(4); break;
+            case 3: FD_W(3); break;
+            case 2: FD_W(2); break;
+            case 1: FD_W(1); break;
+            default: FD_W(0); break;
+          }
+#undef FD_W
+          if constexpr (SC)
+            ssc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[w]), qf[i], ssc, 0, 0, 0);
+          if constexpr (PV) {
+            const u32x4_t vv = {vlo[w][0], vlo[w][1], vhi[w][0], vhi[w][1]};
+            o[i & 7] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vv), ppv[i >> 3], o[i & 7], 0, 0, 0);
+          }
+          if ((i & 1) == 1) piece(i >> 1);
+          if (i + kWin < kKk) FD_R(i + kWin);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#undef FD_R
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) piece(k);
+      }
+      if constexpr (SM) {
+        // O is relative to the running max from here on (after this step's P·V)
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+          for (int db = 0; db < D / 32; ++db) o[db] *= alpha;
+        }
+      }
+      // the next step reads K of block j+2 and V of block j: even steps wait for
+      // every copy, odd ones for all but their own
+      if (PAR == 0) {
         __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(0));
+      } else {
+        const int own = ((((j + 3) >> 1) < ntiles) ? C::kLoads : 0) + ((((j + 1) >> 1) < ntiles) ? C::kLoads : 0);
+        if (own >= 2 * C::kLoads) __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(2 * C::kLoads));
+        else if (own >= C::kLoads) __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(C::kLoads));
+        else __builtin_amdgcn_s_waitcnt(C::waitcnt_vm(0));
+      }
       __syncthreads();
     };
-    if constexpr (C::kStages == 3) {
-      int t = 0;
-      for (; t + 3 <= ntiles; t += 3) {
-        tile_step(t, 0);
-        tile_step(t + 1, 1);
-        tile_step(t + 2, 2);
-      }
-      if (t < ntiles) tile_step(t, 0);
-      if (t + 1 < ntiles) tile_step(t + 1, 1);
-    } else {
-      for (int t = 0; t < ntiles; ++t) tile_step(t, t & 1);
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    // step 0 (no P·V yet); steady steps 1 .. nblk-2 (an even count); step
+    // nblk-1 (no scores); step nblk (the last P·V).  nblk = 2 ntiles is even.
+    step(I0{}, F_{}, T_{}, T_{}, 0);
+    for (int j = 1; j + 2 < nblk; j += 2) {
+      step(I1{}, T_{}, T_{}, T_{}, j);
+      step(I0{}, T_{}, T_{}, T_{}, j + 1);
     }
+    step(I1{}, T_{}, T_{}, F_{}, nblk - 1);
+    step(I0{}, T_{}, F_{}, F_{}, nblk);
+  } else {
+    static_assert(C::kPipe || (D == 256 && KSPLIT == 1), "no loop for this configuration");
   }
 
   // ---- merge the key parts of each (head, query block), then normalise and store
