@@ -175,12 +175,13 @@ def _gqa_case(B, Hq, Hkv, T, D, samples: int, eager: bool) -> dict:
 def bench_gqa(samples: int, only: bool = False) -> dict:
     """The BASELINE GQA kernel config (B=1 T=2048 16/4x128, the roofline line), plus the shapes the
     reference's isolated benchmark sweeps (B = 2, 4; ref: experiments/native_gqa/bench_native_gqa.py:43-61)
-    and the decider-2b checkpoint's real attention shape (8/2x256)."""
+    and the decider-2b checkpoint's real attention shape (8/2x256, at B=1 where the long query tiles
+    are key-split and at B=2 where they are not)."""
     out = _gqa_case(1, 16, 4, 2048, 128, samples, eager=not only)
     out.update(bound="mfma", peak_tflops=MFMA_BF16_PEAK_TFLOPS)
     if not only:
         out["other_shapes"] = [_gqa_case(B, Hq, Hkv, 2048, D, max(10, samples // 3), eager=True)
-                               for B, Hq, Hkv, D in ((2, 16, 4, 128), (4, 16, 4, 128), (1, 8, 2, 256))]
+                               for B, Hq, Hkv, D in ((2, 16, 4, 128), (4, 16, 4, 128), (1, 8, 2, 256), (2, 8, 2, 256))]
     return out
 
 
