@@ -19,10 +19,13 @@
 //   wavefront finishes tile t (mask, softmax, P·V), the scores of tile t+1
 //   are computed, one MFMA of that dependent chain after each of eight pieces
 //   of the softmax, so the VALU work issues while the MFMAs run; tiles t+2 and
-//   t+3 are in flight.  head_dim 256 (whose 4 stages would not fit the
-//   160 KiB LDS) has one wavefront per SIMD walking 32-key blocks: the P·V of
-//   block j-1 and the scores of block j+1 are issued with the softmax of
-//   block j between their MFMAs, over 2-stage K and V rings.
+//   t+3 are in flight.
+// * One wavefront per head (head_dim 256 always, 64 and 128 for padded
+//   batches with more than two work items per CU): 4 wavefronts per
+//   workgroup, each walking 32-key blocks; the P·V of block j-1 and the scores
+//   of block j+1 are issued with the softmax of block j between their MFMAs,
+//   over 2-stage K and V rings.  At head_dim <= 128 two such workgroups share
+//   a CU, so one wavefront's softmax runs under the other's MFMAs.
 //   16-byte chunks are XOR-swizzled per row so that the MFMA operand reads
 //   below are bank-conflict free.
 // * The score tile is computed transposed, S^T = K · Q^T, with
@@ -45,6 +48,7 @@
 //   contiguous range of (head group, query tile) items, keeping a KV head's
 //   tiles in one L2.
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "fd_common.h"
@@ -115,7 +119,7 @@ struct Cfg {
   // tiles t+2, t+3 are in flight.  head_dim 256 (one wavefront per (head,
   // query block)) has 2 stages, used as separate K and V rings.
   static constexpr bool kPipe = KSPLIT > 1 && 4 * kStageBytes <= 160 * 1024;
-  static constexpr int kStages = kPipe ? 4 : 3 * kStageBytes <= 160 * 1024 ? 3 : 2;
+  static constexpr int kStages = kPipe ? 4 : 2;
   static constexpr int kCombineBytes = KSPLIT > 1 ? 4 * 64 * (D / 2 + 2) * 4 : 0;
   static constexpr int kSmemBytes =
       (kStages * kStageBytes > kCombineBytes) ? kStages * kStageBytes : kCombineBytes;
@@ -202,7 +206,7 @@ __device__ __forceinline__ void store_rows(const GqaArgs& a, const f32x16_t (&o)
 }
 
 template <int D, int KSPLIT>
-__global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
+__global__ __launch_bounds__(256 * KSPLIT, (KSPLIT == 1 && D <= 128) ? 2 : 1) void gqa_fwd_kernel(GqaArgs a) {
   using C = Cfg<D, KSPLIT>;
   constexpr int CR = C::kChunksRow;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[C::kSmemBytes];
@@ -277,7 +281,7 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
 
   // Q^T as MFMA B operand: lane supplies Q[qpos][16kk + 8*half + 0..7].
   bf16x8_t qf[D / 16];
-  if constexpr (D == 256 && KSPLIT == 1) {
+  if constexpr (KSPLIT == 1) {
     // The head_dim-256 loop issues its copies and LDS reads as asm and counts
     // them itself; the compiler, which does not see them, must not be left
     // with loads of its own to wait for inside the loop.  So Q is read with
@@ -556,7 +560,7 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
     if (t < ntiles) step(t, 0, sA, sB);
     if (t + 1 < ntiles) step(t + 1, 1, sB, sA);
     if (t + 2 < ntiles) step(t + 2, 2, sA, sB);
-  } else if constexpr (D == 256 && KSPLIT == 1) {
+  } else if constexpr (KSPLIT == 1) {
     // head_dim 256: one wavefront per SIMD (4 per workgroup), each owning one
     // head's 32 queries.  The wavefront walks the keys in 32-key blocks (block
     // b = half b % 2 of tile b / 2) with its own online softmax per block.
@@ -566,17 +570,23 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
     // tiles: K(u) is copied in step 2u-3 and read in steps 2u-1, 2u; V(u) is
     // copied in step 2u-1 and read in steps 2u+1, 2u+2.  Copies and LDS
     // operand reads are asm with explicit waits (see the Q loads).
-    constexpr int kKk = D / 16;   // 16 score MFMAs per block (and 16 P·V MFMAs)
+    constexpr int kKk = D / 16;   // score MFMAs per block (and P·V MFMAs)
+    constexpr int kNdb = D / 32;  // O^T blocks
+    constexpr int RB = CR * 16;   // bytes per K / V row in LDS
+    constexpr int kRowsPer = 64 / CR;  // rows per 1 KiB copy instruction
+    constexpr int kKPer = 16 / (4 * kRowsPer) > 1 ? 16 / (4 * kRowsPer) : 1;  // period of the K copy swizzle in i
+    constexpr int kPieceEvery = kKk >= 8 ? kKk / 8 : 1;  // MFMA pairs per softmax piece
+    constexpr int kPiecesPer = kKk >= 8 ? 1 : 8 / kKk;    // softmax pieces per MFMA pair
     constexpr int kWin = 4;       // MFMA pairs (three reads each) in flight
-    static_assert(C::kBlocks == 2 && C::kStages == 2, "head_dim 256 layout");
+    static_assert(C::kBlocks == 2 && C::kStages == 2, "one-wavefront-per-head layout");
     const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)smem));
     // copy offsets: slot (i*4 + wave)*64 + lane -> row 8i + 2 wave + lane/32, chunk lane%32;
     // the K swizzle depends on row & 15, i.e. on i & 1
-    const int crow = 2 * wave + (lane >> 5);
-    const int cchunk = lane & 31;
-    int ck_off[2];
+    const int crow = kRowsPer * wave + lane / CR;
+    const int cchunk = lane % CR;
+    int ck_off[kKPer];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) ck_off[e] = (cchunk ^ swz_k<CR>(8 * e + crow)) * 8;
+    for (int e = 0; e < kKPer; ++e) ck_off[e] = (cchunk ^ swz_k<CR>(4 * kRowsPer * e + crow)) * 8;
     const int cv_off = (cchunk ^ swz_v<CR>(crow)) * 8;
     auto copy_tile = [&](int u, bool is_v) {
       const uint32_t stage_base = lds0 + static_cast<uint32_t>(((is_v ? 2 : 0) + (u & 1)) * C::kTileBytes);
@@ -586,8 +596,8 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
       const int last = seq_end - 1 - ks0;  // rows past the end re-read the last row: finite data the mask discards
 #pragma unroll
       for (int i = 0; i < C::kLoads; ++i) {
-        const int r = min(8 * i + crow, last);
-        const int rel = r * stride + (is_v ? cv_off : ck_off[i & 1]);
+        const int r = min(4 * kRowsPer * i + crow, last);
+        const int rel = r * stride + (is_v ? cv_off : ck_off[i % kKPer]);
         const uint32_t lds = stage_base + static_cast<uint32_t>((i * C::kWaves + wave) * 1024);
         asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
                      :: "v"(static_cast<uint32_t>(rel) * 2u), "s"(g), "s"(lds) : "memory", "m0");
@@ -597,18 +607,19 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
     // chunk (16 hi + lo) ^ z = 16 hi + (lo ^ z): 8 lane offsets, the rest immediates
     const int krow = sigma(col);
     const int kz = swz_k<CR>(krow);
-    uint32_t kq[8];
+    constexpr int kNkq = kKk < 8 ? kKk : 8;
+    uint32_t kq[kNkq];
 #pragma unroll
-    for (int k3 = 0; k3 < 8; ++k3) kq[k3] = lds0 + static_cast<uint32_t>(krow * CR * 16 + (((2 * k3 + half) ^ kz) * 16));
+    for (int k3 = 0; k3 < kNkq; ++k3) kq[k3] = lds0 + static_cast<uint32_t>(krow * RB + (((2 * k3 + half) ^ kz) * 16));
     // V^T operand (O block db = 4 dh + d2, 16-key slice cs of the tile, half r2):
     // row 16 cs + 8 (grp >> 1) + 4 r2 + li / 4, chunk 16 dh + 4 (d2 ^ (li / 4 & 3)) + c0
     const int vrow = 8 * (grp >> 1) + (li >> 2);
-    const int vr = (li >> 2) & 3;
     const int vc0 = 2 * (grp & 1) + ((li & 3) >> 1);
-    uint32_t vq[4];
+    constexpr int kNvq = kNdb < 4 ? kNdb : 4;
+    uint32_t vq[kNvq];
 #pragma unroll
-    for (int d2 = 0; d2 < 4; ++d2)
-      vq[d2] = lds0 + static_cast<uint32_t>(2 * C::kTileBytes + vrow * CR * 16 + (4 * (d2 ^ vr) + vc0) * 16 + 8 * (li & 1));
+    for (int d2 = 0; d2 < kNvq; ++d2)
+      vq[d2] = lds0 + static_cast<uint32_t>(2 * C::kTileBytes + vrow * RB + (((4 * d2 + vc0) ^ swz_v<CR>(vrow)) * 16) + 8 * (li & 1));
     typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
     typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
     const int nblk = 2 * ntiles;
@@ -643,7 +654,7 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
 #pragma unroll
     for (int kk = 0; kk < kKk; ++kk) {
       u32x4_t kf;
-      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(kf) : "v"(kq[kk & 7]), "i"(256 * (kk >> 3)) : "memory");
+      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(kf) : "v"(kq[kk % kNkq]), "i"(256 * (kk / kNkq)) : "memory");
       asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kf) :: "memory");
       S[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf), qf[kk], S[0], 0, 0, 0);
     }
@@ -660,16 +671,16 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
       bf16x8_t (&psm)[2] = P[PAR];        // block j
       // K of block j+1: tile (j+1)/2 in stage ((j+1)/2) & 1, half (j+1) & 1;
       // V of block j-1: tile (j-1)/2, half (j-1) & 1 (its 16-key slices 2 half, 2 half + 1)
-      const uint32_t koff = static_cast<uint32_t>((((j + 1) >> 1) & 1) * C::kTileBytes + ((j + 1) & 1) * 16384);
-      const uint32_t voff = static_cast<uint32_t>((((j - 1) >> 1) & 1) * C::kTileBytes + ((j - 1) & 1) * 16384);
-      uint32_t kqs[8], vqs[4];
+      const uint32_t koff = static_cast<uint32_t>((((j + 1) >> 1) & 1) * C::kTileBytes + ((j + 1) & 1) * 32 * RB);
+      const uint32_t voff = static_cast<uint32_t>((((j - 1) >> 1) & 1) * C::kTileBytes + ((j - 1) & 1) * 32 * RB);
+      uint32_t kqs[kNkq], vqs[kNvq];
       if constexpr (SC) {
 #pragma unroll
-        for (int k3 = 0; k3 < 8; ++k3) kqs[k3] = kq[k3] + koff;
+        for (int k3 = 0; k3 < kNkq; ++k3) kqs[k3] = kq[k3] + koff;
       }
       if constexpr (PV) {
 #pragma unroll
-        for (int d2 = 0; d2 < 4; ++d2) vqs[d2] = vq[d2] + voff;
+        for (int d2 = 0; d2 < kNvq; ++d2) vqs[d2] = vq[d2] + voff;
       }
       if (PAR == 1) {  // odd steps copy K((j+3)/2) and V((j+1)/2)
         const int uk = (j + 3) >> 1, uv = (j + 1) >> 1;
@@ -720,14 +731,14 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
   do {                                                                                                          \
     const int i_ = (I), w_ = i_ % kWin;                                                                         \
     if constexpr (SC)                                                                                           \
-      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(kf[w_]) : "v"(kqs[i_ & 7]), "i"(256 * (i_ >> 3))      \
+      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(kf[w_]) : "v"(kqs[i_ % kNkq]), "i"(256 * (i_ / kNkq)) \
                    : "memory");                                                                                 \
     if constexpr (PV) {                                                                                         \
-      const int db_ = i_ & 7, cs_ = i_ >> 3;                                                                    \
+      const int db_ = i_ % kNdb, cs_ = i_ / kNdb;                                                               \
       asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(vlo[w_])                                        \
-                   : "v"(vqs[db_ & 3]), "i"(256 * (db_ >> 2) + 8192 * cs_) : "memory");                         \
+                   : "v"(vqs[db_ % kNvq]), "i"(256 * (db_ / kNvq) + 16 * RB * cs_) : "memory");                 \
       asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(vhi[w_])                                        \
-                   : "v"(vqs[db_ & 3]), "i"(256 * (db_ >> 2) + 8192 * cs_ + 2048) : "memory");                  \
+                   : "v"(vqs[db_ % kNvq]), "i"(256 * (db_ / kNvq) + 16 * RB * cs_ + 4 * RB) : "memory");        \
     }                                                                                                           \
   } while (0)
 #pragma unroll
@@ -754,9 +765,12 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
             ssc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[w]), qf[i], ssc, 0, 0, 0);
           if constexpr (PV) {
             const u32x4_t vv = {vlo[w][0], vlo[w][1], vhi[w][0], vhi[w][1]};
-            o[i & 7] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vv), ppv[i >> 3], o[i & 7], 0, 0, 0);
+            o[i % kNdb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vv), ppv[i / kNdb], o[i % kNdb], 0, 0, 0);
           }
-          if ((i & 1) == 1) piece(i >> 1);
+          if (i % kPieceEvery == kPieceEvery - 1) {
+#pragma unroll
+            for (int pp = 0; pp < kPiecesPer; ++pp) piece((i / kPieceEvery) * kPiecesPer + pp);
+          }
           if (i + kWin < kKk) FD_R(i + kWin);
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -798,7 +812,7 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
     step(I1{}, T_{}, T_{}, F_{}, nblk - 1);
     step(I0{}, T_{}, F_{}, F_{}, nblk);
   } else {
-    static_assert(C::kPipe || (D == 256 && KSPLIT == 1), "no loop for this configuration");
+    static_assert(C::kPipe || KSPLIT == 1, "no loop for this configuration");
   }
 
   // ---- merge the key parts of each (head, query block), then normalise and store
@@ -904,6 +918,22 @@ bool stride_ok(const int64_t s[4]) {
 // split measured no faster: every item carries about 5 us of fixed cost
 // (argument loads, the first tiles' latency, merge and store) against about
 // 1 us per 64-key tile, so the extra items cost what the balance saves.
+// head_dim 64 and 128 have two loops: two wavefronts per (head, query block),
+// each on half the keys of every tile (one workgroup per CU), or one
+// wavefront per head walking 32-key blocks in a 64 KiB workgroup of which two
+// fit per CU.  The second needs both workgroup slots of a CU filled to
+// overlap one wavefront's softmax with the other's MFMAs, so it runs when a
+// padded batch of several sequences has more than two work items per CU.
+// Single sequences and packed requests always take the first loop, so a
+// request's rows are the same alone and packed.  FD_GQA_ONE_WAVE=0 / 1 forces
+// the choice (tests run both loops on every shape).
+constexpr int64_t kOneWaveAbove = 2 * 256;
+bool one_wave_loop(int64_t items, int batch, bool varlen) {
+  const char* force = std::getenv("FD_GQA_ONE_WAVE");
+  if (force != nullptr && (force[0] == '0' || force[0] == '1')) return force[0] == '1';
+  return !varlen && batch > 1 && items > kOneWaveAbove;
+}
+
 constexpr int64_t kSplitBelow = 256;
 
 // Query tiles of every (sequence, head group) that the key split halves, or 0.
@@ -1036,12 +1066,15 @@ int gqa_launch(const void* q, const void* k, const void* v, void* out, const int
   const int nblocks = static_cast<int>((items + kNumXcd - 1) / kNumXcd * kNumXcd);
   hipStream_t s = static_cast<hipStream_t>(stream);
   dim3 grid(nblocks);
+  const bool one_wave = a.n_split == 0 && one_wave_loop(items, batch, cu_seqlens != nullptr);
   switch (head_dim) {
     case 64:
-      hipLaunchKernelGGL((gqa_fwd_kernel<64, 2>), grid, dim3(Cfg<64, 2>::kThreads), 0, s, a);
+      if (one_wave) hipLaunchKernelGGL((gqa_fwd_kernel<64, 1>), grid, dim3(Cfg<64, 1>::kThreads), 0, s, a);
+      else hipLaunchKernelGGL((gqa_fwd_kernel<64, 2>), grid, dim3(Cfg<64, 2>::kThreads), 0, s, a);
       break;
     case 128:
-      hipLaunchKernelGGL((gqa_fwd_kernel<128, 2>), grid, dim3(Cfg<128, 2>::kThreads), 0, s, a);
+      if (one_wave) hipLaunchKernelGGL((gqa_fwd_kernel<128, 1>), grid, dim3(Cfg<128, 1>::kThreads), 0, s, a);
+      else hipLaunchKernelGGL((gqa_fwd_kernel<128, 2>), grid, dim3(Cfg<128, 2>::kThreads), 0, s, a);
       break;
     default:
       hipLaunchKernelGGL((gqa_fwd_kernel<256, 1>), grid, dim3(Cfg<256, 1>::kThreads), 0, s, a);

@@ -20,6 +20,20 @@ pytestmark = pytest.mark.gpu
 ATOL = 2e-2
 
 
+@pytest.fixture(autouse=True, params=["two_waves", "one_wave"])
+def gqa_loop(request, monkeypatch):
+    """Every test runs with both head_dim-64/128 loops (the launcher picks by work-item count;
+    FD_GQA_ONE_WAVE forces it).  head_dim 256 has one loop, so its cases run once.  The key-split
+    test compares the split launch with the unsplit one, both of the two-wavefront loop."""
+    one = request.param == "one_wave"
+    if one and request.node.get_closest_marker("two_wave_loop_only"):
+        pytest.skip("the key split runs the two-wavefront loop")
+    callspec = getattr(request.node, "callspec", None)
+    if one and callspec is not None and callspec.params.get("D") == 256:
+        pytest.skip("head_dim 256 has a single loop")
+    monkeypatch.setenv("FD_GQA_ONE_WAVE", "1" if one else "0")
+
+
 def sdpa_fp32(q, k, v):
     """fp32 MATH SDPA with repeated KV heads and a causal mask (q [B,Hq,T,D])."""
     group = q.shape[1] // k.shape[1]
@@ -110,6 +124,7 @@ def test_decider_shape_T2048(recipe, oracle):
 
 @pytest.mark.parametrize("B,Hq,Hkv,T,D", [
     (1, 8, 2, 2048, 256),   # real decider-2b attention shape
+    (4, 16, 4, 2048, 128),  # more than two work items per CU: the launcher's one-wavefront loop
     (2, 8, 2, 333, 256),
     (2, 16, 4, 1000, 128),
     (1, 4, 4, 257, 128),    # MHA (group 1)
@@ -218,6 +233,7 @@ def test_wrapper_rejects_bad_inputs():
         native_gqa_attention(qt, kt, kt)
 
 
+@pytest.mark.two_wave_loop_only
 @pytest.mark.parametrize("Hq,Hkv,T,D,gated", [(16, 4, 1024, 128, False), (16, 4, 1024, 128, True),
                                                (8, 2, 2048, 256, False), (4, 4, 777, 64, False)])
 def test_key_split_equals_the_unsplit_kernel(Hq, Hkv, T, D, gated, oracle):
