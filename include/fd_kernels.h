@@ -104,6 +104,15 @@ FD_API const char* fd_last_error(void);
  * the key split of long query tiles, see fd_gqa_workspace_bytes; NULL / 0 runs
  * unsplit.  With a split the call enqueues two launches on `stream`.
  *
+ * Two loops serve head_dim 64 and 128: two wavefronts per (head, 32 queries)
+ * on the two key halves of every tile, or one wavefront per (head, 32
+ * queries) on all keys.  The second runs for padded batches (cu_seqlens NULL)
+ * of two or more sequences with more than 512 work items (4 query heads x 32
+ * queries each); single sequences and packed requests always run the first,
+ * so a request's rows are the same alone and packed.  The two loops round
+ * differently (at most about one bf16 step apart).  The environment variable
+ * FD_GQA_ONE_WAVE=0 or 1, read at each call, forces the first or the second.
+ *
  * Limits: head_dim in {64, 128, 256}; q_heads % kv_heads == 0; every base
  * pointer and every non-unit stride keeps 16-byte alignment.
  */
