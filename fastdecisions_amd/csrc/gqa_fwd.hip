@@ -651,12 +651,28 @@ __global__ __launch_bounds__(256 * KSPLIT, (KSPLIT == 1 && D <= 128) ? 2 : 1) vo
     f32x16_t S[2];   // scores of block b in S[b & 1]
     bf16x8_t P[2][2];  // P of block b in P[b & 1] (two 16-key slices)
     S[0] = f32x16_t{};
+    {
+      u32x4_t kf0[kWin];
+#define FD_R0(I) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(kf0[(I) % kWin]) \
+                              : "v"(kq[(I) % kNkq]), "i"(256 * ((I) / kNkq)) : "memory")
 #pragma unroll
-    for (int kk = 0; kk < kKk; ++kk) {
-      u32x4_t kf;
-      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(kf) : "v"(kq[kk % kNkq]), "i"(256 * (kk / kNkq)) : "memory");
-      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kf) :: "memory");
-      S[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf), qf[kk], S[0], 0, 0, 0);
+      for (int kk = 0; kk < kWin && kk < kKk; ++kk) FD_R0(kk);
+#pragma unroll
+      for (int kk = 0; kk < kKk; ++kk) {
+        const int younger = min(kWin - 1, kKk - 1 - kk);
+#define FD_W0(N) asm volatile("s_waitcnt lgkmcnt(" #N ")" : "+v"(kf0[kk % kWin]) :: "memory")
+        switch (younger) {
+          case 3: FD_W0(3); break;
+          case 2: FD_W0(2); break;
+          case 1: FD_W0(1); break;
+          default: FD_W0(0); break;
+        }
+#undef FD_W0
+        S[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf0[kk % kWin]), qf[kk], S[0], 0, 0, 0);
+        if (kk + kWin < kKk) FD_R0(kk + kWin);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#undef FD_R0
     }
 
     // block step j: P·V of block j-1 (PV), softmax of block j (SM), scores of
