@@ -72,6 +72,8 @@ def parse_args():
     p.add_argument("--only-kernel", choices=["gqa", "conv", "rmsnorm", "gdr", "copy"], default=None,
                    help="profiling aid: run just this kernel's HIP timing loop ('copy' is the plain device "
                         "copy used to calibrate HBM byte counters)")
+    p.add_argument("--gqa-shape", default="1,16,4,128",
+                   help="with --only-kernel gqa: B,Hq,Hkv,D of the timed shape (T=2048; profiling aid)")
     p.add_argument("--only-forward", action="store_true",
                    help="profiling aid: capture the HIP-path forward and replay it --steps times, nothing else "
                         "(a kernel trace then covers every forward kernel in place)")
@@ -172,12 +174,13 @@ def _gqa_case(B, Hq, Hkv, T, D, samples: int, eager: bool) -> dict:
     return out
 
 
-def bench_gqa(samples: int, only: bool = False) -> dict:
+def bench_gqa(samples: int, only: bool = False, shape=(1, 16, 4, 128)) -> dict:
     """The BASELINE GQA kernel config (B=1 T=2048 16/4x128, the roofline line), plus the shapes the
     reference's isolated benchmark sweeps (B = 2, 4; ref: experiments/native_gqa/bench_native_gqa.py:43-61)
     and the decider-2b checkpoint's real attention shape (8/2x256, at B=1 where the long query tiles
     are key-split and at B=2 where they are not)."""
-    out = _gqa_case(1, 16, 4, 2048, 128, samples, eager=not only)
+    B, Hq, Hkv, D = shape if only else (1, 16, 4, 128)
+    out = _gqa_case(B, Hq, Hkv, 2048, D, samples, eager=not only)
     out.update(bound="mfma", peak_tflops=MFMA_BF16_PEAK_TFLOPS)
     if not only:
         out["other_shapes"] = [_gqa_case(B, Hq, Hkv, 2048, D, max(10, samples // 3), eager=True)
@@ -479,7 +482,8 @@ def main() -> int:
     if args.only_kernel:
         fn = dict(gqa=bench_gqa, conv=bench_conv, rmsnorm=bench_rmsnorm, gdr=bench_gated_delta,
                   copy=bench_copy)[args.only_kernel]
-        print(json.dumps({args.only_kernel: fn(args.kernel_samples, only=True)}), flush=True)
+        kw = {"shape": tuple(int(x) for x in args.gqa_shape.split(","))} if args.only_kernel == "gqa" else {}
+        print(json.dumps({args.only_kernel: fn(args.kernel_samples, only=True, **kw)}), flush=True)
         return 0
     if args.only_forward:
         print(json.dumps({"forward_only": forward_only(args)}), flush=True)
