@@ -470,7 +470,7 @@ def main() -> int:
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build runs the decider forward on a "
-              "single MI355X; see DESIGN.md for how the path would shard across GPUs.", file=sys.stderr)
+              "single MI355X; sharding the path across GPUs is designed, not built.", file=sys.stderr)
         return 2
     import torch
     if not torch.cuda.is_available():
