@@ -120,7 +120,12 @@ struct Cfg {
   // query block)) has 2 stages, used as separate K and V rings.
   static constexpr bool kPipe = KSPLIT > 1 && 4 * kStageBytes <= 160 * 1024;
   static constexpr int kStages = kPipe ? 4 : 2;
-  static constexpr int kCombineBytes = KSPLIT > 1 ? 4 * 64 * (D / 2 + 2) * 4 : 0;
+  // merge of the key parts: a whole O per lane slot (split tiles) or half an O
+  // from each key part (whole tiles)
+  static constexpr int kCombineWhole = 4 * 64 * (D / 2 + 2) * 4;
+  static constexpr int kCombineHalves = 8 * 64 * (D / 4 + 2) * 4;
+  static constexpr int kCombineBytes =
+      KSPLIT > 1 ? (kCombineWhole > kCombineHalves ? kCombineWhole : kCombineHalves) : 0;
   static constexpr int kSmemBytes =
       (kStages * kStageBytes > kCombineBytes) ? kStages * kStageBytes : kCombineBytes;
   // s_waitcnt immediate: vmcnt(N) with expcnt / lgkmcnt left alone (gfx9 encoding)
@@ -174,14 +179,23 @@ __device__ __forceinline__ float* part_slot(const GqaArgs& a, int group, int qti
 }
 
 // Normalised store of a lane's query row (the O^T accumulator: dims
-// 32 db + 8 r4 + 4 half + 0..3), with the optional output gate
-// bf16(o) * bf16(sigmoid(gate)), each product rounded to bf16 as the eager ops do.
-template <int D>
+// 32 db + 8 r4 + 4 half + 0..3) for the O blocks [DB0, DB1), with the optional
+// output gate bf16(o) * bf16(sigmoid(gate)), each product rounded to bf16 as
+// the eager ops do.  The gate loads all go out before the first is used.
+template <int D, int DB0 = 0, int DB1 = D / 32>
 __device__ __forceinline__ void store_rows(const GqaArgs& a, const f32x16_t (&o)[D / 32], float inv, bool qvalid,
                                            uint16_t* orow, const uint16_t* grow, int half) {
   if (!qvalid) return;
+  bf16x4_t gb[DB1 - DB0][4];
+  if (grow != nullptr) {
 #pragma unroll
-  for (int db = 0; db < D / 32; ++db) {
+    for (int db = DB0; db < DB1; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        gb[db - DB0][r4] = *reinterpret_cast<const bf16x4_t*>(grow + db * 32 + r4 * 8 + half * 4);
+  }
+#pragma unroll
+  for (int db = DB0; db < DB1; ++db) {
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
       const int d = db * 32 + r4 * 8 + half * 4;
@@ -189,8 +203,7 @@ __device__ __forceinline__ void store_rows(const GqaArgs& a, const f32x16_t (&o)
                     o[db][r4 * 4 + 3] * inv};
       bf16x4_t ob = __builtin_convertvector(v4, bf16x4_t);
       if (grow != nullptr) {
-        const bf16x4_t gb = *reinterpret_cast<const bf16x4_t*>(grow + d);
-        const f32x4_t gf = __builtin_convertvector(gb, f32x4_t);
+        const f32x4_t gf = __builtin_convertvector(gb[db - DB0][r4], f32x4_t);
         const f32x4_t of = __builtin_convertvector(ob, f32x4_t);
         f32x4_t sg, pr;
 #pragma unroll
@@ -832,7 +845,55 @@ __global__ __launch_bounds__(256 * KSPLIT, (KSPLIT == 1 && D <= 128) ? 2 : 1) vo
   }
 
   // ---- merge the key parts of each (head, query block), then normalise and store
-  if (KSPLIT > 1) {
+  uint16_t* const orow = obase + qpos * a.os[2];
+  const uint16_t* const grow = a.gate ? a.gate + bidx * a.gs[0] + qhead * a.gs[1] + qpos * a.gs[2] : nullptr;
+  if constexpr (KSPLIT > 1) {
+    if (part < 0) {
+      // Each key part hands the other the half of O it does not store and
+      // finishes the half it does (kh 0: blocks 0 .. D/64-1, kh 1: the rest),
+      // so both wavefronts of a SIMD run the normalisation, gate and store.
+      // Every element is the same sum of the same two products as a one-sided
+      // merge gives.
+      constexpr int kHalf = D / 64;          // O blocks per half
+      constexpr int kStride = kHalf * 16 + 2;  // floats per lane: the half, max, denominator
+      float* const mine = reinterpret_cast<float*>(smem) + ((kh * 4 + w4) * 64 + lane) * kStride;
+      const float* const theirs = reinterpret_cast<const float*>(smem) + (((kh ^ 1) * 4 + w4) * 64 + lane) * kStride;
+      // KEEP: the first O block this key part stores (compile-time, so that o
+      // stays in registers)
+      auto hand_over = [&](auto keep_c) {
+        constexpr int GIVE = kHalf - decltype(keep_c)::value;
+#pragma unroll
+        for (int b = 0; b < kHalf; ++b)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mine[b * 16 + r] = o[GIVE + b][r];
+        mine[kHalf * 16] = m_run;
+        mine[kHalf * 16 + 1] = l_run;
+      };
+      auto finish = [&](auto keep_c) {
+        constexpr int KEEP = decltype(keep_c)::value;
+        const float m1 = theirs[kHalf * 16];
+        const float l1 = theirs[kHalf * 16 + 1];
+        const float m = fmaxf(m_run, m1);
+        const float a0 = (m_run == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
+        const float a1 = (m1 == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m1 - m);
+        const float l_tot = half_sum(l_run * a0 + l1 * a1);
+#pragma unroll
+        for (int b = 0; b < kHalf; ++b)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[KEEP + b][r] = o[KEEP + b][r] * a0 + theirs[b * 16 + r] * a1;
+        store_rows<D, KEEP, KEEP + kHalf>(a, o, 1.0f / l_tot, qvalid, orow, grow, half);
+      };
+      using Lo = std::integral_constant<int, 0>;
+      using Hi = std::integral_constant<int, kHalf>;
+      if (kh == 0) hand_over(Lo{});
+      else hand_over(Hi{});
+      __syncthreads();
+      if (kh == 0) finish(Lo{});
+      else finish(Hi{});
+      return;
+    }
+    // a half of a split tile: the key parts merge into key part 0, which
+    // writes the whole unnormalised state to the workspace
     float* cmb = reinterpret_cast<float*>(smem) + (w4 * 64 + lane) * (D / 2 + 2);
     if (kh == 1) {
 #pragma unroll
@@ -870,8 +931,7 @@ __global__ __launch_bounds__(256 * KSPLIT, (KSPLIT == 1 && D <= 128) ? 2 : 1) vo
     return;
   }
   const float l_tot = half_sum(l_run);
-  store_rows<D>(a, o, 1.0f / l_tot, qvalid, obase + qpos * a.os[2],
-                a.gate ? a.gate + bidx * a.gs[0] + qhead * a.gs[1] + qpos * a.gs[2] : nullptr, half);
+  store_rows<D>(a, o, 1.0f / l_tot, qvalid, orow, grow, half);
 }
 
 // Merge of the two halves of every split tile (one wavefront per tile and
