@@ -328,6 +328,32 @@ def bench_copy(samples: int, only: bool = True) -> dict:
                 frac=4 * n / us / 1e3 / HBM_PEAK_GBS)
 
 
+def bench_gemm_ceiling(samples: int) -> dict:
+    """Measured on-box MFMA ceilings: torch.matmul (hipBLASLt / rocBLAS) on square 8192^3
+    GEMMs in bf16 and in fp32 (allow_tf32 off), the rates the MFMA-bound kernels are set against
+    besides the published peaks."""
+    import torch
+    n = 8192
+    g = torch.Generator().manual_seed(0)
+    out = {}
+    for name, dt, reps in (("bf16", torch.bfloat16, 8), ("fp32", torch.float32, 2)):
+        a = torch.randn((n, n), generator=g).to(dt).cuda()
+        b = torch.randn((n, n), generator=g).to(dt).cuda()
+        c = torch.empty((n, n), dtype=dt, device="cuda")
+        prev = torch.backends.cuda.matmul.allow_tf32
+        torch.backends.cuda.matmul.allow_tf32 = False
+        try:
+            times = time_graphs({"gemm": graph_of([lambda: torch.matmul(a, b, out=c)] * reps)}, {"gemm": reps},
+                                max(5, samples // 3), 2)
+        finally:
+            torch.backends.cuda.matmul.allow_tf32 = prev
+        us = summary(times["gemm"])["median_us"]
+        out[name] = dict(shape=f"{n}x{n}x{n}", hip=summary(times["gemm"]), tflops=2 * n ** 3 / us / 1e6)
+        del a, b, c
+    torch.cuda.empty_cache()
+    return out
+
+
 # --------------------------------------------------------------------------- full forward
 
 def bench_forward(args) -> dict:
@@ -502,6 +528,18 @@ def main() -> int:
         log(f"gated delta: {kernels['gated_delta']['hip']['median_us']:.1f} us, "
             f"{kernels['gated_delta']['tflops']:.1f} TFLOP/s")
         torch.cuda.empty_cache()
+        # measured on-box ceilings beside the published peaks: a device copy for the HBM-bound
+        # kernels, hipBLASLt GEMMs for the MFMA-bound ones
+        copy = bench_copy(args.kernel_samples)
+        gemm = bench_gemm_ceiling(args.kernel_samples)
+        kernels["measured_ceilings"] = dict(hbm_copy_64MiB=copy, gemm=gemm)
+        for k_, ceil in (("packed_conv", copy["gbs"]), ("add_rmsnorm", copy["gbs"])):
+            kernels[k_]["frac_of_measured_ceiling"] = kernels[k_]["gbs"] / ceil
+        kernels["gqa"]["frac_of_measured_ceiling"] = kernels["gqa"]["tflops"] / gemm["bf16"]["tflops"]
+        kernels["gated_delta"]["frac_of_measured_ceiling"] = kernels["gated_delta"]["tflops"] / gemm["fp32"]["tflops"]
+        log(f"ceilings: copy {copy['gbs']:.0f} GB/s, bf16 GEMM {gemm['bf16']['tflops']:.0f} TFLOP/s, "
+            f"fp32 GEMM {gemm['fp32']['tflops']:.1f} TFLOP/s")
+        torch.cuda.empty_cache()
 
     fwd = None
     if not args.no_forward:
@@ -517,7 +555,9 @@ def main() -> int:
         gq = kernels["gqa"]
         roofline = dict(bound="mfma", kernel="gqa_fwd_kernel<128> (B=1 T=2048 16/4 heads D=128)",
                         achieved=gq["tflops"], peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s", frac=gq["frac"],
-                        traffic=profiled_traffic(GQA_PROFILE), traffic_source=str(GQA_PROFILE.relative_to(ROOT)))
+                        traffic=profiled_traffic(GQA_PROFILE), traffic_source=str(GQA_PROFILE.relative_to(ROOT)),
+                        measured_ceiling=kernels["measured_ceilings"]["gemm"]["bf16"]["tflops"],
+                        frac_of_measured_ceiling=gq["frac_of_measured_ceiling"])
     line = {
         "metric": "median GPU forward ms, B=1 T=2048 decider-2b-shaped; per-kernel % roofline",
         "value": fwd["median_ms"] if fwd else None,
