@@ -165,6 +165,33 @@ def test_exact_identities():
     assert torch.equal(op, o[:, perm])
 
 
+def test_gate_sigmoid_is_exact_for_every_bf16_value():
+    """The gated store's bf16(sigmoid(gate)) equals torch's bf16 sigmoid bit for bit for each of
+    the 65536 bf16 gate values.  K = 0 makes every score equal and V = 1 every output row exactly
+    1.0 (the P·V sum and the denominator both count the visible keys), so the gated output is the
+    rounded sigmoid itself."""
+    from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
+    announce("gqa gate sigmoid over every bf16 value")
+    T, Hq, Hkv, D = 512, 16, 4, 128
+    bits = torch.arange(T * Hq * D, dtype=torch.int64) % 65536  # every bf16 pattern, 16 times
+    bits = torch.where(bits >= 32768, bits - 65536, bits).to(torch.int16)
+    gate = bits.view(torch.bfloat16).reshape(1, T, Hq, D).cuda().transpose(1, 2)
+    q = seeded((1, T, Hq, D), 1300).cuda().transpose(1, 2)
+    k = torch.zeros((1, Hkv, T, D), dtype=torch.bfloat16, device="cuda")
+    v = torch.ones((1, T, Hkv, D), dtype=torch.bfloat16, device="cuda").transpose(1, 2)
+    plain = native_gqa_attention(q, k, v)
+    gated = native_gqa_attention(q, k, v, gate=gate)
+    expect = torch.sigmoid(gate)
+    torch.cuda.synchronize()
+    assert torch.equal(plain, torch.ones_like(plain))
+    gated, expect = gated.contiguous(), expect.contiguous()
+    nan = torch.isnan(expect)
+    assert torch.equal(torch.isnan(gated), nan)
+    differ = (gated.view(torch.int16) != expect.view(torch.int16)) & ~nan
+    print(f"gate sigmoid: {int(differ.sum())} of {differ.numel()} outputs differ from torch.sigmoid")
+    assert not differ.any()
+
+
 def test_varlen_equals_per_request():
     """BASELINE config 5 style: 4 requests, lengths log-uniform in [256, 8192], packed with cu_seqlens."""
     from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
