@@ -26,7 +26,9 @@
 //       depthwise conv accumulates in fp64 and rounds once: measured equal on
 //       every output of the config-2 tensor, where every fp32 tap order
 //       differs on 0.3 % of them);
-//   (+ bias, one fp32 add), then y / (1 + expf(-y)) for SiLU, one bf16 rounding.
+//   (+ bias, one fp32 add), then y / (1 + expf(-y)) for SiLU, one bf16 rounding
+//   (fd_silu_bf16: the hardware exp2 and reciprocal wherever they round to the
+//   same bf16, which fd_silu_check confirms for every fp32 input).
 // The taps are the reference's (ref: :139-177): w[W-1] multiplies x[t], w[j]
 // multiplies x[t-W+1+j], taps before the sequence start are zero.
 #include "fd_common.h"
@@ -157,7 +159,7 @@ __device__ __forceinline__ void conv_block(int lin, int nblocks, const ConvArgs&
     for (int j = 0; j < WIDTH; ++j) acc = __builtin_fma(wd[j][e], xw[j], acc);
     float t = static_cast<float>(acc);
     if (HAS_BIAS) t = t + bs.v[e];
-    return SILU ? fd_silu(t) : t;
+    return SILU ? fd_silu_bf16(t) : t;
   };
 
   if (r0 + RUN <= seg_end && r0 + RUN <= total_rows) {
@@ -387,4 +389,31 @@ extern "C" int fd_packed_conv_gate_fwd(const void* x, int64_t x_row_stride, cons
                       a_log_dtype, dt_bias_dtype, heads};
   return packed_conv_entry(who, x, x_row_stride, weight, nullptr, q, k, v, batch, seq_len, key_dim, value_dim, width,
                            cu_seqlens, n_seqs, FD_ACT_SILU, &gate, stream);
+}
+
+namespace {
+// bf16(fd_silu_bf16(y)) against bf16(fd_silu(y)) for the fp32 bit patterns
+// [begin, begin + count); both NaN counts as equal.  One atomic per wavefront.
+__global__ __launch_bounds__(256) void silu_check_kernel(uint32_t begin, uint32_t count,
+                                                         unsigned long long* mismatches) {
+  unsigned n = 0;
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < count; i += gridDim.x * 256u) {
+    const float y = __uint_as_float(begin + i);
+    const uint32_t a = fd_pack2(fd_silu_bf16(y), 0.0f) & 0xffffu;
+    const uint32_t b = fd_pack2(fd_silu(y), 0.0f) & 0xffffu;
+    const bool a_nan = (a & 0x7f80u) == 0x7f80u && (a & 0x7fu) != 0;
+    const bool b_nan = (b & 0x7f80u) == 0x7f80u && (b & 0x7fu) != 0;
+    if (a != b && !(a_nan && b_nan)) ++n;
+  }
+  for (int off = 32; off >= 1; off >>= 1) n += __shfl_xor(n, off, 64);
+  if ((threadIdx.x & 63) == 0 && n != 0) atomicAdd(mismatches, static_cast<unsigned long long>(n));
+}
+}  // namespace
+
+extern "C" int fd_silu_check(uint32_t begin, uint32_t count, unsigned long long* mismatches, void* stream) {
+  FD_REQUIRE(mismatches != nullptr, FD_ERR_INVALID_ARGUMENT, "fd_silu_check: mismatches must be non-null");
+  if (count == 0) return 0;
+  hipLaunchKernelGGL(silu_check_kernel, dim3(8192), dim3(256), 0, static_cast<hipStream_t>(stream), begin, count,
+                     mismatches);
+  return fd_check_launch("fd_silu_check");
 }

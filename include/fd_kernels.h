@@ -35,6 +35,7 @@
  *                       replaces F.linear(x, cat(W_a, W_b)) + unpack_gate
  *                       (ref: src/decider/combined_gates.py:19-43, packed_conv.py:45-53)
  *   fd_packed_conv_gate_fwd  fd_packed_conv_strided_fwd and fd_gate_proj_fwd of one layer in one launch
+ *   fd_silu_check       numerics self-check of the conv's SiLU (no reference counterpart)
  *
  * Conventions shared by every entry point:
  *   - every tensor pointer is a device pointer; bf16 tensors are passed as raw
@@ -248,6 +249,18 @@ FD_API int fd_packed_conv_gate_fwd(const void* x, int64_t x_row_stride, const vo
                                    const void* gate_weight, int hidden, const void* a_log,
                                    int a_log_dtype, const void* dt_bias, int dt_bias_dtype, float* g,
                                    void* beta, int heads, void* stream);
+
+/*
+ * Numerics self-check of the conv's SiLU; no counterpart in the reference.
+ * The conv kernels evaluate SiLU with the hardware exp2 and reciprocal and
+ * fall back to y / (1 + expf(-y)) (the expression PyTorch's fp32 SiLU
+ * evaluates) where the two could round to different bf16 values.  This entry
+ * point adds to *mismatches (a device uint64 the caller zeroes) the number of
+ * fp32 bit patterns in [begin, begin + count) whose two bf16 roundings differ
+ * (both NaN counts as equal).  The GPU tests run it over all 2^32 patterns
+ * and require 0.
+ */
+FD_API int fd_silu_check(uint32_t begin, uint32_t count, unsigned long long* mismatches, void* stream);
 
 /*
  * Fused residual add + RMSNorm over rows of `width` features.

@@ -27,7 +27,7 @@ def test_header_declares_the_expected_entry_points():
                                     "fd_packed_conv_strided_fwd", "fd_gated_delta_norm_fwd",
                                     "fd_gate_proj_fwd", "fd_packed_conv_gate_fwd",
                                     "fd_silu_mul_split_fwd", "fd_gated_delta_fwd_noalloc",
-                                    "fd_gqa_workspace_bytes"}
+                                    "fd_gqa_workspace_bytes", "fd_silu_check"}
 
 
 def test_library_exports_every_declared_symbol_and_nothing_else():

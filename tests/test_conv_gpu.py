@@ -117,6 +117,24 @@ def test_config2_full_size(oracle):
     print(f"config2: 0 of {x.numel()} differ from torch fp32 conv1d+SiLU; {n} differ from the CPU oracle by 1 ulp")
 
 
+def test_silu_fast_path_rounds_like_torch_for_every_fp32_input():
+    """The conv's SiLU uses the hardware exp2 and reciprocal wherever they round to the same bf16 as
+    y / (1 + expf(-y)), PyTorch's fp32 SiLU expression, and that expression elsewhere.  fd_silu_check
+    compares the two bf16 roundings on the GPU; this runs it over all 2^32 fp32 bit patterns."""
+    import ctypes
+    from fastdecisions_amd import _lib
+    announce("conv SiLU fast path over every fp32 bit pattern")
+    lib = _lib.lib()
+    count = torch.zeros(1, dtype=torch.int64, device="cuda")
+    chunk = 1 << 30
+    for begin in range(0, 1 << 32, chunk):
+        _lib.check("fd_silu_check", lib.fd_silu_check(ctypes.c_uint32(begin), ctypes.c_uint32(chunk),
+                                                      count.data_ptr(), _lib.stream_handle(count.device)))
+    torch.cuda.synchronize()
+    print(f"SiLU fast path: {int(count.item())} of 2^32 fp32 inputs round differently")
+    assert int(count.item()) == 0
+
+
 @pytest.mark.parametrize("batch", [1, 2, 4])
 @pytest.mark.parametrize("weight_shape", [(6144, 4), (6144, 1, 4)])
 def test_reference_random_batches_and_weight_shapes(oracle, batch, weight_shape):
