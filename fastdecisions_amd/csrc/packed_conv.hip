@@ -412,6 +412,8 @@ __global__ __launch_bounds__(256) void silu_check_kernel(uint32_t begin, uint32_
 
 extern "C" int fd_silu_check(uint32_t begin, uint32_t count, unsigned long long* mismatches, void* stream) {
   FD_REQUIRE(mismatches != nullptr, FD_ERR_INVALID_ARGUMENT, "fd_silu_check: mismatches must be non-null");
+  FD_REQUIRE(static_cast<uint64_t>(begin) + count <= (1ULL << 32), FD_ERR_INVALID_ARGUMENT,
+             "fd_silu_check: [begin, begin + count) must lie within the 2^32 fp32 bit patterns");
   if (count == 0) return 0;
   hipLaunchKernelGGL(silu_check_kernel, dim3(8192), dim3(256), 0, static_cast<hipStream_t>(stream), begin, count,
                      mismatches);

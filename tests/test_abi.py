@@ -91,6 +91,17 @@ def test_conv_argument_errors():
     assert call(B=0) == _lib.FD_OK  # empty batch: nothing to launch
 
 
+def test_silu_check_argument_errors():
+    import ctypes
+    from fastdecisions_amd import _lib
+    lib = _lib.lib()
+    f = 1 << 20
+    assert lib.fd_silu_check(ctypes.c_uint32(0), ctypes.c_uint32(16), None, None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert lib.fd_silu_check(ctypes.c_uint32(0xFFFFFFF0), ctypes.c_uint32(0x20), f, None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert "2^32" in _err(lib)
+    assert lib.fd_silu_check(ctypes.c_uint32(5), ctypes.c_uint32(0), f, None) == _lib.FD_OK  # empty range
+
+
 def test_gqa_argument_errors():
     from fastdecisions_amd import _lib
     lib = _lib.lib()
