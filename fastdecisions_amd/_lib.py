@@ -6,6 +6,10 @@ device pointers handed over by torch are then valid inside the library.
 
 There is no fallback: if the library is missing or cannot be loaded, every
 entry point raises ``RuntimeError`` naming the problem.
+
+``FD_KERNELS_LIB`` names another build of the library to load instead of
+the in-tree ``libfd_kernels.so`` (for comparing builds side by side); it must
+export every symbol listed in ``SIGNATURES``.
 """
 from __future__ import annotations
 
