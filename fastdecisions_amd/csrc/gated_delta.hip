@@ -27,13 +27,18 @@
 //      in four 16-row blocks; each finished block is stored while the next runs.
 //   3. gd_state_kernel — one workgroup per (request, value head, 16 value
 //      columns): the only sequential part.  Each state column evolves on its
-//      own, so the 128 value columns split over 8 workgroups.  The state slice
-//      lives in registers; the operands of the chunks two ahead are loaded
-//      straight into registers (three register sets, one wavefront per SIMD)
-//      while the current chunk runs; two barriers per chunk.
-//      Its products run on bf16 MFMA over exact bf16 splits of the fp32 operands.
-//   4. gd_out_kernel — one workgroup per (chunk, value head), chunk-parallel:
-//      o = scale e^{gc} (q S_chunk) + A v', on bf16 MFMA over the same splits.
+//      own, so the 128 value columns split over 8 workgroups.  Four wavefronts
+//      run the chain: the state slice lives in their registers, and the
+//      operands of the chunks two ahead are loaded straight into registers
+//      (three register sets) while the current chunk runs; two barriers per
+//      chunk.  Four more wavefronts, one per SIMD beside the chain's, compute
+//      each chunk's output o = scale e^{gc} (q S_chunk) + A v' for the
+//      slice's columns from the state and v' planes the chain leaves in LDS,
+//      so neither the chunk-start states nor v' go through HBM.
+//      All products run on bf16 MFMA over exact bf16 splits of the fp32 operands.
+//   4. fd_gated_rmsnorm_fwd's kernel — with the layer's gated RMSNorm
+//      (fd_gated_delta_norm_fwd) only: the output rows, written to the
+//      workspace, normalised into the caller's output.
 // The intermediates sit in the workspace in the order their consumer's MFMA
 // operands are loaded (one wavefront load = 1-2 KiB contiguous).  The MFMA
 // lane layout (v_mfma_f32_16x16x32_bf16): lane l supplies A[l%16][8(l/16)+j]
@@ -67,28 +72,20 @@ struct GdArgs {
   int32_t* len;      // [nc]  valid rows of each chunk (0 = unused)
   int32_t* first;    // [N+1] first chunk of each request
   float* gc;         // [Hv, nc, 3, 64]: e^{gc_t}, e^{gl - gc_t}, then e^{gl} (gl = gc of the last row)
-  uint16_t* qn;      // [Hv, nc, 64, 128] bf16
+  // q and A are stored in the state pass's output-wavefront operand order
+  // (lane = 16 * g4 + c16): every load there reads 1-2 KiB contiguous
+  uint16_t* qn;      // [Hv, nc, rt 4, st 4, lane 64, 8] bf16: q[16rt + c16][32st + 8g4 + e]
   // w, k^T and u are stored in the state pass's operand order: every load of a
   // wavefront there reads 1 KiB contiguous (lane = 16 * g4 + c16, see gd_state_kernel)
   uint16_t* kn;      // [Hv, nc, wv 4, m 2, st 2, lane 64, 8] bf16: k^T[32wv + 16m + c16][32st + 8g4 + e]
   uint16_t* w;       // [Hv, nc, plane 3, wv 4, st 4, lane 64, 8] bf16: w_x[16wv + c16][32st + 8g4 + e],
                      // w split exactly into hi + mid + lo planes
   float* u;          // [Hv, nc, js 8, wv 4, lane 64, r 4]: u[16wv + 4g4 + r][16js + c16]
-  float* vn;         // [Hv, nc, n 8, s 2, lane 64, j 8]: v'[32s + 8g4 + j][16n + c16] (output pass B order)
-  float* aq;         // [Hv, nc, 64, 64]
-  float* sc;         // [Hv, nc, n 8, s 4, lane 64, j 8]: chunk-start S[32s + 8g4 + j][16n + c16] (output pass B order)
+  float* aq;         // [Hv, nc, rt 4, st 2, lane 64, 8]: A[16rt + c16][32st + 8g4 + e]
   int hk, hv, nc, nseq;
   int varlen, seq_len, nct;  // packed requests (table) or a padded batch of nct chunks per sequence
   int beta_f32, l2norm;
   float scale;
-  // optional gated RMSNorm epilogue of the output pass (transformers Qwen3_5RMSNormGated):
-  // gate of token row r, head h at z + r * z_ts + h * z_hs; null z = plain output
-  const uint16_t* z;
-  int64_t z_ts, z_hs;
-  const void* nw;  // [128] norm weight, bf16 or fp32 (nw_f32)
-  int nw_f32;
-  int nw_vec;      // nw 16-byte aligned: each lane loads its 8 weights as vectors
-  float norm_eps;
 };
 
 // round to bf16 and back (v_cvt_pk_bf16_f32, round to nearest even)
@@ -247,6 +244,11 @@ constexpr int kPrepBytes = kPrepBG + kC * 4;
 // are the solutions of (I + L) x = rhs; thread j < 128 solves for column j of
 // u, thread 128 + j for column j of w, by forward substitution with the rows of
 // L read from LDS (every lane reads the same address: broadcast).
+// position of A[i][j] in the output wavefronts' operand order
+__device__ __forceinline__ int aq_index(int i, int j) {
+  return (((i >> 4) * 2 + (j >> 5)) * 64 + 16 * ((j & 31) >> 3) + (i & 15)) * 8 + (j & 7);
+}
+
 __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
   const int h = blockIdx.x % a.hv;
   const int c = blockIdx.x / a.hv;
@@ -309,7 +311,7 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
     *reinterpret_cast<uint4*>(sQ + row * kRowK + c16 * 8) = q4;
     *reinterpret_cast<uint4*>(sK + row * kRowK + c16 * 8) = k4;
     *reinterpret_cast<uint4*>(sV + row * kRowK + c16 * 8) = v4;
-    *reinterpret_cast<uint4*>(gq + row * kD + c16 * 8) = q4;
+    *reinterpret_cast<uint4*>(gq + (((row >> 4) * 4 + (c16 >> 2)) * 64 + 16 * (c16 & 3) + (row & 15)) * 8) = q4;
   }
   // g (inclusive cumsum over the chunk) and beta
   if (wv == 0) {
@@ -353,11 +355,11 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
       const int i = 32 * I + (r >> 2) * 8 + (l >> 5) * 4 + (r & 3);
       const float dec = i >= j ? expf(sG[i] - gj) : 0.0f;
       sL[j * kRowF + i] = i > j ? (sB[i] * accG[r]) * dec : 0.0f;  // transposed: sL[j][i] = L[i][j]
-      gaq[i * kC + j] = i >= j ? (a.scale * accA[r]) * dec : 0.0f;
+      gaq[aq_index(i, j)] = i >= j ? (a.scale * accA[r]) * dec : 0.0f;
     }
   } else {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) gaq[(r * 2 + (l >> 5)) * kC + 32 + (l & 31)] = 0.0f;
+    for (int r = 0; r < 16; ++r) gaq[aq_index(r * 2 + (l >> 5), 32 + (l & 31))] = 0.0f;
   }
   __syncthreads();
 
@@ -487,7 +489,7 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// 3. sequential state pass over the chunks of one request
+// 3. sequential state pass over the chunks of one request, with the chunks' outputs
 //
 // Both products of a chunk run on v_mfma_f32_16x16x32_bf16 with the fp32
 // operands split exactly into bf16 planes (x = hi + mid + lo): w S keeps six of
@@ -499,10 +501,12 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
 constexpr int kRowSB = kD + 8;   // bf16 row stride of a transposed state plane (272 B)
 constexpr int kRowVB = kC + 8;   // bf16 row stride of a transposed v' plane (144 B)
 
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gd_state_kernel(GdArgs a) {
+constexpr int kStateThreads = 512;
+
+__global__ __launch_bounds__(kStateThreads) void gd_state_kernel(GdArgs a) {
   // XCD-aware order: block b runs on XCD b % 8; the logical index below gives
   // each XCD a contiguous range, so the 8 column slices of one head (which read
-  // the same w / k tiles) share one L2.  The grid is a multiple of 8.
+  // the same w / k / q / A tiles) share one L2.  The grid is a multiple of 8.
   const int nb = gridDim.x;
   const int lb = (blockIdx.x % 8) * (nb / 8) + blockIdx.x / 8;
   const int js = lb % kSlices;
@@ -513,346 +517,280 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 
   __shared__ __attribute__((aligned(16))) uint16_t sS[3][kSlice * kRowSB];   // state planes [col][dk]
   __shared__ __attribute__((aligned(16))) uint16_t sVd[3][kSlice * kRowVB];  // e^{gl - gc} v' planes [col][t]
+  __shared__ __attribute__((aligned(16))) uint16_t sVp[3][kSlice * kRowVB];  // v' planes [col][t]
 
   const int tid = threadIdx.x;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l = tid & 63;
   const int g4 = l >> 4;
   const int c16 = l & 15;
   const int col = kSlice * js + c16;  // value column owned in the C layout
-
-  // state slice in the C layout (fp32): S[m][r] = S[dk = 32wv + 16m + 4g4 + r][col]
-  float S[2][4];
   const size_t state_base = (static_cast<size_t>(sq) * a.hv + h) * kD * kD;
-#pragma unroll
-  for (int m = 0; m < 2; ++m)
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      S[m][r] = a.s0 ? a.s0[state_base + static_cast<size_t>(32 * wv + 16 * m + 4 * g4 + r) * kD + col] : 0.0f;
 
-  // operands of one chunk, loaded straight into registers one chunk ahead; two
-  // register sets alternate (the loop body is unrolled by two) and every load is
-  // issued unconditionally (past the last chunk it re-reads the last one)
-  struct ChunkRegs {
-    uint4 w[3][4];  // plane x, step s: w_x[16wv + c16][32s + 8g4 .. +7]      (A of w S)
-    uint4 k[2][2];  // tile m, step s: k^T[32wv + 16m + c16][32s + 8g4 .. +7]  (A of k^T v')
-    float u[4];     // u[16wv + 4g4 + r][col]                                 (C layout)
-    f32x4_t dec;    // e^{gl - gc_t}, t = 16wv + 4g4 .. +3
-    float egl;      // e^{gl}
-  };
-  // Part `part` of the operand loads of chunk c: parts 0-2 are the w planes,
-  // part 3 k^T, u and the exponentials; -1 loads all of them.
-  auto load_chunk = [&](ChunkRegs& R, int c, int part = -1) {
-    c = min(c, last - 1);
-    const size_t hc = static_cast<size_t>(h) * a.nc + c;
-    // operand-ordered tiles: each wavefront load is 1 KiB contiguous (lane l = 16 g4 + c16)
-    const uint16_t* w = a.w + hc * 3 * kC * kD + (wv * 4 * 64 + l) * 8;
-#pragma unroll
-    for (int x = 0; x < 3; ++x) {
-      if (part >= 0 && part != x) continue;
-#pragma unroll
-      for (int st = 0; st < 4; ++st) R.w[x][st] = *reinterpret_cast<const uint4*>(w + x * kC * kD + st * 64 * 8);
-    }
-    if (part >= 0 && part != 3) return;
-    const uint16_t* kt = a.kn + hc * kC * kD + (wv * 4 * 64 + l) * 8;
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
-#pragma unroll
-      for (int st = 0; st < 2; ++st) R.k[m][st] = *reinterpret_cast<const uint4*>(kt + (m * 2 + st) * 64 * 8);
-    const f32x4_t u4 = *reinterpret_cast<const f32x4_t*>(a.u + hc * kC * kD + ((js * 4 + wv) * 64 + l) * 4);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) R.u[r] = u4[r];
-    const float* gx = a.gc + hc * 3 * kC;
-    R.dec = *reinterpret_cast<const f32x4_t*>(gx + kC + 16 * wv + 4 * g4);
-    R.egl = gx[2 * kC];
-  };
-
-  // One chunk.  The loads of chunk cp (two ahead) into P go out in four parts,
-  // each where the wavefront waits anyway (before a barrier, behind an issued
-  // MFMA group): the address unit takes about 16 cycles per 1 KiB load per CU,
-  // and one burst of all 19 would stall the in-order wavefront for most of a
-  // step.  sched_barrier keeps each part in place.
-  auto step = [&](const ChunkRegs& R, int c, ChunkRegs& P, int cp) {
-    const size_t hc = static_cast<size_t>(h) * a.nc + c;
-    // state at the chunk start: bf16 planes to LDS (B of w S), fp32 to the workspace (output pass)
-    // (in the output pass's B-operand order: S[dk][col] at step s = dk / 32 of column group
-    // n = js, lane 16 (dk % 32 / 8) + c16, element dk % 8; 64 lanes write 1 KiB contiguous)
-    float* sc = a.sc + hc * kD * kD + static_cast<size_t>(js) * 4 * 64 * 8;
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int dk = 32 * wv + 16 * m + 4 * g4;
-      uint2 ph, pm, pl;
-      split3x4(S[m], ph, pm, pl);
-      *reinterpret_cast<uint2*>(sS[0] + c16 * kRowSB + dk) = ph;
-      *reinterpret_cast<uint2*>(sS[1] + c16 * kRowSB + dk) = pm;
-      *reinterpret_cast<uint2*>(sS[2] + c16 * kRowSB + dk) = pl;
-      *reinterpret_cast<f32x4_t*>(sc + (wv * 64 + 16 * (2 * m + (g4 >> 1)) + c16) * 8 + 4 * (g4 & 1)) =
-          f32x4_t{S[m][0], S[m][1], S[m][2], S[m][3]};
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    load_chunk(P, cp, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
-
-    // v' = u - w S for rows 16wv..16wv+15 of this slice
-    f32x4_t acc0 = {};
-    f32x4_t acc1 = {};
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const int off = c16 * kRowSB + 32 * st + 8 * g4;
-      const uint4 sh = *reinterpret_cast<const uint4*>(sS[0] + off);
-      const uint4 sm = *reinterpret_cast<const uint4*>(sS[1] + off);
-      const uint4 sl = *reinterpret_cast<const uint4*>(sS[2] + off);
-      acc0 = mfma_bf16(R.w[0][st], sh, acc0);
-      acc1 = mfma_bf16(R.w[0][st], sm, acc1);
-      acc0 = mfma_bf16(R.w[1][st], sh, acc0);
-      acc1 = mfma_bf16(R.w[0][st], sl, acc1);
-      acc0 = mfma_bf16(R.w[1][st], sm, acc0);
-      acc1 = mfma_bf16(R.w[2][st], sh, acc1);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    load_chunk(P, cp, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    f32x4_t vnew;
-    float vdec[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      vnew[r] = R.u[r] - (acc0[r] + acc1[r]);
-      vdec[r] = vnew[r] * R.dec[r];
-    }
-    // v'[t][col] in the output pass's B-operand order: step s = t / 32, lane 16 (t % 32 / 8) + c16
-    *reinterpret_cast<f32x4_t*>(a.vn + hc * kD * kC +
-                                ((js * 2 + (wv >> 1)) * 64 + 16 * (2 * (wv & 1) + (g4 >> 1)) + c16) * 8 +
-                                4 * (g4 & 1)) = vnew;
-    {
-      const int off = c16 * kRowVB + 16 * wv + 4 * g4;
-      uint2 ph, pm, pl;
-      split3x4(vdec, ph, pm, pl);
-      *reinterpret_cast<uint2*>(sVd[0] + off) = ph;
-      *reinterpret_cast<uint2*>(sVd[1] + off) = pm;
-      *reinterpret_cast<uint2*>(sVd[2] + off) = pl;
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    load_chunk(P, cp, 2);
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
-
-    // S <- e^{gl} S + k^T (e^{gl - gc} v'), dk rows 32wv..32wv+31
-    f32x4_t st0 = {S[0][0] * R.egl, S[0][1] * R.egl, S[0][2] * R.egl, S[0][3] * R.egl};
-    f32x4_t st1 = {S[1][0] * R.egl, S[1][1] * R.egl, S[1][2] * R.egl, S[1][3] * R.egl};
-#pragma unroll
-    for (int st = 0; st < 2; ++st) {
-      const int off = c16 * kRowVB + 32 * st + 8 * g4;
-      const uint4 dh = *reinterpret_cast<const uint4*>(sVd[0] + off);
-      const uint4 dm = *reinterpret_cast<const uint4*>(sVd[1] + off);
-      const uint4 dl = *reinterpret_cast<const uint4*>(sVd[2] + off);
-      st0 = mfma_bf16(R.k[0][st], dh, st0);
-      st1 = mfma_bf16(R.k[1][st], dh, st1);
-      st0 = mfma_bf16(R.k[0][st], dm, st0);
-      st1 = mfma_bf16(R.k[1][st], dm, st1);
-      st0 = mfma_bf16(R.k[0][st], dl, st0);
-      st1 = mfma_bf16(R.k[1][st], dl, st1);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    load_chunk(P, cp, 3);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      S[0][r] = st0[r];
-      S[1][r] = st1[r];
-    }
-    // no third barrier: the next writes of sS follow this step's second barrier,
-    // and the next writes of sVd follow the next step's first
-  };
-
-  if (first < last) {
-    // three register sets, loads two chunks ahead of the step that uses them
-    ChunkRegs A, B, Cr;
-    load_chunk(A, first);
-    load_chunk(B, first + 1);
-    for (int c = first; c < last; c += 3) {
-      step(A, c, Cr, c + 2);
-      if (c + 1 < last) step(B, c + 1, A, c + 3);
-      if (c + 2 < last) step(Cr, c + 2, B, c + 4);
-    }
-  }
-
-  if (a.sN != nullptr) {
+  if (wv < 4) {
+    // ---- the state chain (wavefront wv: v' rows 16wv .. +15, state rows 32wv .. +31)
+    // state slice in the C layout (fp32): S[m][r] = S[dk = 32wv + 16m + 4g4 + r][col]
+    float S[2][4];
 #pragma unroll
     for (int m = 0; m < 2; ++m)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        a.sN[state_base + static_cast<size_t>(32 * wv + 16 * m + 4 * g4 + r) * kD + col] = S[m][r];
-  }
-}
+        S[m][r] = a.s0 ? a.s0[state_base + static_cast<size_t>(32 * wv + 16 * m + 4 * g4 + r) * kD + col] : 0.0f;
 
-// ---------------------------------------------------------------------------
-// 4. per-chunk output: o = scale e^{gc} (q S) + A v'
-// output pass: 8 wavefronts, wavefront wv owns the 16 value columns 16wv .. +15
-constexpr int kOutThreads = 512;
-constexpr int kOutRows = kOutThreads / 16;  // rows one 16-lanes-per-row sweep covers
-
-__global__ __launch_bounds__(kOutThreads, 2) void gd_out_kernel(GdArgs a) {
-  const int h = blockIdx.x % a.hv;
-  const int c = blockIdx.x / a.hv;
-  int r0, L;
-  chunk_rows(a, c, &r0, &L);
-  if (L <= 0) return;
-  const size_t hc = static_cast<size_t>(h) * a.nc + c;
-
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[kC * kRowK];
-  __shared__ __attribute__((aligned(16))) float sA[kC * kRowF];
-  __shared__ __attribute__((aligned(16))) uint16_t sO[kC * kRowK];  // bf16 output rows (norm epilogue)
-  __shared__ float sG[kC];
-
-  const int tid = threadIdx.x;
-  const int wv = tid >> 6;
-  const int l = tid & 63;
-  const int g4 = l >> 4;
-  const int c16 = l & 15;
-
-  const uint16_t* gq = a.qn + hc * kC * kD;
-  const float* gaq = a.aq + hc * kC * kC;
+    // operands of one chunk, loaded straight into registers two chunks ahead;
+    // three register sets rotate (the loop body is unrolled by three) and every
+    // load is issued unconditionally (past the last chunk it re-reads the last one)
+    struct ChunkRegs {
+      uint4 w[3][4];  // plane x, step s: w_x[16wv + c16][32s + 8g4 .. +7]      (A of w S)
+      uint4 k[2][2];  // tile m, step s: k^T[32wv + 16m + c16][32s + 8g4 .. +7]  (A of k^T v')
+      float u[4];     // u[16wv + 4g4 + r][col]                                 (C layout)
+      f32x4_t dec;    // e^{gl - gc_t}, t = 16wv + 4g4 .. +3
+      float egl;      // e^{gl}
+    };
+    // Part `part` of the operand loads of chunk c: parts 0-2 are the w planes,
+    // part 3 k^T, u and the exponentials; -1 loads all of them.
+    auto load_chunk = [&](ChunkRegs& R, int c, int part = -1) {
+      c = min(c, last - 1);
+      const size_t hc = static_cast<size_t>(h) * a.nc + c;
+      const uint16_t* w = a.w + hc * 3 * kC * kD + (wv * 4 * 64 + l) * 8;
 #pragma unroll
-  for (int i = 0; i < kC * 16 / kOutThreads; ++i) {
-    const int row = (tid >> 4) + (kOutThreads / 16) * i;
-    *reinterpret_cast<uint4*>(sQ + row * kRowK + (tid & 15) * 8) =
-        *reinterpret_cast<const uint4*>(gq + row * kD + (tid & 15) * 8);
-    const int idx = 4 * tid + 4 * kOutThreads * i;
-    *reinterpret_cast<f32x4_t*>(sA + (idx >> 6) * kRowF + (idx & 63)) = *reinterpret_cast<const f32x4_t*>(gaq + idx);
-  }
-  if (wv == 0) sG[l] = a.gc[hc * 3 * kC + l];  // e^{gc_t}
-  // the norm epilogue's gate rows and their silu(z) = z / (1 + exp(-z)), computed now so that the
-  // loads and the VALU work overlap the MFMA phase (16 lanes per row, row it * kOutRows + tid / 16;
-  // rows past the chunk's end use row L - 1)
-  float act[kC / kOutRows][8];
-  if (a.z != nullptr) {
+      for (int x = 0; x < 3; ++x) {
+        if (part >= 0 && part != x) continue;
 #pragma unroll
-    for (int it = 0; it < kC / kOutRows; ++it) {
-      const int t = it * kOutRows + (tid >> 4);
-      const int tc = t < L ? t : L - 1;
-      float zv[8];
-      unpack8(*reinterpret_cast<const uint4*>(a.z + static_cast<int64_t>(r0 + tc) * a.z_ts + h * a.z_hs +
-                                              (tid & 15) * 8), zv);
+        for (int st = 0; st < 4; ++st) R.w[x][st] = *reinterpret_cast<const uint4*>(w + x * kC * kD + st * 64 * 8);
+      }
+      if (part >= 0 && part != 3) return;
+      const uint16_t* kt = a.kn + hc * kC * kD + (wv * 4 * 64 + l) * 8;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) act[it][e] = zv[e] / (1.0f + expf(-zv[e]));
-    }
-  }
-  __syncthreads();
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) R.k[m][st] = *reinterpret_cast<const uint4*>(kt + (m * 2 + st) * 64 * 8);
+      const f32x4_t u4 = *reinterpret_cast<const f32x4_t*>(a.u + hc * kC * kD + ((js * 4 + wv) * 64 + l) * 4);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) R.u[r] = u4[r];
+      const float* gx = a.gc + hc * 3 * kC;
+      R.dec = *reinterpret_cast<const f32x4_t*>(gx + kC + 16 * wv + 4 * g4);
+      R.egl = gx[2 * kC];
+    };
 
-  // bf16 MFMA over exact three-plane splits of the fp32 operands: q S takes the
-  // three products of the bf16 q with S's planes, A v' six of the nine plane products
-  const size_t o_row = static_cast<size_t>(a.hv) * kD;
-  auto split8 = [](const float* p, uint4& hi, uint4& mid, uint4& lo) {
-    const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(p);
-    const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(p + 4);
-    const float va[4] = {v0[0], v0[1], v0[2], v0[3]};
-    const float vb[4] = {v1[0], v1[1], v1[2], v1[3]};
-    uint2 ha, ma, la, hb, mb, lb;
-    split3x4(va, ha, ma, la);
-    split3x4(vb, hb, mb, lb);
-    hi = make_uint4(ha.x, ha.y, hb.x, hb.y);
-    mid = make_uint4(ma.x, ma.y, mb.x, mb.y);
-    lo = make_uint4(la.x, la.y, lb.x, lb.y);
-  };
-  {
-    const int n = wv;  // 16 value columns
-    // B operands: S[32s + 8g4 .. +7][16n + c16] and v'[32s + 8g4 .. +7][16n + c16], stored in
-    // this order by the state pass (each lane reads 32 B, a wavefront 2 KiB contiguous)
-    uint4 bS[3][4], bN[3][2];
-    const float* sc = a.sc + hc * kD * kD + (static_cast<size_t>(n) * 4 * 64 + l) * 8;
+    // One chunk.  The loads of chunk cp (two ahead) into P go out in four parts,
+    // each where the wavefront waits anyway (before a barrier, behind an issued
+    // MFMA group): the address unit takes about 16 cycles per 1 KiB load per CU,
+    // and one burst of all 19 would stall the in-order wavefront for most of a
+    // step.  sched_barrier keeps each part in place.
+    auto step = [&](const ChunkRegs& R, int c, ChunkRegs& P, int cp) {
+      // state at the chunk start: bf16 planes to LDS (B of w S and of the output's q S)
 #pragma unroll
-    for (int st = 0; st < 4; ++st) split8(sc + st * 64 * 8, bS[0][st], bS[1][st], bS[2][st]);
-    const float* vn = a.vn + hc * kD * kC + (static_cast<size_t>(n) * 2 * 64 + l) * 8;
-#pragma unroll
-    for (int st = 0; st < 2; ++st) split8(vn + st * 64 * 8, bN[0][st], bN[1][st], bN[2][st]);
-#pragma unroll 1
-    for (int rt = 0; rt < 4; ++rt) {
-      // A operands: q[16rt + c16][32s + 8g4 .. +7] (bf16) and A[16rt + c16][32s + 8g4 .. +7] (fp32, split)
+      for (int m = 0; m < 2; ++m) {
+        const int dk = 32 * wv + 16 * m + 4 * g4;
+        uint2 ph, pm, pl;
+        split3x4(S[m], ph, pm, pl);
+        *reinterpret_cast<uint2*>(sS[0] + c16 * kRowSB + dk) = ph;
+        *reinterpret_cast<uint2*>(sS[1] + c16 * kRowSB + dk) = pm;
+        *reinterpret_cast<uint2*>(sS[2] + c16 * kRowSB + dk) = pl;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      load_chunk(P, cp, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+
+      // v' = u - w S for rows 16wv..16wv+15 of this slice
+      f32x4_t acc0 = {};
       f32x4_t acc1 = {};
-      f32x4_t acc2 = {};
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        const uint4 aq = *reinterpret_cast<const uint4*>(sQ + (16 * rt + c16) * kRowK + 32 * st + 8 * g4);
-        acc1 = mfma_bf16(aq, bS[0][st], acc1);
-        acc1 = mfma_bf16(aq, bS[1][st], acc1);
-        acc1 = mfma_bf16(aq, bS[2][st], acc1);
+        const int off = c16 * kRowSB + 32 * st + 8 * g4;
+        const uint4 sh = *reinterpret_cast<const uint4*>(sS[0] + off);
+        const uint4 sm = *reinterpret_cast<const uint4*>(sS[1] + off);
+        const uint4 sl = *reinterpret_cast<const uint4*>(sS[2] + off);
+        acc0 = mfma_bf16(R.w[0][st], sh, acc0);
+        acc1 = mfma_bf16(R.w[0][st], sm, acc1);
+        acc0 = mfma_bf16(R.w[1][st], sh, acc0);
+        acc1 = mfma_bf16(R.w[0][st], sl, acc1);
+        acc0 = mfma_bf16(R.w[1][st], sm, acc0);
+        acc1 = mfma_bf16(R.w[2][st], sh, acc1);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      load_chunk(P, cp, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4_t vnew;
+      float vdec[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        vnew[r] = R.u[r] - (acc0[r] + acc1[r]);
+        vdec[r] = vnew[r] * R.dec[r];
+      }
+      {
+        const int off = c16 * kRowVB + 16 * wv + 4 * g4;
+        uint2 ph, pm, pl;
+        split3x4(vdec, ph, pm, pl);
+        *reinterpret_cast<uint2*>(sVd[0] + off) = ph;
+        *reinterpret_cast<uint2*>(sVd[1] + off) = pm;
+        *reinterpret_cast<uint2*>(sVd[2] + off) = pl;
+        // v'[t][col] planes for the output wavefronts
+        const float vv[4] = {vnew[0], vnew[1], vnew[2], vnew[3]};
+        split3x4(vv, ph, pm, pl);
+        *reinterpret_cast<uint2*>(sVp[0] + off) = ph;
+        *reinterpret_cast<uint2*>(sVp[1] + off) = pm;
+        *reinterpret_cast<uint2*>(sVp[2] + off) = pl;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      load_chunk(P, cp, 2);
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+
+      // S <- e^{gl} S + k^T (e^{gl - gc} v'), dk rows 32wv..32wv+31
+      f32x4_t st0 = {S[0][0] * R.egl, S[0][1] * R.egl, S[0][2] * R.egl, S[0][3] * R.egl};
+      f32x4_t st1 = {S[1][0] * R.egl, S[1][1] * R.egl, S[1][2] * R.egl, S[1][3] * R.egl};
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
-        uint4 ah, am, al;
-        split8(sA + (16 * rt + c16) * kRowF + 32 * st + 8 * g4, ah, am, al);
-        acc2 = mfma_bf16(ah, bN[0][st], acc2);
-        acc2 = mfma_bf16(ah, bN[1][st], acc2);
-        acc2 = mfma_bf16(am, bN[0][st], acc2);
-        acc2 = mfma_bf16(ah, bN[2][st], acc2);
-        acc2 = mfma_bf16(am, bN[1][st], acc2);
-        acc2 = mfma_bf16(al, bN[0][st], acc2);
+        const int off = c16 * kRowVB + 32 * st + 8 * g4;
+        const uint4 dh = *reinterpret_cast<const uint4*>(sVd[0] + off);
+        const uint4 dm = *reinterpret_cast<const uint4*>(sVd[1] + off);
+        const uint4 dl = *reinterpret_cast<const uint4*>(sVd[2] + off);
+        st0 = mfma_bf16(R.k[0][st], dh, st0);
+        st1 = mfma_bf16(R.k[1][st], dh, st1);
+        st0 = mfma_bf16(R.k[0][st], dm, st0);
+        st1 = mfma_bf16(R.k[1][st], dm, st1);
+        st0 = mfma_bf16(R.k[0][st], dl, st0);
+        st1 = mfma_bf16(R.k[1][st], dl, st1);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      load_chunk(P, cp, 3);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        S[0][r] = st0[r];
+        S[1][r] = st1[r];
+      }
+      // no third barrier: the next writes of sS follow this step's second
+      // barrier, and the next writes of sVd and sVp follow the next step's first
+    };
+
+    if (first < last) {
+      ChunkRegs A, B, Cr;
+      load_chunk(A, first);
+      load_chunk(B, first + 1);
+      for (int c = first; c < last; c += 3) {
+        step(A, c, Cr, c + 2);
+        if (c + 1 < last) step(B, c + 1, A, c + 3);
+        if (c + 2 < last) step(Cr, c + 2, B, c + 4);
+      }
+    }
+
+    if (a.sN != nullptr) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          a.sN[state_base + static_cast<size_t>(32 * wv + 16 * m + 4 * g4 + r) * kD + col] = S[m][r];
+    }
+  } else {
+    // ---- the chunk outputs (wavefront wv: rows 16rt .. +15 of every chunk)
+    //   o[t][col] = scale e^{gc_t} (q S_chunk)[t][col] + (A v')[t][col]
+    // q S takes the three products of the bf16 q with the state planes the
+    // chain wrote; A v' six of the nine plane products of exact three-plane
+    // splits of the fp32 A and v'.
+    const int rt = wv - 4;
+    const size_t o_row = static_cast<size_t>(a.hv) * kD;
+    struct OutRegs {
+      uint4 q[4];       // q[16rt + c16][32st + 8g4 .. +7]
+      f32x4_t av[2][2];  // A[16rt + c16][32st + 8g4 + 4i .. +3]
+      f32x4_t eg;       // e^{gc_t}, t = 16rt + 4g4 .. +3
+    };
+    auto load_out = [&](OutRegs& R, int c) {
+      c = min(c, last - 1);
+      const size_t hc = static_cast<size_t>(h) * a.nc + c;
+      const uint16_t* qp = a.qn + hc * kC * kD + (rt * 4 * 64 + l) * 8;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) R.q[st] = *reinterpret_cast<const uint4*>(qp + st * 64 * 8);
+      const float* ap = a.aq + hc * kC * kC + (rt * 2 * 64 + l) * 8;
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        R.av[st][0] = *reinterpret_cast<const f32x4_t*>(ap + st * 64 * 8);
+        R.av[st][1] = *reinterpret_cast<const f32x4_t*>(ap + st * 64 * 8 + 4);
+      }
+      R.eg = *reinterpret_cast<const f32x4_t*>(a.gc + hc * 3 * kC + 16 * rt + 4 * g4);
+    };
+    auto split8v = [](f32x4_t v0, f32x4_t v1, uint4& hi, uint4& mid, uint4& lo) {
+      const float va[4] = {v0[0], v0[1], v0[2], v0[3]};
+      const float vb[4] = {v1[0], v1[1], v1[2], v1[3]};
+      uint2 ha, ma, la, hb, mb, lb;
+      split3x4(va, ha, ma, la);
+      split3x4(vb, hb, mb, lb);
+      hi = make_uint4(ha.x, ha.y, hb.x, hb.y);
+      mid = make_uint4(ma.x, ma.y, mb.x, mb.y);
+      lo = make_uint4(la.x, la.y, lb.x, lb.y);
+    };
+    // the barriers match the chain's step: the first finds the chunk-start
+    // state planes in sS, the second the v' planes in sVp
+    auto out_step = [&](const OutRegs& R, int c, OutRegs& P, int cp) {
+      __syncthreads();
+      // the chain's operand reads of the state planes go first: the A split and
+      // the next chunk's loads (no LDS) come before this wavefront's own reads
+      uint4 ah[2], am[2], al[2];
+      split8v(R.av[0][0], R.av[0][1], ah[0], am[0], al[0]);
+      load_out(P, cp);
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4_t acc1 = {};
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int off = c16 * kRowSB + 32 * st + 8 * g4;
+        const uint4 sh = *reinterpret_cast<const uint4*>(sS[0] + off);
+        const uint4 sm = *reinterpret_cast<const uint4*>(sS[1] + off);
+        const uint4 sl = *reinterpret_cast<const uint4*>(sS[2] + off);
+        acc1 = mfma_bf16(R.q[st], sh, acc1);
+        acc1 = mfma_bf16(R.q[st], sm, acc1);
+        acc1 = mfma_bf16(R.q[st], sl, acc1);
+      }
+      __syncthreads();
+      // likewise the chain's reads of the e^{gl - gc} v' planes go first
+      split8v(R.av[1][0], R.av[1][1], ah[1], am[1], al[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4_t acc2 = {};
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const int off = c16 * kRowVB + 32 * st + 8 * g4;
+        const uint4 b0 = *reinterpret_cast<const uint4*>(sVp[0] + off);
+        const uint4 b1 = *reinterpret_cast<const uint4*>(sVp[1] + off);
+        const uint4 b2 = *reinterpret_cast<const uint4*>(sVp[2] + off);
+        acc2 = mfma_bf16(ah[st], b0, acc2);
+        acc2 = mfma_bf16(ah[st], b1, acc2);
+        acc2 = mfma_bf16(am[st], b0, acc2);
+        acc2 = mfma_bf16(ah[st], b2, acc2);
+        acc2 = mfma_bf16(am[st], b1, acc2);
+        acc2 = mfma_bf16(al[st], b0, acc2);
+      }
+      int r0, L;
+      chunk_rows(a, c, &r0, &L);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = 16 * rt + 4 * g4 + r;
         if (t < L) {
-          const float val = (a.scale * sG[t]) * acc1[r] + acc2[r];
-          const uint16_t bits = static_cast<uint16_t>(fd_pack2(val, 0.0f));
-          if (a.z != nullptr)
-            sO[t * kRowK + 16 * n + c16] = bits;
-          else
-            a.o[static_cast<size_t>(r0 + t) * o_row + h * kD + 16 * n + c16] = bits;
+          const float val = (a.scale * R.eg[r]) * acc1[r] + acc2[r];
+          a.o[static_cast<size_t>(r0 + t) * o_row + h * kD + col] = static_cast<uint16_t>(fd_pack2(val, 0.0f));
         }
       }
-    }
-  }
-  if (a.z == nullptr) return;
+    };
 
-  // gated RMSNorm of the chunk's rows of this head, 16 lanes per row with the
-  // fd_gated_rmsnorm_fwd sequence (lane sums of 8 squares, xor butterfly 8/4/2/1):
-  //   y = bf16(x / sqrt(mean(x^2) + eps)); y2 = bf16(w y) (fp32 for an fp32 weight);
-  //   out = bf16(y2 * z / (1 + exp(-z)))
-  __syncthreads();
-  const int ln = tid & 15;
-  // this lane's 8 norm weights, as fp32 values
-  float nwv[8];
-  if (a.nw_vec && a.nw_f32) {
-    const float4 w0 = *reinterpret_cast<const float4*>(static_cast<const float*>(a.nw) + ln * 8);
-    const float4 w1 = *reinterpret_cast<const float4*>(static_cast<const float*>(a.nw) + ln * 8 + 4);
-    nwv[0] = w0.x; nwv[1] = w0.y; nwv[2] = w0.z; nwv[3] = w0.w;
-    nwv[4] = w1.x; nwv[5] = w1.y; nwv[6] = w1.z; nwv[7] = w1.w;
-  } else if (a.nw_vec) {
-    unpack8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.nw) + ln * 8), nwv);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      nwv[e] = a.nw_f32 ? static_cast<const float*>(a.nw)[ln * 8 + e]
-                        : fd_bf16_to_f32(static_cast<const uint16_t*>(a.nw)[ln * 8 + e]);
-  }
-#pragma unroll
-  for (int it = 0; it < kC / kOutRows; ++it) {
-    const int t = it * kOutRows + (tid >> 4);
-    const int tc = t < L ? t : L - 1;  // rows past the chunk's end compute on row L - 1 and store nothing
-    float xv[8], y[8];
-    unpack8(*reinterpret_cast<const uint4*>(sO + tc * kRowK + ln * 8), xv);
-    float s = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s = s + xv[e] * xv[e];
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) s = s + __shfl_xor(s, off);
-    const float inv = 1.0f / __builtin_sqrtf(s / static_cast<float>(kD) + a.norm_eps);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float yn = bf16r(xv[e] * inv);
-      const float gw = a.nw_f32 ? nwv[e] * yn : bf16r(nwv[e] * yn);
-      y[e] = gw * act[it][e];
+    if (first < last) {
+      OutRegs A, B, Cr;
+      load_out(A, first);
+      load_out(B, first + 1);
+      for (int c = first; c < last; c += 3) {
+        out_step(A, c, Cr, c + 2);
+        if (c + 1 < last) out_step(B, c + 1, A, c + 3);
+        if (c + 2 < last) out_step(Cr, c + 2, B, c + 4);
+      }
     }
-    if (t < L) *reinterpret_cast<uint4*>(a.o + static_cast<size_t>(r0 + t) * o_row + h * kD + ln * 8) = pack8(y);
   }
 }
 
 struct GdLayout {
-  size_t row0, len, first, gc, qn, kn, w, u, vn, aq, sc, total;
+  size_t row0, len, first, gc, qn, kn, w, u, aq, ob, total;
 };
 
-GdLayout gd_layout(int64_t nc, int64_t hv, int64_t nseq) {
+GdLayout gd_layout(int64_t nc, int64_t hv, int64_t nseq, int64_t tokens) {
   auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
   const size_t hc = static_cast<size_t>(hv) * static_cast<size_t>(nc);
   GdLayout L;
@@ -873,12 +811,10 @@ GdLayout gd_layout(int64_t nc, int64_t hv, int64_t nseq) {
   off = al(off + hc * 3 * kC * kD * 2);
   L.u = off;
   off = al(off + hc * kC * kD * 4);
-  L.vn = off;
-  off = al(off + hc * kD * kC * 4);
   L.aq = off;
   off = al(off + hc * kC * kC * 4);
-  L.sc = off;
-  off = al(off + hc * kD * kD * 4);
+  L.ob = off;
+  off = al(off + static_cast<size_t>(tokens) * hv * kD * 2);
   L.total = off;
   return L;
 }
@@ -906,7 +842,7 @@ extern "C" FD_API int64_t fd_gated_delta_workspace_bytes(int batch, int seq_len,
   if (v_heads <= 0 || head_k_dim != kD || head_v_dim != kD) return FD_ERR_UNSUPPORTED;
   int64_t nc = 0, nseq = 0;
   if (!gd_counts(batch, seq_len, n_seqs, n_seqs > 0, &nc, &nseq)) return FD_ERR_INVALID_ARGUMENT;
-  return static_cast<int64_t>(gd_layout(nc, v_heads, nseq).total);
+  return static_cast<int64_t>(gd_layout(nc, v_heads, nseq, static_cast<int64_t>(batch) * seq_len).total);
 }
 
 namespace {
@@ -949,7 +885,8 @@ int gd_run(const void* q, const void* k, const void* v, const float* g, const vo
   FD_REQUIRE(nc * v_heads < (1LL << 31) && nseq * v_heads * kSlices < (1LL << 31), FD_ERR_INVALID_ARGUMENT,
              "fd_gated_delta_fwd: problem too large");
   if (nseq == 0) return FD_OK;  // empty batch: nothing to launch
-  const GdLayout lay = gd_layout(nc, v_heads, nseq);
+  const int64_t total = static_cast<int64_t>(batch) * seq_len;
+  const GdLayout lay = gd_layout(nc, v_heads, nseq, total);
   FD_REQUIRE(workspace_bytes >= static_cast<int64_t>(lay.total), FD_ERR_INVALID_ARGUMENT,
              "fd_gated_delta_fwd: workspace too small (%lld bytes, need %lld)",
              static_cast<long long>(workspace_bytes), static_cast<long long>(lay.total));
@@ -961,7 +898,8 @@ int gd_run(const void* q, const void* k, const void* v, const float* g, const vo
   a.v = static_cast<const uint16_t*>(v);
   a.g = g;
   a.beta = beta;
-  a.o = static_cast<uint16_t*>(out);
+  // with the gated norm the raw output rows go to the workspace and the norm writes `out`
+  a.o = norm ? reinterpret_cast<uint16_t*>(ws + lay.ob) : static_cast<uint16_t*>(out);
   a.s0 = initial_state;
   a.sN = final_state;
   a.row0 = reinterpret_cast<int32_t*>(ws + lay.row0);
@@ -972,9 +910,7 @@ int gd_run(const void* q, const void* k, const void* v, const float* g, const vo
   a.kn = reinterpret_cast<uint16_t*>(ws + lay.kn);
   a.w = reinterpret_cast<uint16_t*>(ws + lay.w);
   a.u = reinterpret_cast<float*>(ws + lay.u);
-  a.vn = reinterpret_cast<float*>(ws + lay.vn);
   a.aq = reinterpret_cast<float*>(ws + lay.aq);
-  a.sc = reinterpret_cast<float*>(ws + lay.sc);
   a.hk = k_heads;
   a.hv = v_heads;
   a.nc = static_cast<int>(nc);
@@ -985,26 +921,21 @@ int gd_run(const void* q, const void* k, const void* v, const float* g, const vo
   a.beta_f32 = beta_dtype == FD_DTYPE_F32;
   a.l2norm = l2norm_qk != 0;
   a.scale = scale;
-  a.z = norm ? static_cast<const uint16_t*>(norm->z) : nullptr;
-  a.z_ts = norm ? norm->z_ts : 0;
-  a.z_hs = norm ? norm->z_hs : 0;
-  a.nw = norm ? norm->w : nullptr;
-  a.nw_f32 = norm ? norm->w_dtype == FD_DTYPE_F32 : 0;
-  a.nw_vec = norm ? fd_aligned16(norm->w) : 0;
-  a.norm_eps = norm ? norm->eps : 0.0f;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int total = batch * seq_len;
-  if (varlen) hipLaunchKernelGGL(gd_chunk_table, dim3(1), dim3(kThreads), 0, s, cu_seqlens, a.nseq, seq_len, total, a);
+  if (varlen)
+    hipLaunchKernelGGL(gd_chunk_table, dim3(1), dim3(kThreads), 0, s, cu_seqlens, a.nseq, seq_len,
+                       static_cast<int>(total), a);
   if (nc > 0) {
     hipLaunchKernelGGL(gd_prep_kernel, dim3(static_cast<unsigned>(nc * v_heads)), dim3(kThreads), 0, s, a);
   }
-  hipLaunchKernelGGL(gd_state_kernel, dim3(static_cast<unsigned>(nseq * v_heads * kSlices)), dim3(kThreads), 0, s,
-                     a);
-  if (nc > 0) {
-    hipLaunchKernelGGL(gd_out_kernel, dim3(static_cast<unsigned>(nc * v_heads)), dim3(kOutThreads), 0, s, a);
-  }
-  return fd_check_launch("fd_gated_delta_fwd");
+  hipLaunchKernelGGL(gd_state_kernel, dim3(static_cast<unsigned>(nseq * v_heads * kSlices)), dim3(kStateThreads), 0,
+                     s, a);
+  const int rc = fd_check_launch("fd_gated_delta_fwd");
+  if (rc != FD_OK || norm == nullptr || total == 0) return rc;
+  // the layer's gated RMSNorm over the raw output rows (one row per token and value head)
+  return fd_gated_rmsnorm_fwd(a.o, norm->z, norm->z_ts, norm->z_hs, v_heads, norm->w, norm->w_dtype, out,
+                              total * v_heads, kD, norm->eps, stream);
 }
 
 }  // namespace

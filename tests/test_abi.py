@@ -129,9 +129,10 @@ def test_gated_delta_argument_errors():
     f = 1 << 20
     need = lib.fd_gated_delta_workspace_bytes(1, 2048, 16, 128, 128, 0)
     # 32 chunks x 16 heads of per-chunk intermediates, plus the chunk table: exponentials,
-    # q and k in bf16, w in three bf16 planes, u and v' in fp32, A in fp32, the chunk-start state
-    per_chunk = (3 * 64 * 4 + 2 * 64 * 128 * 2 + 3 * 64 * 128 * 2 + 2 * 64 * 128 * 4 + 64 * 64 * 4
-                 + 128 * 128 * 4)
+    # q and k in bf16, w in three bf16 planes, u in fp32, A in fp32, and the bf16 output rows
+    # the gated norm reads (64 tokens x 128 per chunk and head)
+    per_chunk = (3 * 64 * 4 + 2 * 64 * 128 * 2 + 3 * 64 * 128 * 2 + 64 * 128 * 4 + 64 * 64 * 4
+                 + 64 * 128 * 2)
     assert need >= 32 * 16 * per_chunk and need < 32 * 16 * per_chunk + 4096
     assert lib.fd_gated_delta_workspace_bytes(1, 2048, 16, 64, 128, 0) == _lib.FD_ERR_UNSUPPORTED
     assert lib.fd_gated_delta_workspace_bytes(2, 100, 4, 128, 128, 3) == _lib.FD_ERR_INVALID_ARGUMENT
