@@ -33,7 +33,7 @@ def _gated_delta_rule_fake(q, k, v, g, beta, cu_seqlens):
 def gated_delta_rule_norm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
                           z: torch.Tensor, norm_weight: torch.Tensor, eps: float,
                           cu_seqlens: Optional[torch.Tensor]) -> torch.Tensor:
-    """The delta rule followed by the layer's gated RMSNorm in the same output pass
+    """The delta rule followed by the layer's gated RMSNorm in one call of the library
     (``self.norm(core_attn_out, z)``, ref: src/decider/packed_conv.py:60-61)."""
     out, _ = chunk_gated_delta_rule(q, k, v, g, beta, use_qk_l2norm_in_kernel=True, cu_seqlens=cu_seqlens,
                                     norm=(z, norm_weight, eps))

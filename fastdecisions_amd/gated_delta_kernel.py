@@ -18,9 +18,10 @@ Differences a caller can see:
   must be bf16, g fp32, beta bf16 or fp32; the output is bf16;
 * ``norm=(z, weight, eps)`` applies the layer's gated RMSNorm
   (transformers ``Qwen3_5RMSNormGated``, the call after the delta rule at
-  ref: src/decider/packed_conv.py:60-61) inside the output pass
-  (``fd_gated_delta_norm_fwd``): the result equals ``gated_rms_norm`` of the
-  plain output, bit for bit; z is a ``[B, T, Hv, Dv]`` bf16 view.
+  ref: src/decider/packed_conv.py:60-61) in the same library call
+  (``fd_gated_delta_norm_fwd``: the delta rule's rows pass through the
+  workspace): the result equals ``gated_rms_norm`` of the plain output, bit
+  for bit; z is a ``[B, T, Hv, Dv]`` bf16 view.
 """
 from __future__ import annotations
 

@@ -156,7 +156,7 @@ def _forward(self, hidden_states, cache_params=None, attention_mask=None, **kwar
         beta = b.sigmoid()
         g = -self.A_log.float().exp() * F.softplus(a.float() + self.dt_bias)
     if getattr(self, "_fd_gated_delta", False) and getattr(self, "_fd_gated_norm", False):
-        # the delta rule with the gated RMSNorm in its output pass (one kernel sequence)
+        # the delta rule and the gated RMSNorm in one library call (one kernel sequence)
         from .gated_delta import gated_delta_rule_norm
         core_attn_out = gated_delta_rule_norm(query, key, value, g, beta, z, self.norm.weight,
                                               float(self.norm.variance_epsilon), cu_seqlens)

@@ -17,7 +17,7 @@
  *   fd_gated_delta_fwd  chunked gated delta rule of the Gated-DeltaNet layers
  *                       replaces the torch_chunk_gated_delta_rule call
  *                       (ref: src/decider/packed_conv.py:55-59)
- *   fd_gated_delta_norm_fwd  fd_gated_delta_fwd with the layer's gated RMSNorm applied in the output pass
+ *   fd_gated_delta_norm_fwd  fd_gated_delta_fwd followed by the layer's gated RMSNorm
  *   fd_gqa_gated_fwd    fd_gqa_fwd with the attention layer's sigmoid output gate applied in the store
  *   fd_attn_prologue_fwd   q/k RMSNorm over head_dim + partial rotary embedding of the attention layers
  *                       replaces the eager prologue of the patched attention forward
@@ -335,7 +335,7 @@ FD_API int fd_gated_delta_fwd(const void* q, const void* k, const void* v, const
  *
  * Limit: fd_gated_delta_workspace_bytes of the same sizes must not exceed
  * FD_GD_SCRATCH_BYTES (the decider's B=1, T=2048, 16-value-head call needs
- * about 113 MiB), else FD_ERR_UNSUPPORTED.  Every call on one GPU shares that
+ * about 73 MiB), else FD_ERR_UNSUPPORTED.  Every call on one GPU shares that
  * GPU's scratch: calls that overlap on one GPU (other streams, other threads)
  * race and must be serialised by the caller.  The scratch needs no clearing:
  * each call writes every byte it reads.  The first call on a device looks the
@@ -351,7 +351,8 @@ FD_API int fd_gated_delta_fwd_noalloc(const void* q, const void* k, const void* 
 /*
  * fd_gated_delta_fwd followed by the layer's gated RMSNorm (transformers
  * Qwen3_5RMSNormGated, the call after the delta rule at ref: src/decider/packed_conv.py:60-61),
- * applied in the output pass to each (token, head) row of 128 before it is stored:
+ * applied to each (token, head) row of 128 (the delta rule's rows go to the workspace,
+ * and fd_gated_rmsnorm_fwd's kernel normalises them into `out`):
  *   x = bf16(delta-rule output);  y = bf16(x / sqrt(mean(x^2) + eps));
  *   y2 = bf16(w * y) (fp32 for an fp32 weight);  out = bf16(y2 * z / (1 + exp(-z)))
  * the same values fd_gated_delta_fwd then fd_gated_rmsnorm_fwd produce.

@@ -197,7 +197,7 @@ def test_wrapper_rejects_bad_inputs():
 
 
 def test_norm_epilogue_equals_delta_rule_then_gated_norm():
-    """fd_gated_delta_norm_fwd: the gated RMSNorm applied in the output pass gives the
+    """fd_gated_delta_norm_fwd: the delta rule with the gated RMSNorm in one call gives the
     values of fd_gated_delta_fwd followed by fd_gated_rmsnorm_fwd, bit for bit (a ragged
     tail, grouped heads, the decider shape, packed requests with an empty one, bf16 and
     fp32 norm weights; the gate is a strided view as in the combined projection)."""
