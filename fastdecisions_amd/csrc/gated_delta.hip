@@ -786,6 +786,9 @@ __global__ __launch_bounds__(kStateThreads) void gd_state_kernel(GdArgs a) {
   }
 }
 
+// Byte offsets of the workspace regions: the chunk table, the per-(head, chunk)
+// intermediates GdArgs describes, and `ob`, the raw bf16 output rows
+// [tokens, Hv, 128] that the gated norm reads (fd_gated_delta_norm_fwd only).
 struct GdLayout {
   size_t row0, len, first, gc, qn, kn, w, u, aq, ob, total;
 };
