@@ -889,6 +889,9 @@ int gd_run(const void* q, const void* k, const void* v, const float* g, const vo
              "fd_gated_delta_fwd: problem too large");
   if (nseq == 0) return FD_OK;  // empty batch: nothing to launch
   const int64_t total = static_cast<int64_t>(batch) * seq_len;
+  // the gated norm runs over total * v_heads rows (checked here so nothing is launched if it cannot)
+  FD_REQUIRE(norm == nullptr || total * v_heads < (1LL << 31), FD_ERR_INVALID_ARGUMENT,
+             "fd_gated_delta_norm_fwd: problem too large (batch * seq_len * v_heads must be < 2^31)");
   const GdLayout lay = gd_layout(nc, v_heads, nseq, total);
   FD_REQUIRE(workspace_bytes >= static_cast<int64_t>(lay.total), FD_ERR_INVALID_ARGUMENT,
              "fd_gated_delta_fwd: workspace too small (%lld bytes, need %lld)",

@@ -157,6 +157,30 @@ def test_gated_delta_argument_errors():
     assert call(B=0, ws=0) == _lib.FD_OK  # empty batch: nothing to launch
 
 
+def test_gated_delta_norm_argument_errors():
+    """fd_gated_delta_norm_fwd checks the norm's arguments, and the row count of the norm that
+    follows the delta rule, before anything is launched (no HIP call: the pointers are never read)."""
+    from fastdecisions_amd import _lib
+    lib = _lib.lib()
+    f = 1 << 20
+    need = lib.fd_gated_delta_workspace_bytes(1, 2048, 16, 128, 128, 0)
+
+    def call(z=f, zts=16 * 128 * 2, zhs=128, w=f, wdt=0, eps=1e-6, T=2048, ws=need):
+        return lib.fd_gated_delta_norm_fwd(f, f, f, f, f, z, zts, zhs, w, wdt, eps, f, None, None, f, ws,
+                                           1, T, 16, 16, 128, 128, 0.088, 0, 1, None, 0, None)
+
+    assert call(z=None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert call(w=None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert call(wdt=7) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert call(eps=-1.0) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert call(zhs=100) == _lib.FD_ERR_ALIGNMENT
+    assert call(zts=128) == _lib.FD_ERR_ALIGNMENT  # the token stride must cover the 16 heads
+    assert call(z=f + 8) == _lib.FD_ERR_ALIGNMENT
+    # 2^27 tokens x 16 value heads = 2^31 norm rows: refused before the delta rule is launched
+    assert call(T=1 << 27, ws=1 << 62) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert "problem too large" in _err(lib)
+
+
 def test_noalloc_delta_rule_rejects_sizes_beyond_its_static_scratch():
     """fd_gated_delta_fwd_noalloc checks its sizes against the static scratch before any HIP call."""
     from fastdecisions_amd import _lib
