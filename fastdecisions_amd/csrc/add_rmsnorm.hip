@@ -7,17 +7,24 @@
 // residual emitted as a second output, as the eager decoder layer does
 // (transformers Qwen3_5DecoderLayer residual add, Qwen3_5RMSNorm).
 //
-// HBM-bound: one 64-lane wavefront owns one row.  Lane l loads 16-byte
-// vectors (8 bf16) at chunks l, l+64, l+128, ... so each wavefront load
-// instruction reads 1 KiB contiguous; the whole row stays in registers between
-// the reduction and the store, so x and residual are read from HBM exactly
-// once.  No LDS, no barrier: the sum of squares is reduced with a 6-step
-// xor butterfly across the wavefront.
+// HBM-bound: each 16-byte chunk (8 bf16) of a row belongs to one lane, and
+// each wavefront load instruction reads 1 KiB contiguous; the row stays in
+// registers between the reduction and the store, so x and residual are read
+// from HBM exactly once.
+//   - Widths that are a multiple of 1024: two wavefronts per row (a
+//     128-thread workgroup).  Wavefront q owns chunks (q * CPL + c) * 64 + lane,
+//     c = 0 .. CPL - 1 (CPL = width / 1024).  At the decider's [2048, 2048]
+//     call that is 4 wavefronts per SIMD instead of 2: the call went from
+//     8.7 to 7.8 us (6.8 to 5.6 us with the inputs in L2), config 3
+//     ([4, 2048, 2048]) from 23.5 to 22.4 us.
+//   - Other widths: one wavefront per row, lane l owns chunks l, l+64, l+128, ...
+//     (no LDS, no barrier).
 //
 // fp32 sequence (the CPU restatement reproduces it bit for bit):
 //   h_i    = bf16(f32(x_i) + f32(r_i))
 //   lane   : s = 0; for each owned chunk in order, for e = 0..7: s = s + h*h (two roundings)
 //   wave   : for off = 32,16,8,4,2,1: s = s + shfl_xor(s, off)
+//   row    : the wavefront's s, or with two wavefronts s(q = 0) + s(q = 1)
 //   inv    = 1 / sqrt(s / width + eps)       (correctly rounded sqrt and division)
 //   out_i  = bf16((h_i * inv) * g_i),  g_i = 1 + w_i  or  w_i
 #include "fd_common.h"
@@ -58,9 +65,10 @@ __device__ __forceinline__ void load_gain8<float>(const float* w, int chunk, int
 }
 
 // NCH = chunks of 8 features per lane (width <= 512 * NCH).  One row per
-// wavefront: at the decider's [2048, 2048] call, two or four rows per
-// wavefront (the loads of all rows first, the rows finished in turn) measured
-// 20 % and 54 % slower, for fewer wavefronts in flight.
+// wavefront, for widths that are not a multiple of 1024.  (At [2048, 2048],
+// which now runs two wavefronts per row, two or four rows per wavefront -- the
+// loads of all rows first, the rows finished in turn -- measured 20 % and 54 %
+// slower than one row per wavefront, for fewer wavefronts in flight.)
 template <int NCH, typename WT, bool HAS_RES>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void add_rmsnorm_kernel(
     const uint16_t* x, const uint16_t* res, const WT* __restrict__ w,
@@ -157,6 +165,90 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void add_rmsnorm_kernel(
   }
 }
 
+// Two wavefronts per row (width == 1024 * CPL), one row per 128-thread
+// workgroup; the order of the fp32 operations is the file header's.
+template <int CPL, typename WT, bool HAS_RES>
+__global__ __launch_bounds__(128) void add_rmsnorm_pair_kernel(
+    const uint16_t* x, const uint16_t* res, const WT* __restrict__ w,
+    uint16_t* out, uint16_t* res_out, int width, float eps, int gain_offset) {
+  __shared__ float part[2];
+  const int lane = threadIdx.x & 63;
+  const int q = threadIdx.x >> 6;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * width;
+  // every load before any store (residual_out may alias residual)
+  uint4 xv[CPL], rv[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int chunk = (q * CPL + c) * 64 + lane;
+    xv[c] = *reinterpret_cast<const uint4*>(x + base + chunk * 8);
+    rv[c] = make_uint4(0u, 0u, 0u, 0u);
+    if (HAS_RES) rv[c] = *reinterpret_cast<const uint4*>(res + base + chunk * 8);
+  }
+  uint32_t hw[CPL][4];
+  float h[CPL][8];
+  float s = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const uint32_t xw[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+    const uint32_t rw[4] = {rv[c].x, rv[c].y, rv[c].z, rv[c].w};
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      hw[c][p] = HAS_RES ? fd_pack2(fd_lo(xw[p]) + fd_lo(rw[p]), fd_hi(xw[p]) + fd_hi(rw[p])) : xw[p];
+      h[c][2 * p] = fd_lo(hw[c][p]);
+      h[c][2 * p + 1] = fd_hi(hw[c][p]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float sq = h[c][e] * h[c][e];
+      s = s + sq;
+    }
+  }
+  if (HAS_RES && res_out != nullptr) {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c)
+      *reinterpret_cast<uint4*>(res_out + base + ((q * CPL + c) * 64 + lane) * 8) =
+          make_uint4(hw[c][0], hw[c][1], hw[c][2], hw[c][3]);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_xor(s, off, 64);
+  if (lane == 0) part[q] = s;
+  __syncthreads();
+  const float mean = (part[0] + part[1]) / static_cast<float>(width);
+  const float inv = 1.0f / __builtin_sqrtf(mean + eps);
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int chunk = (q * CPL + c) * 64 + lane;
+    float g[8];
+    load_gain8<WT>(w, chunk, gain_offset, g);
+    uint32_t o[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      float a = (h[c][2 * p] * inv) * g[2 * p];
+      float b = (h[c][2 * p + 1] * inv) * g[2 * p + 1];
+      o[p] = fd_pack2(a, b);
+    }
+    *reinterpret_cast<uint4*>(out + base + chunk * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+template <int CPL, typename WT>
+int launch_pair(const void* x, const void* res, const void* w, void* out, void* res_out, int64_t rows,
+                int width, float eps, int gain_offset, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(rows)), block(128);
+  if (res != nullptr) {
+    hipLaunchKernelGGL((add_rmsnorm_pair_kernel<CPL, WT, true>), grid, block, 0, stream,
+                       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(res),
+                       static_cast<const WT*>(w), static_cast<uint16_t*>(out), static_cast<uint16_t*>(res_out),
+                       width, eps, gain_offset);
+  } else {
+    hipLaunchKernelGGL((add_rmsnorm_pair_kernel<CPL, WT, false>), grid, block, 0, stream,
+                       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(nullptr),
+                       static_cast<const WT*>(w), static_cast<uint16_t*>(out), static_cast<uint16_t*>(nullptr),
+                       width, eps, gain_offset);
+  }
+  return fd_check_launch("fd_add_rmsnorm_fwd");
+}
+
 template <int NCH, typename WT>
 int launch_nch(const void* x, const void* res, const void* w, void* out, void* res_out, int64_t rows,
                int width, float eps, int gain_offset, hipStream_t stream) {
@@ -179,6 +271,18 @@ int launch_nch(const void* x, const void* res, const void* w, void* out, void* r
 template <typename WT>
 int launch_wt(const void* x, const void* res, const void* w, void* out, void* res_out, int64_t rows,
               int width, float eps, int gain_offset, hipStream_t stream) {
+  if (width % 1024 == 0 && rows < 2147483647LL) {
+    switch (width / 1024) {
+      case 1: return launch_pair<1, WT>(x, res, w, out, res_out, rows, width, eps, gain_offset, stream);
+      case 2: return launch_pair<2, WT>(x, res, w, out, res_out, rows, width, eps, gain_offset, stream);
+      case 3: return launch_pair<3, WT>(x, res, w, out, res_out, rows, width, eps, gain_offset, stream);
+      case 4: return launch_pair<4, WT>(x, res, w, out, res_out, rows, width, eps, gain_offset, stream);
+      case 5: return launch_pair<5, WT>(x, res, w, out, res_out, rows, width, eps, gain_offset, stream);
+      case 6: return launch_pair<6, WT>(x, res, w, out, res_out, rows, width, eps, gain_offset, stream);
+      case 7: return launch_pair<7, WT>(x, res, w, out, res_out, rows, width, eps, gain_offset, stream);
+      default: return launch_pair<8, WT>(x, res, w, out, res_out, rows, width, eps, gain_offset, stream);
+    }
+  }
   const int nch = (width / 8 + 63) / 64;
   if (nch <= 1) return launch_nch<1, WT>(x, res, w, out, res_out, rows, width, eps, gain_offset, stream);
   if (nch <= 2) return launch_nch<2, WT>(x, res, w, out, res_out, rows, width, eps, gain_offset, stream);

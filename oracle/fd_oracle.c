@@ -17,7 +17,8 @@
  *     the (w + 1) gain; the residual is rounded to bf16 before it is normalised as in
  *     transformers' Qwen3_5DecoderLayer + Qwen3_5RMSNorm).
  * The summation order of the RMSNorm matches the GPU kernel's documented order
- * (per-lane chunk order, then a 6-step xor butterfly over 64 lanes), so GPU
+ * (per-lane chunk order, then a 6-step xor butterfly over 64 lanes; for widths
+ * that are a multiple of 1024 two wavefronts per row, whose sums are added), so GPU
  * output is compared bit for bit; the mathematics pins this restatement
  * independently (tests/test_oracle.py: fp64 closed forms, torch's F.conv1d and
  * eager RMSNorm, special cases).
@@ -146,25 +147,35 @@ int fd_oracle_add_rmsnorm(const uint16_t* x, const uint16_t* residual, const voi
         h[i] = bf16_to_f32(x[base + i]);
       }
     }
-    /* lane l owns chunks l, l+64, l+128, ... (8 features each) */
-    float lane_sum[64];
-    for (int l = 0; l < 64; ++l) {
-      float s = 0.0f;
-      for (int chunk = l; chunk < nchunks; chunk += 64) {
-        for (int e = 0; e < 8; ++e) {
-          const float hv = h[chunk * 8 + e];
-          const float sq = hv * hv;
-          s = s + sq;
+    /* one wavefront per row: lane l owns chunks l, l+64, l+128, ... (8 features each);
+     * width a multiple of 1024: two wavefronts, wavefront q's lane l owns chunks
+     * (q * cpl + c) * 64 + l for c = 0 .. cpl - 1, and the row sum is s(0) + s(1) */
+    const int waves = width % 1024 == 0 ? 2 : 1;
+    const int cpl = width / 1024;
+    float row_sum = 0.0f;
+    for (int q = 0; q < waves; ++q) {
+      float lane_sum[64];
+      for (int l = 0; l < 64; ++l) {
+        float s = 0.0f;
+        const int n_own = waves == 2 ? cpl : (nchunks - l + 63) / 64;
+        for (int c = 0; c < n_own; ++c) {
+          const int chunk = waves == 2 ? (q * cpl + c) * 64 + l : l + 64 * c;
+          for (int e = 0; e < 8; ++e) {
+            const float hv = h[chunk * 8 + e];
+            const float sq = hv * hv;
+            s = s + sq;
+          }
         }
+        lane_sum[l] = s;
       }
-      lane_sum[l] = s;
+      for (int off = 32; off >= 1; off >>= 1) {
+        float next[64];
+        for (int l = 0; l < 64; ++l) next[l] = lane_sum[l] + lane_sum[l ^ off];
+        memcpy(lane_sum, next, sizeof(next));
+      }
+      row_sum = q == 0 ? lane_sum[0] : row_sum + lane_sum[0];
     }
-    for (int off = 32; off >= 1; off >>= 1) {
-      float next[64];
-      for (int l = 0; l < 64; ++l) next[l] = lane_sum[l] + lane_sum[l ^ off];
-      memcpy(lane_sum, next, sizeof(next));
-    }
-    const float mean = lane_sum[0] / (float)width;
+    const float mean = row_sum / (float)width;
     const float inv = 1.0f / sqrtf(mean + eps);
     for (int i = 0; i < width; ++i) {
       float g = weight_dtype == 1 ? ((const float*)weight)[i] : bf16_to_f32(((const uint16_t*)weight)[i]);
