@@ -75,3 +75,17 @@ __device__ __forceinline__ float fd_silu_bf16(float y) {
   if (y < -16.0f || low + kSiluTieWindow - 0x8000u < 2u * kSiluTieWindow) f = fd_silu(y);
   return f;
 }
+
+// A value whose bf16 rounding equals that of g * fd_silu(z), for bf16 values g
+// and z (the gated RMSNorm's last product): g * (z * rcp(1 + exp2(-z log2 e)))
+// on the hardware exp2 and reciprocal, and g * fd_silu(z) itself where the two
+// could round differently (products within kSiluTieWindow fp32 ulps of a bf16
+// rounding tie, and z < -16).  fd_gated_silu_check counts the pairs where the
+// two bf16 roundings differ; a GPU test runs it over all 2^32 pairs of bf16
+// bit patterns.
+__device__ __forceinline__ float fd_gated_silu_bf16(float g, float z) {
+  float p = g * (z * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z * -1.44269504088896341f)));
+  const uint32_t low = __float_as_uint(p) & 0xffffu;
+  if (z < -16.0f || low + kSiluTieWindow - 0x8000u < 2u * kSiluTieWindow) p = g * fd_silu(z);
+  return p;
+}

@@ -7,6 +7,9 @@
 //   y2 = bf16(w * y)                                (bf16 weight times bf16 row)
 //   out = bf16(y2 * silu(z)),  silu(z) = z / (1 + exp(-z)) in fp32 on the bf16 gate
 // (with an fp32 weight the product w * y stays fp32, as the eager promotion does).
+// With a bf16 weight the last product runs on the hardware exp2 and reciprocal
+// (fd_gated_silu_bf16: the exact expression where the bf16 rounding could
+// differ; fd_gated_silu_check verifies every (y2, z) pair of bf16 values).
 // A 16-lane group owns one row of 128 (8 features per lane, 16-byte accesses);
 // rows of 64 or 256 use 8 or 32 lanes.
 //
@@ -39,8 +42,11 @@ __device__ __forceinline__ uint4 pack8(const float* x) {
   return make_uint4(fd_pack2(x[0], x[1]), fd_pack2(x[2], x[3]), fd_pack2(x[4], x[5]), fd_pack2(x[6], x[7]));
 }
 
-// LANES lanes per row (LANES * 8 == width)
-template <int LANES, bool W_F32>
+// LANES lanes per row (LANES * 8 == width); W_VEC: the weight is 16-byte aligned
+// and a lane loads its 8 weights as vectors.  The weights are loaded before the
+// per-element work: loaded inside it, each waited out its own memory round trip
+// between the exact-SiLU branches.
+template <int LANES, bool W_F32, bool W_VEC>
 __global__ __launch_bounds__(kThreads) void gated_rmsnorm_kernel(const uint16_t* __restrict__ x,
                                                                  const uint16_t* __restrict__ z, int64_t z_ts,
                                                                  int64_t z_hs, int heads,
@@ -57,6 +63,20 @@ __global__ __launch_bounds__(kThreads) void gated_rmsnorm_kernel(const uint16_t*
   const int tok = static_cast<int>(r) / heads;  // rows < 2^31 (checked by the host)
   const int hd = static_cast<int>(r) - tok * heads;
   unpack8(*reinterpret_cast<const uint4*>(z + tok * z_ts + hd * z_hs + ln * 8), zv);
+  float wv[8];
+  if constexpr (W_VEC && W_F32) {
+    const float4 w0 = *reinterpret_cast<const float4*>(static_cast<const float*>(w) + ln * 8);
+    const float4 w1 = *reinterpret_cast<const float4*>(static_cast<const float*>(w) + ln * 8 + 4);
+    wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
+    wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+  } else if constexpr (W_VEC) {
+    unpack8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(w) + ln * 8), wv);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      wv[e] = W_F32 ? static_cast<const float*>(w)[ln * 8 + e]
+                    : fd_bf16_to_f32(static_cast<const uint16_t*>(w)[ln * 8 + e]);
+  }
   float s = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) s = s + xv[e] * xv[e];
@@ -69,12 +89,16 @@ __global__ __launch_bounds__(kThreads) void gated_rmsnorm_kernel(const uint16_t*
     const float yn = bf16r(xv[e] * inv);
     float g;
     if constexpr (W_F32) {
-      g = static_cast<const float*>(w)[ln * 8 + e] * yn;
+      g = wv[e] * yn;
     } else {
-      g = bf16r(fd_bf16_to_f32(static_cast<const uint16_t*>(w)[ln * 8 + e]) * yn);
+      g = bf16r(wv[e] * yn);
     }
-    const float act = zv[e] / (1.0f + expf(-zv[e]));
-    y[e] = g * act;
+    if constexpr (W_F32) {
+      const float act = zv[e] / (1.0f + expf(-zv[e]));
+      y[e] = g * act;
+    } else {
+      y[e] = fd_gated_silu_bf16(g, zv[e]);  // g is a bf16 value
+    }
   }
   if (valid) *reinterpret_cast<uint4*>(out + r * kWidth + ln * 8) = pack8(y);
 }
@@ -103,7 +127,38 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __re
   *reinterpret_cast<uint4*>(out + r * width + c * 8) = pack8(y);
 }
 
+// bf16(fd_gated_silu_bf16(g, z)) against bf16(g * fd_silu(z)) for the pairs
+// (g, z) = (bf16 bits i >> 16, bf16 bits i & 0xffff), i in [begin, begin + count);
+// both NaN counts as equal.  One atomic per wavefront.
+__global__ __launch_bounds__(256) void gated_silu_check_kernel(uint32_t begin, uint32_t count,
+                                                               unsigned long long* mismatches) {
+  unsigned n = 0;
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < count; i += gridDim.x * 256u) {
+    const uint32_t bits = begin + i;
+    const float g = __uint_as_float(bits & 0xffff0000u);
+    const float z = __uint_as_float(bits << 16);
+    const uint32_t a = fd_pack2(fd_gated_silu_bf16(g, z), 0.0f) & 0xffffu;
+    const uint32_t b = fd_pack2(g * fd_silu(z), 0.0f) & 0xffffu;
+    const bool a_nan = (a & 0x7f80u) == 0x7f80u && (a & 0x7fu) != 0;
+    const bool b_nan = (b & 0x7f80u) == 0x7f80u && (b & 0x7fu) != 0;
+    if (a != b && !(a_nan && b_nan)) ++n;
+  }
+  for (int off = 32; off >= 1; off >>= 1) n += __shfl_xor(n, off, 64);
+  if ((threadIdx.x & 63) == 0 && n != 0) atomicAdd(mismatches, static_cast<unsigned long long>(n));
+}
+
 }  // namespace
+
+extern "C" FD_API int fd_gated_silu_check(uint32_t begin, uint32_t count, unsigned long long* mismatches,
+                                          void* stream) {
+  FD_REQUIRE(mismatches != nullptr, FD_ERR_INVALID_ARGUMENT, "fd_gated_silu_check: mismatches must be non-null");
+  FD_REQUIRE(static_cast<uint64_t>(begin) + count <= (1ULL << 32), FD_ERR_INVALID_ARGUMENT,
+             "fd_gated_silu_check: [begin, begin + count) must lie within the 2^32 (g, z) bf16 pairs");
+  if (count == 0) return FD_OK;
+  hipLaunchKernelGGL(gated_silu_check_kernel, dim3(8192), dim3(256), 0, static_cast<hipStream_t>(stream), begin,
+                     count, mismatches);
+  return fd_check_launch("fd_gated_silu_check");
+}
 
 extern "C" FD_API int fd_gated_rmsnorm_fwd(const void* x, const void* gate, int64_t gate_token_stride,
                                            int64_t gate_head_stride, int heads, const void* weight, int weight_dtype,
@@ -131,17 +186,21 @@ extern "C" FD_API int fd_gated_rmsnorm_fwd(const void* x, const void* gate, int6
   const uint16_t* zp = static_cast<const uint16_t*>(gate);
   uint16_t* op = static_cast<uint16_t*>(out);
   const dim3 grid(static_cast<unsigned>(blocks));
+  const bool wvec = fd_aligned16(weight);
+#define FD_GN2(L, F, V)                                                                                       \
+  hipLaunchKernelGGL((gated_rmsnorm_kernel<L, F, V>), grid, dim3(kThreads), 0, s, xp, zp, gate_token_stride,  \
+                     gate_head_stride, heads, weight, op, rows, eps)
 #define FD_GN(L)                                                                                              \
   do {                                                                                                        \
-    if (weight_dtype == FD_DTYPE_F32)                                                                         \
-      hipLaunchKernelGGL((gated_rmsnorm_kernel<L, true>), grid, dim3(kThreads), 0, s, xp, zp,                 \
-                         gate_token_stride, gate_head_stride, heads, weight, op, rows, eps);                  \
-    else                                                                                                      \
-      hipLaunchKernelGGL((gated_rmsnorm_kernel<L, false>), grid, dim3(kThreads), 0, s, xp, zp,                \
-                         gate_token_stride, gate_head_stride, heads, weight, op, rows, eps);                  \
+    if (weight_dtype == FD_DTYPE_F32) {                                                                       \
+      if (wvec) FD_GN2(L, true, true); else FD_GN2(L, true, false);                                           \
+    } else {                                                                                                  \
+      if (wvec) FD_GN2(L, false, true); else FD_GN2(L, false, false);                                         \
+    }                                                                                                         \
   } while (0)
   if (lanes == 8) FD_GN(8); else if (lanes == 16) FD_GN(16); else FD_GN(32);
 #undef FD_GN
+#undef FD_GN2
   return fd_check_launch("fd_gated_rmsnorm_fwd");
 }
 

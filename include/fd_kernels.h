@@ -36,6 +36,7 @@
  *                       (ref: src/decider/combined_gates.py:19-43, packed_conv.py:45-53)
  *   fd_packed_conv_gate_fwd  fd_packed_conv_strided_fwd and fd_gate_proj_fwd of one layer in one launch
  *   fd_silu_check       numerics self-check of the conv's SiLU (no reference counterpart)
+ *   fd_gated_silu_check numerics self-check of the gated RMSNorm's last product (no reference counterpart)
  *
  * Conventions shared by every entry point:
  *   - every tensor pointer is a device pointer; bf16 tensors are passed as raw
@@ -261,6 +262,18 @@ FD_API int fd_packed_conv_gate_fwd(const void* x, int64_t x_row_stride, const vo
  * and require 0.
  */
 FD_API int fd_silu_check(uint32_t begin, uint32_t count, unsigned long long* mismatches, void* stream);
+
+/*
+ * Numerics self-check of fd_gated_rmsnorm_fwd with a bf16 weight (no
+ * counterpart in the reference): its last product out = bf16(y2 * silu(z))
+ * takes y2 and z as bf16 values and runs on the hardware exp2 and reciprocal,
+ * with the exact y2 * (z / (1 + expf(-z))) where the bf16 roundings could
+ * differ.  Adds to *mismatches (device unsigned long long) the number of pairs
+ * (y2, z) = (bf16 bits i >> 16, bf16 bits i & 0xffff), i in [begin, begin + count),
+ * where the two bf16 roundings differ (both NaN counts as equal).
+ * begin + count <= 2^32.  The GPU test runs all 2^32 pairs and requires 0.
+ */
+FD_API int fd_gated_silu_check(uint32_t begin, uint32_t count, unsigned long long* mismatches, void* stream);
 
 /*
  * Fused residual add + RMSNorm over rows of `width` features.

@@ -27,7 +27,7 @@ def test_header_declares_the_expected_entry_points():
                                     "fd_packed_conv_strided_fwd", "fd_gated_delta_norm_fwd",
                                     "fd_gate_proj_fwd", "fd_packed_conv_gate_fwd",
                                     "fd_silu_mul_split_fwd", "fd_gated_delta_fwd_noalloc",
-                                    "fd_gqa_workspace_bytes", "fd_silu_check"}
+                                    "fd_gqa_workspace_bytes", "fd_silu_check", "fd_gated_silu_check"}
 
 
 def test_library_exports_every_declared_symbol_and_nothing_else():
@@ -100,6 +100,12 @@ def test_silu_check_argument_errors():
     assert lib.fd_silu_check(ctypes.c_uint32(0xFFFFFFF0), ctypes.c_uint32(0x20), f, None) == _lib.FD_ERR_INVALID_ARGUMENT
     assert "2^32" in _err(lib)
     assert lib.fd_silu_check(ctypes.c_uint32(5), ctypes.c_uint32(0), f, None) == _lib.FD_OK  # empty range
+    assert lib.fd_gated_silu_check(ctypes.c_uint32(0), ctypes.c_uint32(16), None, None) == \
+        _lib.FD_ERR_INVALID_ARGUMENT
+    assert lib.fd_gated_silu_check(ctypes.c_uint32(0xFFFFFFF0), ctypes.c_uint32(0x20), f, None) == \
+        _lib.FD_ERR_INVALID_ARGUMENT
+    assert "2^32" in _err(lib)
+    assert lib.fd_gated_silu_check(ctypes.c_uint32(5), ctypes.c_uint32(0), f, None) == _lib.FD_OK
 
 
 def test_gqa_argument_errors():

@@ -18,6 +18,26 @@ from helpers import announce, from_bits, to_bits, ulp_diff
 pytestmark = pytest.mark.gpu
 
 
+def test_gated_silu_fast_path_rounds_like_the_exact_product_for_every_bf16_pair():
+    """With a bf16 weight the gated norm's last product bf16(y2 * silu(z)) takes y2 and z as bf16
+    values and uses the hardware exp2 and reciprocal wherever they round to the same bf16 as
+    y2 * (z / (1 + expf(-z))), the eager expression, and that expression elsewhere.
+    fd_gated_silu_check compares the two bf16 roundings on the GPU; this runs it over all 2^32
+    (y2, z) pairs of bf16 bit patterns."""
+    import ctypes
+    from fastdecisions_amd import _lib
+    announce("gated SiLU product fast path over every bf16 pair")
+    lib = _lib.lib()
+    count = torch.zeros(1, dtype=torch.int64, device="cuda")
+    chunk = 1 << 30
+    for begin in range(0, 1 << 32, chunk):
+        _lib.check("fd_gated_silu_check", lib.fd_gated_silu_check(
+            ctypes.c_uint32(begin), ctypes.c_uint32(chunk), count.data_ptr(), _lib.stream_handle(count.device)))
+    torch.cuda.synchronize()
+    print(f"gated SiLU fast path: {int(count.item())} of 2^32 (y2, z) pairs round differently")
+    assert int(count.item()) == 0
+
+
 def test_gated_rmsnorm_golden(oracle, golden):
     from fastdecisions_amd.gated_norm_kernel import gated_rms_norm
     d = golden("fusions")
