@@ -16,6 +16,8 @@
 // fd_silu_mul_fwd replaces the MLP's ``act_fn(gate_proj(x)) * up_proj(x)``
 // (transformers Qwen3_5MLP) on a combined [rows, 2*width] gate|up projection:
 //   out = bf16(bf16(silu(gate)) * up)
+// with bf16(silu(gate)) from fd_silu_bf16 (the hardware exp2 and reciprocal,
+// the exact expression near bf16 ties; the same bf16 for every fp32 input).
 // HBM-bound, 16-byte loads and stores, one thread per 8 features.
 // fd_silu_mul_split_fwd does the same when the features come from two
 // gate|up projections (features [0, width1) from the first, the rest from the
@@ -120,7 +122,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __re
   unpack8(*reinterpret_cast<const uint4*>(src), g);
   unpack8(*reinterpret_cast<const uint4*>(src + up), u);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) s[e] = g[e] / (1.0f + expf(-g[e]));
+  for (int e = 0; e < 8; ++e) s[e] = fd_silu_bf16(g[e]);  // rounds to bf16 as g / (1 + expf(-g)) does
   unpack8(pack8(s), s);  // act_fn's bf16 output
 #pragma unroll
   for (int e = 0; e < 8; ++e) y[e] = s[e] * u[e];
