@@ -240,15 +240,15 @@ constexpr int kPrepB = kPrepG + kC * 4;                     // fp32 [64]  beta
 constexpr int kPrepBG = kPrepB + kC * 4;                    // fp32 [64]  beta e^gc
 constexpr int kPrepBytes = kPrepBG + kC * 4;
 
-// One workgroup per (chunk, value head).  u = T (beta v) and w = T (beta e^gc k)
-// are the solutions of (I + L) x = rhs; thread j < 128 solves for column j of
-// u, thread 128 + j for column j of w, by forward substitution with the rows of
-// L read from LDS (every lane reads the same address: broadcast).
-// position of A[i][j] in the output wavefronts' operand order
+// position of A[i][j] in the state pass's output-wavefront operand order
 __device__ __forceinline__ int aq_index(int i, int j) {
   return (((i >> 4) * 2 + (j >> 5)) * 64 + 16 * ((j & 31) >> 3) + (i & 15)) * 8 + (j & 7);
 }
 
+// One workgroup per (chunk, value head).  u = T (beta v) and w = T (beta e^gc k)
+// are the solutions of (I + L) x = rhs; thread j < 128 solves for column j of
+// u, thread 128 + j for column j of w, by forward substitution with the rows of
+// L read from LDS (every lane reads the same address: broadcast).
 __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
   const int h = blockIdx.x % a.hv;
   const int c = blockIdx.x / a.hv;
