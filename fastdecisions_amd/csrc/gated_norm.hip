@@ -135,8 +135,9 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __re
 __global__ __launch_bounds__(256) void gated_silu_check_kernel(uint32_t begin, uint32_t count,
                                                                unsigned long long* mismatches) {
   unsigned n = 0;
-  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < count; i += gridDim.x * 256u) {
-    const uint32_t bits = begin + i;
+  // 64-bit index: a 32-bit one would wrap past 2^32 - stride and never reach count
+  for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < count; i += gridDim.x * 256ull) {
+    const uint32_t bits = begin + static_cast<uint32_t>(i);
     const float g = __uint_as_float(bits & 0xffff0000u);
     const float z = __uint_as_float(bits << 16);
     const uint32_t a = fd_pack2(fd_gated_silu_bf16(g, z), 0.0f) & 0xffffu;

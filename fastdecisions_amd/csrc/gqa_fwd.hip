@@ -20,12 +20,13 @@
 //   are computed, one MFMA of that dependent chain after each of eight pieces
 //   of the softmax, so the VALU work issues while the MFMAs run; tiles t+2 and
 //   t+3 are in flight.
-// * One wavefront per head (head_dim 256 always, 64 and 128 for padded
-//   batches with more than two work items per CU): 4 wavefronts per
-//   workgroup, each walking 32-key blocks; the P·V of block j-1 and the scores
-//   of block j+1 are issued with the softmax of block j between their MFMAs,
-//   over 2-stage K and V rings.  At head_dim <= 128 two such workgroups share
-//   a CU, so one wavefront's softmax runs under the other's MFMAs.
+// * head_dim 256: one wavefront per head (4 per workgroup), each walking
+//   32-key blocks; the P·V of block j-1 and the scores of block j+1 are
+//   issued with the softmax of block j between their MFMAs, over 2-stage K
+//   and V rings.
+// * Which loop runs depends on head_dim alone, so for head_dim <= 128 a
+//   request's output rows are bit-identical whether it runs alone, packed
+//   with others (cu_seqlens) or in a padded batch of any size.
 //   16-byte chunks are XOR-swizzled per row so that the MFMA operand reads
 //   below are bank-conflict free.
 // * The score tile is computed transposed, S^T = K · Q^T, with
@@ -48,7 +49,6 @@
 //   contiguous range of (head group, query tile) items, keeping a KV head's
 //   tiles in one L2.
 #include <algorithm>
-#include <cstdlib>
 #include <type_traits>
 
 #include "fd_common.h"
@@ -99,7 +99,7 @@ struct GqaArgs {
   int64_t qs[4], ks[4], vs[4], os[4];
   const uint16_t* gate;  // output gate (fd_gqa_gated_fwd) or null
   int64_t gs[4];
-  float* part;    // [n_groups][n_split][2][4 slots][64 lanes][D/2 + 2]
+  float* part;    // [n_groups][n_split][2][4 slots][64 lanes][D/2 + 4]: o, max, denominator, 2 pad
   // units of a group, longest first: 4 * query tile + (part + 1), part -1 = whole tile
   uint16_t units[kMaxUnits];
 };
@@ -120,12 +120,8 @@ struct Cfg {
   // query block)) has 2 stages, used as separate K and V rings.
   static constexpr bool kPipe = KSPLIT > 1 && 4 * kStageBytes <= 160 * 1024;
   static constexpr int kStages = kPipe ? 4 : 2;
-  // merge of the key parts: a whole O per lane slot (split tiles) or half an O
-  // from each key part (whole tiles)
-  static constexpr int kCombineWhole = 4 * 64 * (D / 2 + 2) * 4;
-  static constexpr int kCombineHalves = 8 * 64 * (D / 4 + 2) * 4;
-  static constexpr int kCombineBytes =
-      KSPLIT > 1 ? (kCombineWhole > kCombineHalves ? kCombineWhole : kCombineHalves) : 0;
+  // merge of the key parts: half an O, the running max and the denominator from each
+  static constexpr int kCombineBytes = KSPLIT > 1 ? 8 * 64 * (D / 4 + 2) * 4 : 0;
   static constexpr int kSmemBytes =
       (kStages * kStageBytes > kCombineBytes) ? kStages * kStageBytes : kCombineBytes;
   // s_waitcnt immediate: vmcnt(N) with expcnt / lgkmcnt left alone (gfx9 encoding)
@@ -171,11 +167,17 @@ __device__ __forceinline__ float half_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Floats per lane record of a split tile's half in the workspace: O^T (D/2),
+// running max, denominator and two pad floats, so every record (and each of
+// its 16-byte vector accesses) is 16-byte aligned.
+template <int D>
+constexpr int kPartFloats = D / 2 + 4;
+
 // Workspace slot of one (head, query block) slot x lane of a split tile's half.
 template <int D>
 __device__ __forceinline__ float* part_slot(const GqaArgs& a, int group, int qtile, int part, int w4, int lane) {
   const size_t tile = static_cast<size_t>(group) * a.n_split + (a.n_qtiles - 1 - qtile);
-  return a.part + ((tile * 2 + part) * 4 * 64 + w4 * 64 + lane) * (D / 2 + 2);
+  return a.part + ((tile * 2 + part) * 4 * 64 + w4 * 64 + lane) * kPartFloats<D>;
 }
 
 // Normalised store of a lane's query row (the O^T accumulator: dims
@@ -219,7 +221,7 @@ __device__ __forceinline__ void store_rows(const GqaArgs& a, const f32x16_t (&o)
 }
 
 template <int D, int KSPLIT>
-__global__ __launch_bounds__(256 * KSPLIT, (KSPLIT == 1 && D <= 128) ? 2 : 1) void gqa_fwd_kernel(GqaArgs a) {
+__global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
   using C = Cfg<D, KSPLIT>;
   constexpr int CR = C::kChunksRow;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[C::kSmemBytes];
@@ -848,74 +850,49 @@ __global__ __launch_bounds__(256 * KSPLIT, (KSPLIT == 1 && D <= 128) ? 2 : 1) vo
   uint16_t* const orow = obase + qpos * a.os[2];
   const uint16_t* const grow = a.gate ? a.gate + bidx * a.gs[0] + qhead * a.gs[1] + qpos * a.gs[2] : nullptr;
   if constexpr (KSPLIT > 1) {
-    if (part < 0) {
-      // Each key part hands the other the half of O it does not store and
-      // finishes the half it does (kh 0: blocks 0 .. D/64-1, kh 1: the rest),
-      // so both wavefronts of a SIMD run the normalisation, gate and store.
-      // Every element is the same sum of the same two products as a one-sided
-      // merge gives.
-      constexpr int kHalf = D / 64;          // O blocks per half
-      constexpr int kStride = kHalf * 16 + 2;  // floats per lane: the half, max, denominator
-      float* const mine = reinterpret_cast<float*>(smem) + ((kh * 4 + w4) * 64 + lane) * kStride;
-      const float* const theirs = reinterpret_cast<const float*>(smem) + (((kh ^ 1) * 4 + w4) * 64 + lane) * kStride;
-      // KEEP: the first O block this key part stores (compile-time, so that o
-      // stays in registers)
-      auto hand_over = [&](auto keep_c) {
-        constexpr int GIVE = kHalf - decltype(keep_c)::value;
+    // (head_dim <= 128 never splits a tile over workgroups, so every item is a
+    // whole tile.)  Each key part hands the other the half of O it does not store and
+    // finishes the half it does (kh 0: blocks 0 .. D/64-1, kh 1: the rest),
+    // so both wavefronts of a SIMD run the normalisation, gate and store.
+    // Every element is the same sum of the same two products as a one-sided
+    // merge gives.
+    constexpr int kHalf = D / 64;          // O blocks per half
+    constexpr int kStride = kHalf * 16 + 2;  // floats per lane: the half, max, denominator
+    float* const mine = reinterpret_cast<float*>(smem) + ((kh * 4 + w4) * 64 + lane) * kStride;
+    const float* const theirs = reinterpret_cast<const float*>(smem) + (((kh ^ 1) * 4 + w4) * 64 + lane) * kStride;
+    // KEEP: the first O block this key part stores (compile-time, so that o
+    // stays in registers)
+    auto hand_over = [&](auto keep_c) {
+      constexpr int GIVE = kHalf - decltype(keep_c)::value;
 #pragma unroll
-        for (int b = 0; b < kHalf; ++b)
+      for (int b = 0; b < kHalf; ++b)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mine[b * 16 + r] = o[GIVE + b][r];
-        mine[kHalf * 16] = m_run;
-        mine[kHalf * 16 + 1] = l_run;
-      };
-      auto finish = [&](auto keep_c) {
-        constexpr int KEEP = decltype(keep_c)::value;
-        const float m1 = theirs[kHalf * 16];
-        const float l1 = theirs[kHalf * 16 + 1];
-        const float m = fmaxf(m_run, m1);
-        const float a0 = (m_run == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
-        const float a1 = (m1 == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m1 - m);
-        const float l_tot = half_sum(l_run * a0 + l1 * a1);
+        for (int r = 0; r < 16; ++r) mine[b * 16 + r] = o[GIVE + b][r];
+      mine[kHalf * 16] = m_run;
+      mine[kHalf * 16 + 1] = l_run;
+    };
+    auto finish = [&](auto keep_c) {
+      constexpr int KEEP = decltype(keep_c)::value;
+      const float m1 = theirs[kHalf * 16];
+      const float l1 = theirs[kHalf * 16 + 1];
+      const float m = fmaxf(m_run, m1);
+      const float a0 = (m_run == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
+      const float a1 = (m1 == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m1 - m);
+      const float l_tot = half_sum(l_run * a0 + l1 * a1);
 #pragma unroll
-        for (int b = 0; b < kHalf; ++b)
+      for (int b = 0; b < kHalf; ++b)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) o[KEEP + b][r] = o[KEEP + b][r] * a0 + theirs[b * 16 + r] * a1;
-        store_rows<D, KEEP, KEEP + kHalf>(a, o, 1.0f / l_tot, qvalid, orow, grow, half);
-      };
-      using Lo = std::integral_constant<int, 0>;
-      using Hi = std::integral_constant<int, kHalf>;
-      if (kh == 0) hand_over(Lo{});
-      else hand_over(Hi{});
-      __syncthreads();
-      if (kh == 0) finish(Lo{});
-      else finish(Hi{});
-      return;
-    }
-    // a half of a split tile: the key parts merge into key part 0, which
-    // writes the whole unnormalised state to the workspace
-    float* cmb = reinterpret_cast<float*>(smem) + (w4 * 64 + lane) * (D / 2 + 2);
-    if (kh == 1) {
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) cmb[db * 16 + r] = o[db][r];
-      cmb[D / 2] = m_run;
-      cmb[D / 2 + 1] = l_run;
-    }
+        for (int r = 0; r < 16; ++r) o[KEEP + b][r] = o[KEEP + b][r] * a0 + theirs[b * 16 + r] * a1;
+      store_rows<D, KEEP, KEEP + kHalf>(a, o, 1.0f / l_tot, qvalid, orow, grow, half);
+    };
+    using Lo = std::integral_constant<int, 0>;
+    using Hi = std::integral_constant<int, kHalf>;
+    if (kh == 0) hand_over(Lo{});
+    else hand_over(Hi{});
     __syncthreads();
-    if (kh == 1) return;
-    const float m1 = cmb[D / 2];
-    const float l1 = cmb[D / 2 + 1];
-    const float m = fmaxf(m_run, m1);
-    const float a0 = (m_run == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
-    const float a1 = (m1 == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m1 - m);
-    l_run = l_run * a0 + l1 * a1;
-    m_run = m;  // o and l_run are now relative to m
-#pragma unroll
-    for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * a0 + cmb[db * 16 + r] * a1;
+    if (kh == 0) finish(Lo{});
+    else finish(Hi{});
+    return;
   }
   if (part >= 0) {
     // a half of a split tile: the unnormalised state goes to the workspace
@@ -988,33 +965,21 @@ bool stride_ok(const int64_t s[4]) {
   return true;
 }
 
-// Work items below which a padded batch splits its long query tiles: fewer
-// than the 256 CUs of the MI355X, so CUs would idle (e.g. B=1, T=2048, 8/2
-// heads of 256).  At one item per CU (B=1, T=2048, 16/4 heads of 128) the
-// split measured no faster: every item carries about 5 us of fixed cost
-// (argument loads, the first tiles' latency, merge and store) against about
-// 1 us per 64-key tile, so the extra items cost what the balance saves.
-// head_dim 64 and 128 have two loops: two wavefronts per (head, query block),
-// each on half the keys of every tile (one workgroup per CU), or one
-// wavefront per head walking 32-key blocks in a 64 KiB workgroup of which two
-// fit per CU.  The second needs both workgroup slots of a CU filled to
-// overlap one wavefront's softmax with the other's MFMAs, so it runs when a
-// padded batch of several sequences has more than two work items per CU.
-// Single sequences and packed requests always take the first loop, so a
-// request's rows are the same alone and packed.  FD_GQA_ONE_WAVE=0 / 1 forces
-// the choice (tests run both loops on every shape).
-constexpr int64_t kOneWaveAbove = 2 * 256;
-bool one_wave_loop(int64_t items, int batch, bool varlen) {
-  const char* force = std::getenv("FD_GQA_ONE_WAVE");
-  if (force != nullptr && (force[0] == '0' || force[0] == '1')) return force[0] == '1';
-  return !varlen && batch > 1 && items > kOneWaveAbove;
-}
-
+// Key split (head_dim 256 only): a padded batch with fewer work items than
+// the 256 CUs of the MI355X (e.g. B=1, T=2048, 8/2 heads of 256: 128 items)
+// runs the longest half of its query tiles as two items over the two halves
+// of their key tiles, merged by gqa_combine_kernel.  The merge rounds
+// differently from the whole-tile loop, so a head_dim-256 row depends on
+// whether the split ran (the caller turns it off by passing no workspace).
+// head_dim 64 and 128 never split: at one item per CU (B=1, T=2048, 16/4
+// heads of 128) the split measured no faster, and without it every launch of
+// these head dims runs the same loop, whatever the batch.
 constexpr int64_t kSplitBelow = 256;
 
 // Query tiles of every (sequence, head group) that the key split halves, or 0.
-int split_tiles(int n_qtiles, int64_t items, bool varlen) {
-  if (varlen || items >= kSplitBelow || n_qtiles < 4 || n_qtiles + n_qtiles / 2 > kMaxUnits) return 0;
+int split_tiles(int n_qtiles, int64_t items, bool varlen, int head_dim) {
+  if (head_dim != 256 || varlen || items >= kSplitBelow || n_qtiles < 4 || n_qtiles + n_qtiles / 2 > kMaxUnits)
+    return 0;
   return n_qtiles / 2;
 }
 
@@ -1044,7 +1009,7 @@ void fill_units(GqaArgs& a, int qspan) {
 }
 
 int64_t split_bytes(int64_t n_groups, int n_split, int head_dim) {
-  return n_groups * n_split * 2 * 4 * 64 * static_cast<int64_t>(head_dim / 2 + 2) * 4;
+  return n_groups * n_split * 2 * 4 * 64 * static_cast<int64_t>(head_dim / 2 + 4) * 4;
 }
 
 // Sizes shared by the launcher and fd_gqa_workspace_bytes.
@@ -1128,7 +1093,7 @@ int gqa_launch(const void* q, const void* k, const void* v, void* out, const int
   a.n_hgroups = g.n_hgroups;
   FD_REQUIRE(g.items < 2147483647LL / 2, FD_ERR_INVALID_ARGUMENT, "fd_gqa_fwd: problem too large");
   a.n_groups = g.n_hgroups * g.n_slots;
-  a.n_split = split_tiles(g.n_qtiles, g.items, cu_seqlens != nullptr);
+  a.n_split = split_tiles(g.n_qtiles, g.items, cu_seqlens != nullptr, head_dim);
   a.part = static_cast<float*>(workspace);
   if (a.n_split > 0 && (workspace == nullptr || !fd_aligned16(workspace) ||
                         workspace_bytes < split_bytes(a.n_groups, a.n_split, head_dim)))
@@ -1142,15 +1107,12 @@ int gqa_launch(const void* q, const void* k, const void* v, void* out, const int
   const int nblocks = static_cast<int>((items + kNumXcd - 1) / kNumXcd * kNumXcd);
   hipStream_t s = static_cast<hipStream_t>(stream);
   dim3 grid(nblocks);
-  const bool one_wave = a.n_split == 0 && one_wave_loop(items, batch, cu_seqlens != nullptr);
   switch (head_dim) {
     case 64:
-      if (one_wave) hipLaunchKernelGGL((gqa_fwd_kernel<64, 1>), grid, dim3(Cfg<64, 1>::kThreads), 0, s, a);
-      else hipLaunchKernelGGL((gqa_fwd_kernel<64, 2>), grid, dim3(Cfg<64, 2>::kThreads), 0, s, a);
+      hipLaunchKernelGGL((gqa_fwd_kernel<64, 2>), grid, dim3(Cfg<64, 2>::kThreads), 0, s, a);
       break;
     case 128:
-      if (one_wave) hipLaunchKernelGGL((gqa_fwd_kernel<128, 1>), grid, dim3(Cfg<128, 1>::kThreads), 0, s, a);
-      else hipLaunchKernelGGL((gqa_fwd_kernel<128, 2>), grid, dim3(Cfg<128, 2>::kThreads), 0, s, a);
+      hipLaunchKernelGGL((gqa_fwd_kernel<128, 2>), grid, dim3(Cfg<128, 2>::kThreads), 0, s, a);
       break;
     default:
       hipLaunchKernelGGL((gqa_fwd_kernel<256, 1>), grid, dim3(Cfg<256, 1>::kThreads), 0, s, a);
@@ -1158,11 +1120,7 @@ int gqa_launch(const void* q, const void* k, const void* v, void* out, const int
   }
   if (a.n_split > 0) {
     const dim3 cgrid(static_cast<unsigned>(a.n_groups * a.n_split * 4));
-    switch (head_dim) {
-      case 64: hipLaunchKernelGGL(gqa_combine_kernel<64>, cgrid, dim3(64), 0, s, a); break;
-      case 128: hipLaunchKernelGGL(gqa_combine_kernel<128>, cgrid, dim3(64), 0, s, a); break;
-      default: hipLaunchKernelGGL(gqa_combine_kernel<256>, cgrid, dim3(64), 0, s, a); break;
-    }
+    hipLaunchKernelGGL(gqa_combine_kernel<256>, cgrid, dim3(64), 0, s, a);
   }
   return fd_check_launch("fd_gqa_fwd");
 }
@@ -1201,6 +1159,6 @@ extern "C" int64_t fd_gqa_workspace_bytes(int batch, int q_heads, int kv_heads, 
   const bool varlen = n_seqs > 0;
   if (varlen && (batch != 1 || max_seqlen < 0 || max_seqlen > seq_len)) return FD_ERR_INVALID_ARGUMENT;
   const GqaShape g = gqa_shape(batch, q_heads, kv_heads, seq_len, n_seqs, max_seqlen, varlen);
-  const int n_split = split_tiles(g.n_qtiles, g.items, varlen);
+  const int n_split = split_tiles(g.n_qtiles, g.items, varlen, head_dim);
   return n_split > 0 ? split_bytes(static_cast<int64_t>(g.n_hgroups) * g.n_slots, n_split, head_dim) : 0;
 }

@@ -397,8 +397,9 @@ namespace {
 __global__ __launch_bounds__(256) void silu_check_kernel(uint32_t begin, uint32_t count,
                                                          unsigned long long* mismatches) {
   unsigned n = 0;
-  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < count; i += gridDim.x * 256u) {
-    const float y = __uint_as_float(begin + i);
+  // 64-bit index: a 32-bit one would wrap past 2^32 - stride and never reach count
+  for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < count; i += gridDim.x * 256ull) {
+    const float y = __uint_as_float(begin + static_cast<uint32_t>(i));
     const uint32_t a = fd_pack2(fd_silu_bf16(y), 0.0f) & 0xffffu;
     const uint32_t b = fd_pack2(fd_silu(y), 0.0f) & 0xffffu;
     const bool a_nan = (a & 0x7f80u) == 0x7f80u && (a & 0x7fu) != 0;

@@ -169,20 +169,48 @@ def build_decider(shape: DeciderShape = DECIDER_2B_SHAPED, seed: int = 0, device
     return model.eval()
 
 
-def install_hip_kernels(model: DeciderModel) -> dict:
-    """Route the hot ops of every layer to the HIP kernels; returns per-op patch counts."""
+# Install levels, each adding to the one before:
+#   north_star           the reference's three patches: packed conv (Gated-DeltaNet layers, delta rule
+#                        still transformers' torch form), native GQA (attention layers), residual add +
+#                        RMSNorm (linear-attention decoder layers)
+#   residual_chain       add+RMSNorm in every decoder layer, each MLP residual add inside the next norm
+#   gated_delta          the chunked gated-delta rule on the HIP kernels
+#   combined_gates       a|b gate projections as one GEMM + the gate transform kernel
+#   gated_norm           the delta rule's gated RMSNorm in the delta-rule launch sequence
+#   attention_fusions    q/k RMSNorm + RoPE prologue, gated GQA store, q|gate|k|v as one GEMM
+#   combined_projections q|k|v|z as one GEMM, conv + a|b projection + gate transform in one launch
+#   mlp_fusion           gate|up as two GEMMs + one SiLU*mul kernel
+INSTALL_LEVELS = ("north_star", "residual_chain", "gated_delta", "combined_gates", "gated_norm",
+                  "attention_fusions", "combined_projections", "mlp_fusion")
+
+
+def install_hip_kernels(model: DeciderModel, level: str = INSTALL_LEVELS[-1]) -> dict:
+    """Route the hot ops of every layer to the HIP kernels, up to and including ``level``
+    (one of ``INSTALL_LEVELS``; the default installs everything); returns per-step patch counts.
+    Installing a later level onto a model installed at an earlier one adds the missing steps."""
     from .combined_gates import install_combined_gates, install_combined_projections
     from .gated_delta import install_gated_delta_rule
     from .layer_fusions import install_gated_norm, install_mlp_fusion
     from .native_gqa import install_attention_fusions, install_native_gqa
     from .packed_conv import install_packed_conv
     from .persistent_residual_rms import install_persistent_residual_rms
-    return dict(packed_conv=install_packed_conv(model.core), native_gqa=install_native_gqa(model.core),
-                residual_rms=install_persistent_residual_rms(model.core, all_layers=True),
-                gated_delta=install_gated_delta_rule(model.core), combined_gates=install_combined_gates(model.core),
-                combined_projections=install_combined_projections(model.core),
-                attention_fusions=install_attention_fusions(model.core), gated_norm=install_gated_norm(model.core),
-                mlp_fusion=install_mlp_fusion(model.core))
+    if level not in INSTALL_LEVELS:
+        raise ValueError(f"level must be one of {INSTALL_LEVELS} (got {level!r})")
+    core = model.core
+    steps = dict(
+        north_star=lambda: dict(packed_conv=install_packed_conv(core), native_gqa=install_native_gqa(core),
+                                residual_rms=install_persistent_residual_rms(core)),
+        residual_chain=lambda: dict(residual_rms_all_layers=install_persistent_residual_rms(core, all_layers=True)),
+        gated_delta=lambda: dict(gated_delta=install_gated_delta_rule(core)),
+        combined_gates=lambda: dict(combined_gates=install_combined_gates(core)),
+        gated_norm=lambda: dict(gated_norm=install_gated_norm(core)),
+        attention_fusions=lambda: dict(attention_fusions=install_attention_fusions(core)),
+        combined_projections=lambda: dict(combined_projections=install_combined_projections(core)),
+        mlp_fusion=lambda: dict(mlp_fusion=install_mlp_fusion(core)))
+    counts = {}
+    for name in INSTALL_LEVELS[:INSTALL_LEVELS.index(level) + 1]:
+        counts.update(steps[name]())
+    return counts
 
 
 def synthetic_ids(batch: int, seq_len: int, vocab: int, seed: int, device="cuda") -> torch.Tensor:

@@ -11,9 +11,11 @@ here they are part of the package:
 * ``native_gqa_varlen`` — the same over packed requests (``cu_seqlens``);
 * ``install_native_gqa(core)`` — binds ``candidate_forward`` on every
   ``Qwen3_5Attention`` of a model and returns the count.  Unsupported calls
-  (KV cache, training, grad, non-CUDA, non-bf16) fall back to the original
-  forward, as the other install patches of the reference do
-  (ref: src/decider/packed_conv.py:27-38);
+  (KV cache, training, grad, non-CUDA, non-bf16, an ``attention_mask`` that is
+  not plain causal) fall back to the original forward, as the other install
+  patches of the reference do (ref: src/decider/packed_conv.py:27-38); the
+  reference checks the masks once, in eager execution, before it swaps the
+  kernel in (ref: experiments/native_gqa/bench_native_gqa_model.py:84-107);
 * ``attn_prologue`` / ``native_gqa_gated`` — the attention layer's prologue
   (q/k RMSNorm + partial RoPE, one kernel) and the attention with its sigmoid
   output gate applied in the store; ``install_attention_fusions(core)``
@@ -114,15 +116,37 @@ def _fused_forward(self, hidden_states, position_embeddings, cu_seqlens, max_seq
     return self.o_proj(out.transpose(1, 2).reshape(*shape, -1)), None
 
 
+def plain_causal(mask, t: int) -> bool:
+    """True when ``mask`` adds nothing to the in-kernel causal mask over ``t`` tokens: None, a boolean
+    mask equal to the lower triangle, or an additive mask that is 0 on and below the diagonal and
+    below -1e4 above it (the checks of ref: experiments/native_gqa/bench_native_gqa_model.py:84-99).
+    A tensor mask is read back to the host, so during graph capture (where that is not allowed)
+    it counts as not plain and the caller falls back to the original forward."""
+    if mask is None:
+        return True
+    if not isinstance(mask, torch.Tensor) or mask.ndim < 2 or tuple(mask.shape[-2:]) != (t, t):
+        return False
+    if mask.is_cuda and torch.cuda.is_current_stream_capturing():
+        return False
+    allowed = torch.ones((t, t), device=mask.device, dtype=torch.bool).tril()
+    if mask.dtype == torch.bool:
+        return bool(torch.equal(mask, allowed.expand_as(mask)))
+    if not mask.is_floating_point():
+        return False
+    return bool((mask[..., allowed] == 0).all().item()) and bool((mask[..., ~allowed] < -1e4).all().item())
+
+
 def candidate_forward(self, hidden_states, position_embeddings, attention_mask=None, past_key_values=None,
                       **kwargs):
     """Qwen3_5Attention.forward with the attention itself on the HIP kernel
     (ref: experiments/native_gqa/bench_native_gqa_model.py:43-56).  The causal
-    mask is applied in-kernel; ``attention_mask`` must describe plain causal
-    attention over right-padded rows (the engine's contract, ref: src/decider/engine.py:3-5)."""
+    mask is applied in-kernel, so the kernel runs only when ``attention_mask`` adds
+    nothing to it (``plain_causal``); any other mask (padding, segments, a bias)
+    runs the original forward, which applies it."""
     if (past_key_values is not None or self.training or torch.is_grad_enabled()
             or not hidden_states.is_cuda or hidden_states.dtype != torch.bfloat16
-            or self.head_dim not in (64, 128, 256)):
+            or self.head_dim not in (64, 128, 256)
+            or not plain_causal(attention_mask, hidden_states.shape[1])):
         return self._native_gqa_original_forward(hidden_states, position_embeddings, attention_mask,
                                                  past_key_values=past_key_values, **kwargs)
     cu_seqlens = kwargs.get("cu_seq_lens_q")

@@ -16,6 +16,12 @@ masking inside each request, and an
 optional output ``gate`` (logical ``[B, Hq, T, D]`` like the output): the
 attention layer's ``output * sigmoid(gate)`` applied in the kernel's store
 (``fd_gqa_gated_fwd``; ref: experiments/native_gqa/bench_native_gqa_model.py:54-55).
+
+``key_split`` (default on) lets a head_dim-256 call with fewer work items than
+the GPU has CUs (e.g. B=1, T=2048, 8/2 heads) run its longest query tiles as two
+halves of their key range, merged by a second launch.  Off, every tile runs
+whole; a request's rows are then bit-identical alone, packed or in a padded
+batch, which head_dim 64 and 128 always are (they never split).
 """
 from __future__ import annotations
 
@@ -24,20 +30,6 @@ import torch
 from . import _lib
 
 SUPPORTED_HEAD_DIMS = (64, 128, 256)
-
-_KEY_SPLIT = True
-
-
-def set_key_split(enabled: bool) -> bool:
-    """Turn the key split of long query tiles on (the default) or off; returns the previous setting.
-
-    With it, a padded batch with few work items (e.g. B=1, T=2048) runs the longest
-    query tiles as two halves of their key range, merged by a second launch
-    (fd_gqa_workspace_bytes).  Off, every tile runs whole, as packed varlen batches
-    always do: a request then gives bit-identical rows alone and packed."""
-    global _KEY_SPLIT
-    previous, _KEY_SPLIT = _KEY_SPLIT, bool(enabled)
-    return previous
 
 
 def native_gqa_attention(
@@ -49,6 +41,7 @@ def native_gqa_attention(
     cu_seqlens: torch.Tensor | None = None,
     max_seqlen: int | None = None,
     gate: torch.Tensor | None = None,
+    key_split: bool = True,
 ) -> torch.Tensor:
     # Logical shapes: Q [B, Hq, T, D], K/V [B, Hkv, T, D] (ref: :120).
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
@@ -108,9 +101,10 @@ def native_gqa_attention(
             (batch, seq_len, q_heads, head_dim), device=q.device, dtype=q.dtype
         ).permute(0, 2, 1, 3)
         lib = _lib.lib()
-        # workspace of the key split of long query tiles (0 bytes: the kernel runs unsplit)
+        # workspace of the key split of long query tiles (head_dim 256 with few work items;
+        # 0 bytes: the kernel runs unsplit)
         nbytes = 0
-        if _KEY_SPLIT:
+        if key_split:
             nbytes = lib.fd_gqa_workspace_bytes(batch, q_heads, kv_heads, seq_len, head_dim, n_seqs,
                                                 int(max_seqlen))
             if nbytes < 0:

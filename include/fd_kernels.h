@@ -103,17 +103,18 @@ FD_API const char* fd_last_error(void);
  * [0, seq_len] on the device.
  *
  * workspace / workspace_bytes: optional device memory (16-byte aligned) for
- * the key split of long query tiles, see fd_gqa_workspace_bytes; NULL / 0 runs
- * unsplit.  With a split the call enqueues two launches on `stream`.
+ * the key split of long query tiles at head_dim 256, see
+ * fd_gqa_workspace_bytes; NULL / 0 runs unsplit.  With a split the call
+ * enqueues two launches on `stream`.
  *
- * Two loops serve head_dim 64 and 128: two wavefronts per (head, 32 queries)
- * on the two key halves of every tile, or one wavefront per (head, 32
- * queries) on all keys.  The second runs for padded batches (cu_seqlens NULL)
- * of two or more sequences with more than 512 work items (4 query heads x 32
- * queries each); single sequences and packed requests always run the first,
- * so a request's rows are the same alone and packed.  The two loops round
- * differently (at most about one bf16 step apart).  The environment variable
- * FD_GQA_ONE_WAVE=0 or 1, read at each call, forces the first or the second.
+ * Batch invariance: for head_dim 64 and 128 every call runs the same loop
+ * (two wavefronts per (head, 32 queries), one on each 32-key half of every
+ * 64-key tile, merged at the end), whatever the batch, the packing or the
+ * workspace, so a request's output rows are bit-identical alone, packed with
+ * others through cu_seqlens, or in a padded batch.  For head_dim 256 that
+ * holds when no key split runs (workspace NULL or 0 bytes, or more work items
+ * than fd_gqa_workspace_bytes splits); a split rounds the split tiles
+ * differently, by at most about one bf16 step.
  *
  * Limits: head_dim in {64, 128, 256}; q_heads % kv_heads == 0; every base
  * pointer and every non-unit stride keeps 16-byte alignment.
@@ -131,13 +132,15 @@ FD_API int fd_gqa_fwd(const void* q, const void* k, const void* v, void* out,
  * batch), 0 when they run unsplit, or a negative FD_ERR_* code.
  *
  * Causal attention gives the query tiles near the end of a sequence up to
- * twice the average work; when a padded batch has few work items (B=1,
- * T=2048: one per CU), those tiles set the kernel's length.  With a workspace
- * of at least this size the longest half of the tiles of every (sequence, head
- * group) run as two work items over the two halves of their key tiles, and a
- * second launch on the same stream merges the halves (their running maxima and
- * denominators) and stores the rows.  A null or smaller workspace runs every
- * tile whole: same results within rounding, no split.
+ * twice the average work; when a padded batch has fewer work items than the
+ * GPU has CUs (B=1, T=2048, 8/2 heads of 256: 128), those tiles set the
+ * kernel's length.  With a workspace of at least this size the longest half
+ * of the tiles of every (sequence, head group) run as two work items over the
+ * two halves of their key tiles, and a second launch on the same stream
+ * merges the halves (their running maxima and denominators) and stores the
+ * rows.  A null or smaller workspace runs every tile whole: same results
+ * within rounding, no split.  Only head_dim 256 splits (0 for 64 and 128);
+ * packed requests (n_seqs > 0) never do.
  */
 FD_API int64_t fd_gqa_workspace_bytes(int batch, int q_heads, int kv_heads, int seq_len, int head_dim,
                                       int n_seqs, int max_seqlen);

@@ -17,7 +17,6 @@ GOLDEN = ROOT / "tests" / "golden"
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU; run with -m gpu")
-    config.addinivalue_line("markers", "two_wave_loop_only: GQA test that runs the two-wavefront loop only")
 
 
 def pytest_collection_modifyitems(config, items):

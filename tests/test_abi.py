@@ -262,3 +262,39 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
     with pytest.raises(RuntimeError, match="HIP kernel library not found"):
         _lib.lib()
+
+
+def test_noalloc_rejects_sizes_beyond_the_scratch():
+    """fd_gated_delta_fwd_noalloc checks the workspace its sizes need against the static scratch before
+    any device call; a B=1 T=4096 call with 16 value heads needs more.  The tensor pointers are real
+    (host buffers here, never read: the check returns first)."""
+    from fastdecisions_amd import _lib
+    lib = _lib.lib()
+    T, H = 4096, 16
+    need = lib.fd_gated_delta_workspace_bytes(1, T, H, 128, 128, 0)
+    header = (ROOT / "include" / "fd_kernels.h").read_text()
+    scratch = int(re.search(r"#define FD_GD_SCRATCH_BYTES (\d+)LL", header).group(1))
+    assert need > scratch
+    bufs = [ctypes.create_string_buffer(16 * 1024) for _ in range(6)]
+    ptr = [ctypes.cast(b, ctypes.c_void_p) for b in bufs]
+    rc = lib.fd_gated_delta_fwd_noalloc(ptr[0], ptr[1], ptr[2], ptr[3], ptr[4], ptr[5], None, None, 1, T, H, H,
+                                        128, 128, ctypes.c_float(0.088), _lib.FD_DTYPE_BF16, 1, None, 0, None)
+    assert rc == _lib.FD_ERR_UNSUPPORTED
+    assert b"static scratch" in lib.fd_last_error()
+
+
+
+def test_gqa_key_split_only_at_head_dim_256():
+    """fd_gqa_workspace_bytes (host arithmetic only): head_dim 64 and 128 never ask for a key-split
+    workspace, whatever the batch; head_dim 256 does with fewer work items than CUs, including groups
+    below 4 query heads per KV head, and never for packed requests."""
+    from fastdecisions_amd import _lib
+    lib = _lib.lib()
+    for D in (64, 128):
+        for B, Hq, Hkv, T in ((1, 16, 4, 2048), (1, 16, 4, 300), (1, 4, 4, 1024), (2, 6, 3, 600)):
+            assert lib.fd_gqa_workspace_bytes(B, Hq, Hkv, T, D, 0, 0) == 0, (B, Hq, Hkv, T, D)
+    for B, Hq, Hkv, T in ((1, 8, 2, 2048), (1, 4, 4, 1024), (1, 6, 3, 600)):
+        nbytes = lib.fd_gqa_workspace_bytes(B, Hq, Hkv, T, 256, 0, 0)
+        assert nbytes > 0 and nbytes % 16 == 0, (B, Hq, Hkv, T)
+    assert lib.fd_gqa_workspace_bytes(1, 8, 2, 2048, 256, 4, 700) == 0  # packed requests
+    assert lib.fd_gqa_workspace_bytes(4, 8, 2, 2048, 256, 0, 0) == 0  # enough work items

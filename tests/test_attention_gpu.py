@@ -71,10 +71,8 @@ def test_prologue_decider_shape_from_qproj_view(oracle):
         assert u[..., R:].max() <= 1 and u[..., :R].max() <= 2 and (u == 0).mean() > 0.999
 
 
-@pytest.mark.parametrize("loop", ["0", "1"], ids=["two_waves", "one_wave"])
 @pytest.mark.parametrize("varlen", [False, True])
-def test_gated_store_equals_eager_gate(varlen, loop, monkeypatch):
-    monkeypatch.setenv("FD_GQA_ONE_WAVE", loop)  # both head_dim-128 loops share the gated store
+def test_gated_store_equals_eager_gate(varlen):
     from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
     gen = torch.Generator().manual_seed(21)
     T = 700

@@ -126,9 +126,9 @@ def test_silu_fast_path_rounds_like_torch_for_every_fp32_input():
     announce("conv SiLU fast path over every fp32 bit pattern")
     lib = _lib.lib()
     count = torch.zeros(1, dtype=torch.int64, device="cuda")
-    chunk = 1 << 30
-    for begin in range(0, 1 << 32, chunk):
-        _lib.check("fd_silu_check", lib.fd_silu_check(ctypes.c_uint32(begin), ctypes.c_uint32(chunk),
+    # one launch over 2^32 - 1 patterns (the largest count: its grid-stride index must not wrap), then the last
+    for begin, n in ((0, (1 << 32) - 1), ((1 << 32) - 1, 1)):
+        _lib.check("fd_silu_check", lib.fd_silu_check(ctypes.c_uint32(begin), ctypes.c_uint32(n),
                                                       count.data_ptr(), _lib.stream_handle(count.device)))
     torch.cuda.synchronize()
     print(f"SiLU fast path: {int(count.item())} of 2^32 fp32 inputs round differently")

@@ -29,10 +29,10 @@ def test_gated_silu_fast_path_rounds_like_the_exact_product_for_every_bf16_pair(
     announce("gated SiLU product fast path over every bf16 pair")
     lib = _lib.lib()
     count = torch.zeros(1, dtype=torch.int64, device="cuda")
-    chunk = 1 << 30
-    for begin in range(0, 1 << 32, chunk):
+    # one launch over 2^32 - 1 pairs (the largest count: its grid-stride index must not wrap), then the last
+    for begin, n in ((0, (1 << 32) - 1), ((1 << 32) - 1, 1)):
         _lib.check("fd_gated_silu_check", lib.fd_gated_silu_check(
-            ctypes.c_uint32(begin), ctypes.c_uint32(chunk), count.data_ptr(), _lib.stream_handle(count.device)))
+            ctypes.c_uint32(begin), ctypes.c_uint32(n), count.data_ptr(), _lib.stream_handle(count.device)))
     torch.cuda.synchronize()
     print(f"gated SiLU fast path: {int(count.item())} of 2^32 (y2, z) pairs round differently")
     assert int(count.item()) == 0

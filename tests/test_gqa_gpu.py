@@ -20,20 +20,6 @@ pytestmark = pytest.mark.gpu
 ATOL = 2e-2
 
 
-@pytest.fixture(autouse=True, params=["two_waves", "one_wave"])
-def gqa_loop(request, monkeypatch):
-    """Every test runs with both head_dim-64/128 loops (the launcher picks by work-item count;
-    FD_GQA_ONE_WAVE forces it).  head_dim 256 has one loop, so its cases run once.  The key-split
-    test compares the split launch with the unsplit one, both of the two-wavefront loop."""
-    one = request.param == "one_wave"
-    if one and request.node.get_closest_marker("two_wave_loop_only"):
-        pytest.skip("the key split runs the two-wavefront loop")
-    callspec = getattr(request.node, "callspec", None)
-    if one and callspec is not None and callspec.params.get("D") == 256:
-        pytest.skip("head_dim 256 has a single loop")
-    monkeypatch.setenv("FD_GQA_ONE_WAVE", "1" if one else "0")
-
-
 def sdpa_fp32(q, k, v):
     """fp32 MATH SDPA with repeated KV heads and a causal mask (q [B,Hq,T,D])."""
     group = q.shape[1] // k.shape[1]
@@ -124,7 +110,7 @@ def test_decider_shape_T2048(recipe, oracle):
 
 @pytest.mark.parametrize("B,Hq,Hkv,T,D", [
     (1, 8, 2, 2048, 256),   # real decider-2b attention shape
-    (4, 16, 4, 2048, 128),  # more than two work items per CU: the launcher's one-wavefront loop
+    (4, 16, 4, 2048, 128),  # more than two work items per CU
     (2, 8, 2, 333, 256),
     (2, 16, 4, 1000, 128),
     (1, 4, 4, 257, 128),    # MHA (group 1)
@@ -204,19 +190,30 @@ def test_varlen_equals_per_request():
     q, k, v = model_layout(1, 16, 4, T, 128, 1000)
     o = native_gqa_attention(q, k, v, cu_seqlens=torch.from_numpy(cu).cuda(), max_seqlen=max(lengths))
     torch.cuda.synchronize()
-    from fastdecisions_amd.native_gqa_kernel import set_key_split
     for a, b in zip(cu[:-1], cu[1:]):
         if b == a:
             continue
-        previous = set_key_split(False)  # whole tiles alone, as packed requests run them
-        try:
-            alone = native_gqa_attention(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b])
-        finally:
-            set_key_split(previous)
+        alone = native_gqa_attention(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b])  # default launch, no switches
         ref = sdpa_fp32(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b])
         torch.cuda.synchronize()
-        assert torch.equal(o[:, :, a:b], alone)  # same tiles relative to the request start
+        assert torch.equal(o[:, :, a:b], alone)  # head_dim 128: the same loop alone and packed
         assert (o[:, :, a:b].float() - ref).abs().max().item() <= ATOL
+
+
+@pytest.mark.parametrize("Hq,Hkv,T,D", [(16, 4, 2048, 128), (16, 4, 700, 64), (8, 2, 1024, 256)])
+def test_rows_do_not_depend_on_the_batch(Hq, Hkv, T, D):
+    """A request's rows are bit-identical alone (B=1) and in padded batches of 2 and 5 sequences
+    (different work-item counts per CU).  head_dim 256 with the key split off (its split tiles round
+    differently); head_dim 64 and 128 with the default launch, which has no switch."""
+    from fastdecisions_amd.native_gqa_kernel import native_gqa_attention
+    announce(f"gqa batch invariance {Hq}/{Hkv}x{D} T={T}")
+    split = D != 256
+    q, k, v = model_layout(5, Hq, Hkv, T, D, 1300 + D, D ** -0.5)
+    alone = native_gqa_attention(q[2:3], k[2:3], v[2:3], key_split=split)
+    for lo, hi in ((1, 3), (0, 5)):
+        batch = native_gqa_attention(q[lo:hi], k[lo:hi], v[lo:hi], key_split=split)
+        torch.cuda.synchronize()
+        assert torch.equal(batch[2 - lo:3 - lo], alone), (lo, hi)
 
 
 def test_graph_replay_with_changed_input():
@@ -260,14 +257,14 @@ def test_wrapper_rejects_bad_inputs():
         native_gqa_attention(qt, kt, kt)
 
 
-@pytest.mark.two_wave_loop_only
-@pytest.mark.parametrize("Hq,Hkv,T,D,gated", [(16, 4, 1024, 128, False), (16, 4, 1024, 128, True),
-                                               (8, 2, 2048, 256, False), (4, 4, 777, 64, False)])
+@pytest.mark.parametrize("Hq,Hkv,T,D,gated", [(8, 2, 2048, 256, False), (8, 2, 2048, 256, True),
+                                               (4, 4, 1024, 256, False),   # MHA: one head x 4 query blocks
+                                               (6, 3, 600, 256, True)])    # group 2: 2 heads x 2 query blocks
 def test_key_split_equals_the_unsplit_kernel(Hq, Hkv, T, D, gated, oracle):
-    """Padded batches with fewer work items than CUs: with the workspace fd_gqa_workspace_bytes asks
+    """head_dim 256 with fewer work items than CUs: with the workspace fd_gqa_workspace_bytes asks
     for, the long query tiles run as two halves merged by a second launch; without it every tile runs
     whole.  Both must agree to bf16 rounding (the merge order differs) and stay within the 2e-2 bar of
-    fp32 SDPA."""
+    fp32 SDPA.  Groups below 4 heads per KV head cover the split's several-query-blocks indexing."""
     import ctypes
     from fastdecisions_amd import _lib
     announce(f"gqa key split vs whole tiles B=1 T={T} {Hq}/{Hkv}x{D} gated={gated}")

@@ -49,12 +49,79 @@ def test_install_patches_fall_back_on_cpu(tiny):
     with torch.no_grad():
         before = tiny(ids)
     counts = install_hip_kernels(tiny)
-    assert counts == dict(packed_conv=3, native_gqa=1, residual_rms=4, gated_delta=3, combined_gates=3, combined_projections=3, attention_fusions=1, gated_norm=3,
-                      mlp_fusion=4)
+    assert counts == dict(packed_conv=3, native_gqa=1, residual_rms=3, residual_rms_all_layers=4, gated_delta=3,
+                          combined_gates=3, gated_norm=3, attention_fusions=1, combined_projections=3, mlp_fusion=4)
     assert install_hip_kernels(tiny) == counts  # idempotent
     with torch.no_grad():
         after = tiny(ids)
     assert torch.equal(before, after)
+
+
+def test_install_levels_are_nested():
+    """Each level installs what the one before did and its own step; the reference's three patches
+    alone come first."""
+    from fastdecisions_amd.model import INSTALL_LEVELS, TINY, build_decider, install_hip_kernels
+    assert INSTALL_LEVELS[0] == "north_star"
+    seen = set()
+    for level in INSTALL_LEVELS:
+        model = build_decider(TINY, seed=0, device="cpu", dtype=torch.float32)
+        keys = set(install_hip_kernels(model, level))
+        assert seen < keys
+        seen = keys
+    model = build_decider(TINY, seed=0, device="cpu", dtype=torch.float32)
+    assert install_hip_kernels(model, "north_star") == dict(packed_conv=3, native_gqa=1, residual_rms=3)
+    assert not getattr(model.core, "_fd_residual_chain", False)
+    assert not any(getattr(m, "_fd_gated_delta", False) for m in model.core.modules())
+    with pytest.raises(ValueError, match="level must be one of"):
+        install_hip_kernels(model, "everything")
+
+
+def test_plain_causal_mask_guard():
+    """The native GQA patch runs the kernel only for masks that add nothing to its in-kernel causal mask
+    (the reference's checks, ref: experiments/native_gqa/bench_native_gqa_model.py:84-99)."""
+    from fastdecisions_amd.native_gqa import plain_causal
+    t = 6
+    tril = torch.ones((t, t), dtype=torch.bool).tril()
+    additive = torch.zeros((1, 1, t, t)).masked_fill(~tril, torch.finfo(torch.float32).min)
+    assert plain_causal(None, t)
+    assert plain_causal(tril[None, None].expand(2, 1, t, t), t)
+    assert plain_causal(additive, t)
+    assert plain_causal(additive.to(torch.bfloat16), t)
+    padded = tril.clone()
+    padded[:, 0] = False  # a left-padded first token
+    assert not plain_causal(padded[None, None], t)
+    segments = tril.clone()
+    segments[3:, :3] = False  # two packed requests
+    assert not plain_causal(segments[None, None], t)
+    biased = additive.clone()
+    biased[..., 2, 1] = 0.5  # an attention bias
+    assert not plain_causal(biased, t)
+    leaky = additive.clone()
+    leaky[..., 0, 1] = -10.0  # a future position not fully masked
+    assert not plain_causal(leaky, t)
+    assert not plain_causal(tril[None, None], t + 1)  # another length
+    assert not plain_causal(torch.zeros((1, 1, t, t), dtype=torch.int32), t)
+
+
+def test_non_causal_mask_runs_the_original_attention(tiny, monkeypatch):
+    """candidate_forward hands a padding mask to the original forward even where it would otherwise run
+    the kernel (inputs made to look like CUDA bf16 inference)."""
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5Attention
+    from fastdecisions_amd import native_gqa
+    attn = next(m for m in tiny.core.modules() if isinstance(m, Qwen3_5Attention))
+    native_gqa.install_native_gqa(tiny.core)
+    calls = []
+    monkeypatch.setattr(attn, "_native_gqa_original_forward", lambda *a, **k: calls.append(k) or ("orig", None))
+
+    class Hidden:  # stands in for a CUDA bf16 [1, 4, hidden] tensor: only the attributes the guard reads
+        is_cuda = True
+        dtype = torch.bfloat16
+        shape = (1, 4, tiny.shape.hidden_size)
+    mask = torch.ones((4, 4), dtype=torch.bool).tril()
+    mask[:, 0] = False
+    with torch.no_grad():
+        assert attn.forward(Hidden(), (None, None), mask[None, None]) == ("orig", None)
+    assert len(calls) == 1
 
 
 def test_workloads_are_seeded_and_pack_consistently():

@@ -116,14 +116,9 @@ def test_config5_packed_varlen_decisions_identical(full_model):
     try:
         ids, cu, segments, max_len, slots = pack(reqs)
         announce("config5 packed HIP forward")
-        from fastdecisions_amd.native_gqa_kernel import set_key_split
         with torch.no_grad():
             got = full_model(ids, cu_seqlens=cu, segments=segments, max_seqlen=max_len)
-            previous = set_key_split(False)  # whole query tiles, as the packed batch runs them
-            try:
-                alone_hip = [full_model(r.ids[None].cuda())[0, r.slots].cpu().numpy() for r in reqs]
-            finally:
-                set_key_split(previous)
+            alone_hip = [full_model(r.ids[None].cuda())[0, r.slots].cpu().numpy() for r in reqs]
         torch.cuda.synchronize()
         got_slots = got[0, slots].cpu().numpy()
         for i, r in enumerate(reqs):

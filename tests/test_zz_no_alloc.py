@@ -79,13 +79,3 @@ def test_noalloc_equals_the_workspace_entry_point(case):
     again_o, again_s = _run(True, q, k, v, g, beta, s0, cu_t)
     assert torch.equal(again_o.view(torch.int16), want_o.view(torch.int16)), what
     assert torch.equal(again_s.view(torch.int32), want_s.view(torch.int32)), what
-
-
-def test_noalloc_rejects_sizes_beyond_the_scratch():
-    from fastdecisions_amd import _lib
-    lib = _lib.lib()
-    f = ctypes.c_void_p(256)  # never dereferenced: the size check comes first
-    rc = lib.fd_gated_delta_fwd_noalloc(f, f, f, f, f, f, None, None, 1, 4096, 16, 16, 128, 128,
-                                        ctypes.c_float(0.088), _lib.FD_DTYPE_BF16, 1, None, 0, None)
-    assert rc == _lib.FD_ERR_UNSUPPORTED
-    assert b"static scratch" in lib.fd_last_error()
