@@ -72,7 +72,8 @@ constexpr uint32_t kSiluTieWindow = 32;
 __device__ __forceinline__ float fd_silu_bf16(float y) {
   float f = y * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(y * -1.44269504088896341f));
   const uint32_t low = __float_as_uint(f) & 0xffffu;
-  if (y < -16.0f || low + kSiluTieWindow - 0x8000u < 2u * kSiluTieWindow) f = fd_silu(y);
+  // bitwise |: both tests on every lane, one branch (|| would branch around the fast path too)
+  if ((y < -16.0f) | (low + kSiluTieWindow - 0x8000u < 2u * kSiluTieWindow)) f = fd_silu(y);
   return f;
 }
 
@@ -86,6 +87,6 @@ __device__ __forceinline__ float fd_silu_bf16(float y) {
 __device__ __forceinline__ float fd_gated_silu_bf16(float g, float z) {
   float p = g * (z * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z * -1.44269504088896341f)));
   const uint32_t low = __float_as_uint(p) & 0xffffu;
-  if (z < -16.0f || low + kSiluTieWindow - 0x8000u < 2u * kSiluTieWindow) p = g * fd_silu(z);
+  if ((z < -16.0f) | (low + kSiluTieWindow - 0x8000u < 2u * kSiluTieWindow)) p = g * fd_silu(z);
   return p;
 }

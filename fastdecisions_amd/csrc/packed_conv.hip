@@ -4,13 +4,21 @@
 // (ref: src/decider/packed_conv_kernel.py:115-191), which reads x [B*T, C]
 // token-major and stores straight into q/k/v [B, T, H, D].
 //
-// HBM-bound, no MFMA.  A thread owns 8 contiguous channels (one 16-byte
+// HBM-bound, no MFMA.  A thread owns 4 contiguous channels (one 8-byte
 // vector) and a run of RUN consecutive tokens.  The causal window of the last
 // WIDTH-1 inputs stays in registers, so each input vector is loaded from HBM
 // once; only the WIDTH-1 halo rows in front of a run are read a second time
 // (from L2: the neighbouring run is mapped to the same XCD, see below).  A
-// wavefront covers 512 channels = 1 KiB contiguous per token row, for both the
-// loads and the stores.
+// wavefront covers 256 channels = 512 B contiguous per token row, for both the
+// loads and the stores (4 full 128-byte lines).  Each input row is widened to
+// fp64 once, into a ring of WIDTH rows, and serves the WIDTH outputs that use it.
+//
+// 16-byte accesses were measured slower here (B=1, T=2048, C=6144): 8 channels
+// per thread need 152 VGPRs (3 wavefronts per SIMD instead of 6) and took
+// 15.8 us against 14.7; lane pairs that load and store 16 bytes and swap halves
+// (DPP) took 15.9.  The whole grid is resident in one round at these sizes, so
+// occupancy, not the access width, sets how much of the arithmetic hides under
+// the transfers (the same loads and stores without the arithmetic: 10.75 us).
 //
 // XCD-aware block order: the hardware deals workgroups round-robin over the 8
 // XCDs, so block b runs on XCD b % 8.  Token runs are renumbered so that each
@@ -40,20 +48,21 @@ constexpr int kThreads = 256;
 constexpr int kNumXcd = 8;
 constexpr int kCh = 4;  // channels per thread: one 8-byte vector of bf16
 
-struct Vec4 {
-  float v[kCh];
-};
-
-__device__ __forceinline__ Vec4 unpack4(uint2 raw) {
-  Vec4 r;
-  r.v[0] = fd_lo(raw.x);
-  r.v[1] = fd_hi(raw.x);
-  r.v[2] = fd_lo(raw.y);
-  r.v[3] = fd_hi(raw.y);
-  return r;
-}
-
 __device__ __forceinline__ uint2 load8(const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); }
+
+// The 4 bf16 of an 8-byte vector as doubles (exact), element e = channel c0 + e.
+// The empty asm pins each widened value in registers: without it the compiler
+// re-derives the conversions at every one of the WIDTH outputs that use a value.
+__device__ __forceinline__ void widen4(const uint2 raw, double (&d)[kCh]) {
+  const uint32_t u[2] = {raw.x, raw.y};
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    d[2 * i] = static_cast<double>(fd_lo(u[i]));
+    d[2 * i + 1] = static_cast<double>(fd_hi(u[i]));
+  }
+#pragma unroll
+  for (int e = 0; e < kCh; ++e) asm volatile("" : "+v"(d[e]));
+}
 
 // Grid: 1-D, n_col * n_runs_padded blocks (a multiple of 8).  Linear block b
 // runs on XCD b % 8; logical block L = (b % 8) * (nblocks / 8) + b / 8, so the
@@ -117,8 +126,16 @@ __device__ __forceinline__ void conv_block(int lin, int nblocks, const ConvArgs&
       for (int j = 0; j < WIDTH; ++j) wd[j][e] = fd_bf16_to_f32(w[(c0 + e) * WIDTH + j]);
     }
   }
-  Vec4 bs;
-  if (HAS_BIAS) bs = unpack4(load8(bias + c0));
+  float bs[kCh];
+  if (HAS_BIAS) {
+    const uint2 b = load8(bias + c0);
+    const uint32_t u[2] = {b.x, b.y};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      bs[2 * i] = fd_lo(u[i]);
+      bs[2 * i + 1] = fd_hi(u[i]);
+    }
+  }
 
   // Sequence containing r0: [seg_start, seg_end).  For varlen, seg is the
   // largest index in [0, n_seqs) with cu_seqlens[seg] <= r0; the offsets are
@@ -150,43 +167,47 @@ __device__ __forceinline__ void conv_block(int lin, int nblocks, const ConvArgs&
   }
   const uint16_t* __restrict__ xc = x + c0;
 
-  // One output: the W taps of row r (window values in xw, zero before the
-  // row's sequence start), bias, activation; returns the fp32 result.
-  auto tap_sum = [&](const double (&xw)[WIDTH], int e) {
-    // from +0, so an exact zero sum is +0 whatever the signs of the products
-    double acc = 0.0;
+  // The 8 outputs of one row from the window rows win[0..WIDTH-1] (oldest
+  // first): exact tap sums rounded once to fp32, bias, activation, one
+  // 16-byte store of the bf16 results.  The fast SiLU runs on every lane;
+  // the exact expression only where fd_silu_bf16's test sends it.
+  auto row_out = [&](const double* const (&win)[WIDTH], int r) {
+    float y[kCh];
 #pragma unroll
-    for (int j = 0; j < WIDTH; ++j) acc = __builtin_fma(wd[j][e], xw[j], acc);
-    float t = static_cast<float>(acc);
-    if (HAS_BIAS) t = t + bs.v[e];
-    return SILU ? fd_silu_bf16(t) : t;
+    for (int e = 0; e < kCh; ++e) {
+      double acc = 0.0;  // from +0, so an exact zero sum is +0 whatever the signs of the products
+#pragma unroll
+      for (int j = 0; j < WIDTH; ++j) acc = __builtin_fma(wd[j][e], win[j][e], acc);
+      float t = static_cast<float>(acc);
+      if (HAS_BIAS) t = t + bs[e];
+      y[e] = SILU ? fd_silu_bf16(t) : t;
+    }
+    *reinterpret_cast<uint2*>(dst + static_cast<int64_t>(r) * dst_stride + dst_c) =
+        make_uint2(fd_pack2(y[0], y[1]), fd_pack2(y[2], y[3]));
   };
 
   if (r0 + RUN <= seg_end && r0 + RUN <= total_rows) {
     // The whole run lies in one sequence (the usual case).  Every load is
     // issued up front: WIDTH-1 halo rows (zero before the sequence start) +
-    // RUN rows; every index below is static after unrolling.
+    // RUN rows.  Each row is widened to fp64 once, into a ring of WIDTH rows
+    // (row m in slot m % WIDTH); every index below is static after unrolling.
     uint2 raw[WIDTH - 1 + RUN];
 #pragma unroll
     for (int m = 0; m < WIDTH - 1 + RUN; ++m) {
       const int r = r0 - (WIDTH - 1) + m;
-      raw[m] = (m >= WIDTH - 1 || r >= seg_start) ? load8(xc + static_cast<int64_t>(r) * x_row) : make_uint2(0u, 0u);
+      raw[m] = (m >= WIDTH - 1 || r >= seg_start) ? load8(xc + static_cast<int64_t>(r) * x_row)
+                                                   : make_uint2(0u, 0u);
     }
+    double ring[WIDTH][kCh];
+#pragma unroll
+    for (int m = 0; m < WIDTH - 1; ++m) widen4(raw[m], ring[m % WIDTH]);
 #pragma unroll
     for (int i = 0; i < RUN; ++i) {
-      float y[kCh];
+      widen4(raw[i + WIDTH - 1], ring[(i + WIDTH - 1) % WIDTH]);
+      const double* win[WIDTH];
 #pragma unroll
-      for (int e = 0; e < kCh; ++e) {
-        double xw[WIDTH];
-#pragma unroll
-        for (int j = 0; j < WIDTH; ++j) {
-          const uint2 u = raw[i + j];
-          xw[j] = (e & 1) ? fd_hi(e < 2 ? u.x : u.y) : fd_lo(e < 2 ? u.x : u.y);
-        }
-        y[e] = tap_sum(xw, e);
-      }
-      *reinterpret_cast<uint2*>(dst + static_cast<int64_t>(r0 + i) * dst_stride + dst_c) =
-          make_uint2(fd_pack2(y[0], y[1]), fd_pack2(y[2], y[3]));
+      for (int j = 0; j < WIDTH; ++j) win[j] = ring[(i + j) % WIDTH];
+      row_out(win, r0 + i);
     }
   } else {
     // A sequence starts inside the run, or the run passes the last row: one
@@ -204,22 +225,16 @@ __device__ __forceinline__ void conv_block(int lin, int nblocks, const ConvArgs&
           seg_end = start + seq_len;
         }
       }
-      Vec4 xv[WIDTH];
+      double xw[WIDTH][kCh];
 #pragma unroll
       for (int j = 0; j < WIDTH; ++j) {
         const int src = r - (WIDTH - 1) + j;
-        xv[j] = unpack4(src >= start ? load8(xc + static_cast<int64_t>(src) * x_row) : make_uint2(0u, 0u));
+        widen4(src >= start ? load8(xc + static_cast<int64_t>(src) * x_row) : make_uint2(0u, 0u), xw[j]);
       }
-      float y[kCh];
+      const double* win[WIDTH];
 #pragma unroll
-      for (int e = 0; e < kCh; ++e) {
-        double xw[WIDTH];
-#pragma unroll
-        for (int j = 0; j < WIDTH; ++j) xw[j] = xv[j].v[e];
-        y[e] = tap_sum(xw, e);
-      }
-      *reinterpret_cast<uint2*>(dst + static_cast<int64_t>(r) * dst_stride + dst_c) =
-          make_uint2(fd_pack2(y[0], y[1]), fd_pack2(y[2], y[3]));
+      for (int j = 0; j < WIDTH; ++j) win[j] = xw[j];
+      row_out(win, r);
     }
   }
 }
@@ -235,7 +250,7 @@ __global__ __launch_bounds__(kThreads) void packed_conv_kernel(ConvArgs args) {
 // so every conv block keeps its XCD) run the projection of 16 tokens each with
 // 4 wavefronts taking two hidden-dimension parts apiece, and the rest run
 // exactly the conv's blocks.  The projection's bits equal fd_gate_proj_fwd's.
-// The register budget is held to the conv kernel's own occupancy (5
+// The register budget is held to the conv kernel's own occupancy (5-6
 // wavefronts per SIMD), which the projection body would otherwise lower.
 template <int WIDTH, int RUN, typename LT, typename BT, int NB>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) void conv_gate_kernel(ConvArgs conv, fd_gate::GateProjArgs gate,
@@ -309,13 +324,14 @@ int launch_run(const char* who, const void* x, int64_t x_row, const void* w, con
 }
 
 #ifndef FD_CONV_RUN
-#define FD_CONV_RUN 4
+#define FD_CONV_RUN 8
 #endif
-// Tokens per thread: 4 gives 12 wavefronts per SIMD-round at B=1, T=2048,
-// C=6144; 2 was 14 % slower, 8 and 16 no faster (measured).  The kernel is
-// VALU-bound: about 39 VALU instructions per output (the exact SiLU's expf and
-// IEEE division are about 25 of them), so the 3/4 halo re-read, which hits L2,
-// costs less than longer runs would save.
+// Tokens per thread: 8 gives 6 wavefronts per SIMD at B=1, T=2048, C=6144 (89
+// VGPRs) and measured fastest: 4 was 3 % slower, 16 4 % slower, 2 28 % slower.
+// The fast path is about 17 VALU instructions per output: 4 fp64 fmas, 2 for
+// the input widening (once per row), the fp64 -> fp32 rounding, 5 for the
+// hardware SiLU and 4 for the tie-window test, one branch per output for the
+// exact fallback.
 constexpr int kRun = FD_CONV_RUN;
 
 int packed_conv_entry(const char* who, const void* x, int64_t x_row_stride, const void* weight, const void* bias,

@@ -12,6 +12,31 @@ softmax at temperature 1, copy to host.  Decisions are the argmax
 from __future__ import annotations
 
 import torch
+import torch.nn.functional as F
+
+
+def reference_conv1d_fn(hidden_states, weight, bias=None, activation=None, **kwargs):
+    """transformers' ``causal_conv1d_fn`` ([B, C, T] -> [B, C, T]) as BASELINE config 2 defines the
+    conv of the reference PyTorch path: fp32 ``F.conv1d`` (bias included), SiLU in fp32, one cast
+    to the input dtype.  transformers' own fallback runs the conv in bf16 and rounds its output
+    before the SiLU rounds again.  The reference's engine rebinds the same hook to a fused form
+    (ref: src/decider/engine.py:25-45) that it runs under ``torch.compile``, where it too is
+    computed in fp32 and rounded once."""
+    T = hidden_states.shape[-1]
+    y = F.conv1d(hidden_states.float(), weight.float().unsqueeze(1), None if bias is None else bias.float(),
+                 padding=weight.shape[-1] - 1, groups=hidden_states.shape[1])[..., :T]
+    if activation is not None:
+        from transformers.activations import ACT2FN
+        y = ACT2FN[activation](y)
+    return y.to(hidden_states.dtype)
+
+
+def patch_conv() -> None:
+    """Route transformers' Qwen3.5 causal conv hook to ``reference_conv1d_fn`` (process-wide, as
+    ref: src/decider/engine.py:43-45 does from its Engine constructor, :86-90).  The HIP path's
+    patched Gated-DeltaNet forward does not call the hook; its fallback to the original forward does."""
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as mq
+    mq.causal_conv1d_fn = reference_conv1d_fn
 
 
 class Engine:

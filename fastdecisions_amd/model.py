@@ -154,8 +154,13 @@ def _init_value(name: str, shape, gen: torch.Generator, device) -> torch.Tensor:
 def build_decider(shape: DeciderShape = DECIDER_2B_SHAPED, seed: int = 0, device="cuda",
                   dtype=torch.bfloat16, attn_implementation: str = "sdpa") -> DeciderModel:
     """Seeded random-init decider on ``device``.  Parameters are drawn in
-    ``named_parameters`` order from one generator on ``device``."""
+    ``named_parameters`` order from one generator on ``device``.  The model's
+    reference PyTorch path computes the causal conv as BASELINE config 2 defines
+    it (``engine.patch_conv``, which this calls, as the reference's engine does
+    before it builds its model, ref: src/decider/engine.py:86-90)."""
     from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5TextRotaryEmbedding
+    from .engine import patch_conv
+    patch_conv()
     device = torch.device(device)
     with torch.device("meta"):
         model = DeciderModel(shape, attn_implementation)

@@ -200,10 +200,14 @@ FD_API int fd_attn_prologue_fwd(const void* q_in, int64_t q_token_stride, int64_
  *   v      [batch, seq_len, value_dim] bf16 contiguous
  *
  * y[t, c] = act(w[c, W-1]*x[t, c] + w[c, 0]*x[t-W+1, c] + ... + w[c, W-2]*x[t-1, c] + bias[c])
- * evaluated in fp32 in exactly that order (the reference's order,
- * ref: src/decider/packed_conv_kernel.py:139-177), taps before the start of
- * the sequence read zero (ref: :128-176), SiLU = y / (1 + exp(-y)) (ref: :178-182),
- * one bf16 rounding; channels [0, key_dim) go to q, the next key_dim to k,
+ * with the taps of the reference (ref: src/decider/packed_conv_kernel.py:139-177):
+ * the W products are summed exactly (in fp64; products of two bf16 values are
+ * exact) and rounded once to fp32, the bias is added in fp32, SiLU is
+ * y / (1 + expf(-y)) in fp32 (ref: :178-182), then one bf16 rounding.  This is
+ * PyTorch's fp32 GPU conv1d + SiLU, then a cast, bit for bit (BASELINE config 2's
+ * definition; any fp32 tap order, the reference kernel's included, differs from
+ * it on about 0.3 % of outputs).  Taps before the start of the sequence read
+ * zero (ref: :128-176); channels [0, key_dim) go to q, the next key_dim to k,
  * the rest to v (ref: :184-191).
  *
  * Varlen: cu_seqlens (device int32[n_seqs + 1]) with batch == 1 restarts the

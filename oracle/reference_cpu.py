@@ -9,10 +9,9 @@ median wall time of repeated runs after warm-up:
   ``F.scaled_dot_product_attention(q, repeat_kv(k,4), repeat_kv(v,4), is_causal=True)``;
 * ``conv_config2`` — fp32 depthwise ``F.conv1d`` + SiLU on [1, 2048, 6144];
 * ``rmsnorm_config3`` — eager ``residual + x`` and Qwen3.5 RMSNorm on [4, 2048, 2048];
-* ``decider_forward_sample`` — the eager decider forward (transformers' Qwen3.5
+* ``decider_forward`` — the whole eager decider forward (transformers' Qwen3.5
   layers: SDPA, F.conv1d, eager RMSNorm, torch gated-delta rule) at B=1,
-  T=2048 in fp32 over a bounded slice of the 28 layers, scaled to the whole
-  forward.
+  T=2048 in fp32, all 28 layers.
 """
 from __future__ import annotations
 
@@ -100,18 +99,22 @@ def rmsnorm_config3(warmup: int = 3, runs: int = 10) -> float:
 
 
 @torch.no_grad()
-def decider_forward_sample(layers: int = 4, seq_len: int = 2048, warmup: int = 3, runs: int = 10) -> dict:
-    """Eager fp32 forward of the first ``layers`` decoder layers (3 Gated-DeltaNet + 1 GQA
-    for 4: one period of the 3:1 interleave) of the decider-2b-shaped model, plus
-    embedding, final norm and readout; median of ``runs`` after ``warmup``.  The time is
-    scaled to 28 layers (21 linear-attention + 7 full-attention), which counts the
-    embedding, final norm and readout 7 times (a few ms of the sample)."""
-    from dataclasses import replace
-
+def decider_forward(seq_len: int = 2048, warmup: int = 1, runs: int = 4) -> dict:
+    """Eager fp32 forward of the whole decider-2b-shaped model (28 layers: 21 Gated-DeltaNet +
+    7 GQA, embedding, final norm and letter readout) at B=1, T=``seq_len``; the median of ``runs``
+    after ``warmup`` (the bench keeps the sample to about half a minute of CPU work: one forward
+    takes several seconds)."""
     from fastdecisions_amd.model import DECIDER_2B_SHAPED, build_decider, synthetic_ids
-    shape = replace(DECIDER_2B_SHAPED, num_hidden_layers=layers)
-    model = build_decider(shape, seed=0, device="cpu", dtype=torch.float32)
-    ids = synthetic_ids(1, seq_len, shape.vocab_size, seed=1, device="cpu")
-    ms = _median_ms(lambda: model(ids), warmup, runs)
-    scale = DECIDER_2B_SHAPED.num_hidden_layers / layers
-    return dict(sample_ms=ms, scaled_forward_ms=ms * scale, layers=layers, scale=scale)
+    t0 = time.perf_counter()
+    model = build_decider(DECIDER_2B_SHAPED, seed=0, device="cpu", dtype=torch.float32)
+    build_s = time.perf_counter() - t0
+    ids = synthetic_ids(1, seq_len, DECIDER_2B_SHAPED.vocab_size, seed=1, device="cpu")
+    for _ in range(warmup):
+        model(ids)
+    times = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        model(ids)
+        times.append((time.perf_counter() - t) * 1e3)
+    return dict(median_ms=statistics.median(times), runs_ms=times, layers=DECIDER_2B_SHAPED.num_hidden_layers,
+                warmup=warmup, runs=runs, build_s=build_s)

@@ -54,8 +54,9 @@ def test_install_counts_and_fallback(full_model):
     from fastdecisions_amd.model import install_hip_kernels
     counts = install_hip_kernels(full_model)
     try:
-        assert counts == dict(packed_conv=21, native_gqa=7, residual_rms=28, gated_delta=21, combined_gates=21, combined_projections=21,
-                              attention_fusions=7, gated_norm=21, mlp_fusion=28)
+        assert counts == dict(packed_conv=21, native_gqa=7, residual_rms=21, residual_rms_all_layers=28, gated_delta=21,
+                              combined_gates=21, gated_norm=21, attention_fusions=7, combined_projections=21,
+                              mlp_fusion=28)
         # guarded fallbacks: grad mode goes to the original eager methods
         ids = torch.randint(0, 100, (1, 64), device="cuda")
         with torch.enable_grad():
