@@ -145,10 +145,16 @@ def _forward(self, hidden_states, cache_params=None, attention_mask=None, **kwar
             g, beta = unpack_gate_op(ab, self.A_log, self.dt_bias)
     elif hasattr(self, "_combined_gate_weight"):
         z = self.in_proj_z(hidden_states).reshape(batch, seq, -1, self.head_v_dim)
-        # one GEMM for both gate projections, one kernel for both transforms (ref: :45-48)
-        from .combined_gates import unpack_gate_op
-        ab = F.linear(hidden_states, self._combined_gate_weight)
-        g, beta = unpack_gate_op(ab, self.A_log, self.dt_bias)
+        if _gate_proj_fits(self, hidden_states):
+            # both gate projections and both transforms in one kernel whose rows do not depend on
+            # the token count (a library GEMM of this small N picks its reduction split by M)
+            from .combined_gates import gate_proj_op
+            g, beta = gate_proj_op(hidden_states, self._combined_gate_weight, self.A_log, self.dt_bias)
+        else:
+            # one GEMM for both gate projections, one kernel for both transforms (ref: :45-48)
+            from .combined_gates import unpack_gate_op
+            ab = F.linear(hidden_states, self._combined_gate_weight)
+            g, beta = unpack_gate_op(ab, self.A_log, self.dt_bias)
     else:
         z = self.in_proj_z(hidden_states).reshape(batch, seq, -1, self.head_v_dim)
         b = self.in_proj_b(hidden_states)

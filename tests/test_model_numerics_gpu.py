@@ -35,9 +35,8 @@ Bars:
 * the full HIP path's error against fp32 is no worse than 1.5x the reference
   path's (largest logit and probability error, logits outside the reference
   tolerance);
-* packed requests decide as the same requests run alone, with slot
-  probabilities (every level) and logits (the shipped levels) within the
-  reference's tolerances.
+* packed requests give the same logits as the same requests run alone, bit
+  for bit, at every level.
 """
 from __future__ import annotations
 
@@ -192,25 +191,17 @@ def test_hip_error_against_fp32_is_no_worse_than_eager(runs):
 
 
 def test_packed_requests_equal_requests_alone(runs):
-    """Packed requests decide as the same requests run alone, with logits and slot probabilities within
-    the reference's tolerances (ref: experiments/residual_rms/bench_persistent_residual_rms_model.py:91-102).
-    This build's kernels give packed and lone requests bit-identical rows (their own tests); the
-    library GEMMs between them pick their algorithm by the token count (a small-N GEMM such as the
-    a|b gate projection at the combined_gates level splits its reduction differently for the packed
-    and the lone shapes), so the whole model is held to the tolerance, not to identity: decisions and
-    slot probabilities at every level, every logit at the two shipped configurations (the
-    reference's three patches, and everything installed)."""
-    from fastdecisions_amd.numerics import compare
+    """Packed requests give the same logits as the same requests run alone, bit for bit, at every
+    install level (the reference holds them to its tolerances, ref:
+    experiments/residual_rms/bench_persistent_residual_rms_model.py:91-102).  This build's kernels
+    give packed and lone requests identical rows (their own tests), and so does the a|b gate
+    projection, which runs in this build's kernel rather than a library GEMM: a GEMM with
+    N = 2 x heads picks its reduction split by the token count, and gave packed logits 0.09 away from
+    the lone ones.  The other library GEMMs of the forward give identical rows at both token counts."""
     n4 = runs["n4"]
-    shipped = (runs["levels"][0], runs["levels"][-1])
     for level in runs["levels"]:
-        worst, outside = 0.0, 0
-        for r, packed, alone in zip(runs["reqs"][n4:], runs[level][n4:], runs[level + "/alone5"]):
-            rep = compare(packed, alone, [0] * len(r.slots), r.slots, r.nopts)
-            worst = max(worst, rep["max_abs_logit_diff"])
-            outside += rep["logits_outside_tolerance"]
-            assert rep["probs_close"] and rep["decisions_changed"] == 0, (level, rep)
-            if level in shipped:
-                assert rep["logits_close"], (level, rep)
-        print(f"config5 at {level}: packed vs alone, largest logit difference over all positions {worst:.4g}, "
-              f"{outside} logits outside the tolerance")
+        worst = 0.0
+        for packed, alone in zip(runs[level][n4:], runs[level + "/alone5"]):
+            worst = max(worst, float((packed.float() - alone.float()).abs().max()))
+        print(f"config5 at {level}: packed vs alone, largest logit difference over all positions {worst:.4g}")
+        assert worst == 0.0, (level, worst)
