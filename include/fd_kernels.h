@@ -37,6 +37,7 @@
  *   fd_packed_conv_gate_fwd  fd_packed_conv_strided_fwd and fd_gate_proj_fwd of one layer in one launch
  *   fd_silu_check       numerics self-check of the conv's SiLU (no reference counterpart)
  *   fd_gated_silu_check numerics self-check of the gated RMSNorm's last product (no reference counterpart)
+ *   fd_hbm_copy         streaming device copy, the measured HBM ceiling (no reference counterpart)
  *
  * Conventions shared by every entry point:
  *   - every tensor pointer is a device pointer; bf16 tensors are passed as raw
@@ -283,6 +284,16 @@ FD_API int fd_silu_check(uint32_t begin, uint32_t count, unsigned long long* mis
 FD_API int fd_gated_silu_check(uint32_t begin, uint32_t count, unsigned long long* mismatches, void* stream);
 
 /*
+ * Streaming device copy of `bytes` (a multiple of 16; src and dst 16-byte
+ * aligned, not overlapping) with nontemporal 16-byte loads and stores; no
+ * counterpart in the reference.  It is the copy of known traffic that
+ * bench.py measures at each bandwidth-bound kernel's byte count, so that
+ * those kernels are set against a ceiling measured on the same box and not
+ * only against the 8 TB/s published peak.
+ */
+FD_API int fd_hbm_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
+/*
  * Fused residual add + RMSNorm over rows of `width` features.
  *
  *   h            = bf16(x + residual)            (residual == NULL: h = x)
@@ -342,8 +353,9 @@ FD_API int fd_gated_delta_fwd(const void* q, const void* k, const void* v, const
                               int head_v_dim, float scale, int beta_dtype, int l2norm_qk,
                               const int32_t* cu_seqlens, int n_seqs, void* stream);
 
-/* Bytes of the static device scratch fd_gated_delta_fwd_noalloc works in (128 MiB). */
-#define FD_GD_SCRATCH_BYTES 134217728LL
+/* Bytes of the static device scratch fd_gated_delta_fwd_noalloc works in (80 MiB: the
+ * decider's B=1, T=2048 call with 16 value heads, 72.4 MiB, and a few chunks of margin). */
+#define FD_GD_SCRATCH_BYTES 83886080LL
 
 /*
  * fd_gated_delta_fwd without a workspace argument: the work runs in a static
