@@ -20,7 +20,7 @@ LIB_NAME = "libfd_kernels.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 OFFLOAD_ARCH = "gfx950"
 
-SOURCES = ["fd_abi.cpp", "add_rmsnorm.hip", "packed_conv.hip", "gqa_fwd.hip", "gated_delta.hip", "gate_transform.hip", "attn_prologue.hip", "slot_readout.hip", "gated_norm.hip"]
+SOURCES = ["fd_abi.cpp", "add_rmsnorm.hip", "packed_conv.hip", "gqa_fwd.hip", "gated_delta.hip", "gate_transform.hip", "attn_prologue.hip", "slot_readout.hip", "gated_norm.hip", "hbm_copy.hip"]
 
 COMMON_FLAGS = [
     "-O3",

@@ -118,6 +118,10 @@ SIGNATURES = {
         ctypes.c_int,
         [ctypes.c_uint32, ctypes.c_uint32, _c_void_p, _c_void_p],
     ),
+    "fd_hbm_copy": (
+        ctypes.c_int,
+        [_c_void_p, _c_void_p, ctypes.c_int64, _c_void_p],
+    ),
     "fd_gate_transform_fwd": (
         ctypes.c_int,
         [_c_void_p, _c_void_p, ctypes.c_int64, ctypes.c_int64, _c_void_p, ctypes.c_int, _c_void_p, ctypes.c_int,

@@ -27,7 +27,8 @@ def test_header_declares_the_expected_entry_points():
                                     "fd_packed_conv_strided_fwd", "fd_gated_delta_norm_fwd",
                                     "fd_gate_proj_fwd", "fd_packed_conv_gate_fwd",
                                     "fd_silu_mul_split_fwd", "fd_gated_delta_fwd_noalloc",
-                                    "fd_gqa_workspace_bytes", "fd_silu_check", "fd_gated_silu_check"}
+                                    "fd_gqa_workspace_bytes", "fd_silu_check", "fd_gated_silu_check",
+                                    "fd_hbm_copy"}
 
 
 def test_library_exports_every_declared_symbol_and_nothing_else():
@@ -106,6 +107,19 @@ def test_silu_check_argument_errors():
         _lib.FD_ERR_INVALID_ARGUMENT
     assert "2^32" in _err(lib)
     assert lib.fd_gated_silu_check(ctypes.c_uint32(5), ctypes.c_uint32(0), f, None) == _lib.FD_OK
+
+
+def test_hbm_copy_argument_errors():
+    import ctypes
+    from fastdecisions_amd import _lib
+    lib = _lib.lib()
+    f = 1 << 20
+    assert lib.fd_hbm_copy(None, f, 16, None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert lib.fd_hbm_copy(f, f + 4096, 24, None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert "multiple of 16" in _err(lib)
+    assert lib.fd_hbm_copy(f, f + 4096, -16, None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert lib.fd_hbm_copy(f + 8, f + 4096, 16, None) == _lib.FD_ERR_ALIGNMENT
+    assert lib.fd_hbm_copy(f, f + 4096, 0, None) == _lib.FD_OK  # nothing to copy, nothing launched
 
 
 def test_gqa_argument_errors():
