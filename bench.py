@@ -330,21 +330,25 @@ def bench_copy(samples: int, only: bool = True) -> dict:
 
 def bench_copy_ceiling(nbytes: int, samples: int) -> dict:
     """This library's streaming copy (``fd_hbm_copy``) moving ``nbytes`` per launch (half read, half
-    written), rotated over enough buffer pairs that more than 512 MB pass per replay so the 256 MB
-    MALL cannot serve them: the measured HBM ceiling of a bandwidth-bound kernel of the same bytes."""
+    written) in each of its shapes, rotated over enough buffer pairs that more than 512 MB pass per
+    replay so the 256 MB MALL cannot serve them; the fastest shape is the measured HBM ceiling of a
+    bandwidth-bound kernel of the same bytes."""
     import torch
-    from fastdecisions_amd.hbm_copy import hbm_copy
+    from fastdecisions_amd.hbm_copy import SHAPES, hbm_copy
     half = (nbytes // 2 + 15) // 16 * 16
     sets = max(2, -(-(600 << 20) // (2 * half)))
     xs = [torch.empty(half, dtype=torch.uint8, device="cuda").random_(0, 256) for _ in range(sets)]
     ys = [torch.empty_like(x) for x in xs]
-    graphs = {"copy": graph_of([lambda x=x, y=y: hbm_copy(x, y) for x, y in zip(xs, ys)])}
-    times = time_graphs(graphs, {"copy": sets}, samples, 3)
-    res = summary(times["copy"])
-    del xs, ys
+    graphs = {f"{u}x{bs}": graph_of([lambda x=x, y=y, u=u, bs=bs: hbm_copy(x, y, u, bs) for x, y in zip(xs, ys)])
+              for u, bs in SHAPES}
+    times = time_graphs(graphs, {k_: sets for k_ in graphs}, samples, 3)
+    res = {k_: summary(t) for k_, t in times.items()}
+    best = min(res, key=lambda k_: res[k_]["median_us"])
+    del xs, ys, graphs
     torch.cuda.empty_cache()
-    return dict(bytes=2 * half, rotated_sets=sets, hip=res, gbs=2 * half / res["median_us"] / 1e3,
-                peak_gbs=HBM_PEAK_GBS)
+    return dict(bytes=2 * half, rotated_sets=sets, shape=f"{best} (chunks per thread x block)", hip=res[best],
+                gbs=2 * half / res[best]["median_us"] / 1e3, peak_gbs=HBM_PEAK_GBS,
+                gbs_by_shape={k_: round(2 * half / r["median_us"] / 1e3) for k_, r in res.items()})
 
 
 def bench_gemm_ceiling(samples: int) -> dict:

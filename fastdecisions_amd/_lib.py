@@ -120,7 +120,7 @@ SIGNATURES = {
     ),
     "fd_hbm_copy": (
         ctypes.c_int,
-        [_c_void_p, _c_void_p, ctypes.c_int64, _c_void_p],
+        [_c_void_p, _c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, _c_void_p],
     ),
     "fd_gate_transform_fwd": (
         ctypes.c_int,

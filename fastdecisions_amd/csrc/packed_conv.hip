@@ -328,10 +328,11 @@ int launch_run(const char* who, const void* x, int64_t x_row, const void* w, con
 #endif
 // Tokens per thread: 8 gives 6 wavefronts per SIMD at B=1, T=2048, C=6144 (89
 // VGPRs) and measured fastest: 4 was 3 % slower, 16 4 % slower, 2 28 % slower.
-// The fast path is about 17 VALU instructions per output: 4 fp64 fmas, 2 for
-// the input widening (once per row), the fp64 -> fp32 rounding, 5 for the
-// hardware SiLU and 4 for the tie-window test, one branch per output for the
-// exact fallback.
+// The fast path's arithmetic is about 17 VALU instructions per output: 4 fp64
+// fmas, 2 for the input widening (once per row), the fp64 -> fp32 rounding, 5
+// for the hardware SiLU and 4 for the tie-window test, one branch per output
+// for the exact fallback.  SQ_INSTS_VALU counts 21.8 per output over a whole
+// launch at B=1, T=2048, C=6144 (addresses, packing and the run setup included).
 constexpr int kRun = FD_CONV_RUN;
 
 int packed_conv_entry(const char* who, const void* x, int64_t x_row_stride, const void* weight, const void* bias,

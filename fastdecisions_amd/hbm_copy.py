@@ -11,9 +11,12 @@ import torch
 from . import _lib
 
 
-def hbm_copy(src: torch.Tensor, dst: torch.Tensor) -> torch.Tensor:
+SHAPES = ((1, 256), (2, 256), (4, 256), (1, 512), (2, 512), (4, 512))  # (chunks per thread, block)
+
+
+def hbm_copy(src: torch.Tensor, dst: torch.Tensor, chunks_per_thread: int = 1, block: int = 256) -> torch.Tensor:
     """Copy ``src`` into ``dst`` (contiguous CUDA tensors of equal byte size, a multiple of 16,
-    16-byte aligned, not overlapping); returns ``dst``."""
+    16-byte aligned, not overlapping) in one of the ``SHAPES``; returns ``dst``."""
     if not (src.is_cuda and dst.is_cuda and src.device == dst.device):
         raise ValueError("src and dst must be CUDA tensors on one device")
     if not (src.is_contiguous() and dst.is_contiguous()):
@@ -22,6 +25,6 @@ def hbm_copy(src: torch.Tensor, dst: torch.Tensor) -> torch.Tensor:
     if dst.numel() * dst.element_size() != nbytes:
         raise ValueError("src and dst must hold the same number of bytes")
     with torch.cuda.device(src.device):
-        _lib.check("fd_hbm_copy", _lib.lib().fd_hbm_copy(src.data_ptr(), dst.data_ptr(), nbytes,
-                                                         _lib.stream_handle(src.device)))
+        _lib.check("fd_hbm_copy", _lib.lib().fd_hbm_copy(src.data_ptr(), dst.data_ptr(), nbytes, chunks_per_thread,
+                                                         block, _lib.stream_handle(src.device)))
     return dst

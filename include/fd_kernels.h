@@ -285,13 +285,15 @@ FD_API int fd_gated_silu_check(uint32_t begin, uint32_t count, unsigned long lon
 
 /*
  * Streaming device copy of `bytes` (a multiple of 16; src and dst 16-byte
- * aligned, not overlapping) with nontemporal 16-byte loads and stores; no
- * counterpart in the reference.  It is the copy of known traffic that
- * bench.py measures at each bandwidth-bound kernel's byte count, so that
- * those kernels are set against a ceiling measured on the same box and not
- * only against the 8 TB/s published peak.
+ * aligned, not overlapping) with nontemporal 16-byte loads and stores, each
+ * thread moving `chunks_per_thread` (1, 2 or 4) chunks in workgroups of
+ * `block` (256 or 512) threads; no counterpart in the reference.  It is the
+ * copy of known traffic that bench.py measures at each bandwidth-bound
+ * kernel's byte count (the best of its shapes), so that those kernels are set
+ * against a ceiling measured on the same box and not only against the
+ * 8 TB/s published peak.
  */
-FD_API int fd_hbm_copy(const void* src, void* dst, int64_t bytes, void* stream);
+FD_API int fd_hbm_copy(const void* src, void* dst, int64_t bytes, int chunks_per_thread, int block, void* stream);
 
 /*
  * Fused residual add + RMSNorm over rows of `width` features.

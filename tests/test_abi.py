@@ -114,12 +114,14 @@ def test_hbm_copy_argument_errors():
     from fastdecisions_amd import _lib
     lib = _lib.lib()
     f = 1 << 20
-    assert lib.fd_hbm_copy(None, f, 16, None) == _lib.FD_ERR_INVALID_ARGUMENT
-    assert lib.fd_hbm_copy(f, f + 4096, 24, None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert lib.fd_hbm_copy(None, f, 16, 1, 256, None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert lib.fd_hbm_copy(f, f + 4096, 24, 1, 256, None) == _lib.FD_ERR_INVALID_ARGUMENT
     assert "multiple of 16" in _err(lib)
-    assert lib.fd_hbm_copy(f, f + 4096, -16, None) == _lib.FD_ERR_INVALID_ARGUMENT
-    assert lib.fd_hbm_copy(f + 8, f + 4096, 16, None) == _lib.FD_ERR_ALIGNMENT
-    assert lib.fd_hbm_copy(f, f + 4096, 0, None) == _lib.FD_OK  # nothing to copy, nothing launched
+    assert lib.fd_hbm_copy(f, f + 4096, -16, 1, 256, None) == _lib.FD_ERR_INVALID_ARGUMENT
+    assert lib.fd_hbm_copy(f + 8, f + 4096, 16, 1, 256, None) == _lib.FD_ERR_ALIGNMENT
+    assert lib.fd_hbm_copy(f, f + 4096, 16, 3, 256, None) == _lib.FD_ERR_UNSUPPORTED
+    assert lib.fd_hbm_copy(f, f + 4096, 16, 1, 128, None) == _lib.FD_ERR_UNSUPPORTED
+    assert lib.fd_hbm_copy(f, f + 4096, 0, 4, 512, None) == _lib.FD_OK  # nothing to copy, nothing launched
 
 
 def test_gqa_argument_errors():

@@ -218,3 +218,28 @@ def test_norm_epilogue_equals_delta_rule_then_gated_norm():
         fused, _ = rule(q, k, v, g, beta, use_qk_l2norm_in_kernel=True, cu_seqlens=cu_t, norm=(z, w, 1e-6))
         torch.cuda.synchronize()
         assert torch.equal(fused, ref), (T, hk, hv, cu)
+
+
+
+@pytest.mark.parametrize("T,hk,hv,B", [(2048, 16, 16, 1), (1000, 16, 16, 1), (640, 4, 8, 2)])
+def test_rows_do_not_depend_on_the_batch(oracle, gd, T, hk, hv, B):
+    """The same sequences alone and inside a larger padded batch give the same outputs and final
+    states bit for bit (same chunks, same arithmetic), with and without an initial state."""
+    big = B + 6
+    q, k, v, g, beta = _inputs(T, hk, hv, seed=T + hv, B=big)
+    s0 = torch.randn((big, hv, 128, 128), generator=torch.Generator().manual_seed(3)) * 0.1
+    rule = _rule()
+    for init in (None, s0):
+        announce(f"gated delta alone vs in a batch: B={B} (+{big - B}) T={T} hk={hk} hv={hv} init={init is not None}")
+        args = [t.cuda() for t in (q, k, v, g, beta)]
+        out_big, fin_big = rule(*args, initial_state=None if init is None else init.cuda(), output_final_state=True,
+                                use_qk_l2norm_in_kernel=True)
+        out, fin = rule(*(t[:B].contiguous() for t in args),
+                        initial_state=None if init is None else init[:B].contiguous().cuda(), output_final_state=True,
+                        use_qk_l2norm_in_kernel=True)
+        torch.cuda.synchronize()
+        assert torch.equal(out, out_big[:B])
+        assert torch.equal(fin, fin_big[:B])
+    ref, _ = gd.chunked(_np(q[:B]), _np(k[:B]), _np(v[:B]), g[:B].numpy(), _np(beta[:B]),
+                        initial_state=s0[:B].numpy())
+    _check(oracle, to_bits(out), ref, f"B={B} T={T} hv={hv}")
