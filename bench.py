@@ -639,7 +639,7 @@ def main() -> int:
     roofline = None
     if "gqa" in kernels:
         gq = kernels["gqa"]
-        roofline = dict(bound="mfma", kernel="gqa_fwd_kernel<128> (B=1 T=2048 16/4 heads D=128)",
+        roofline = dict(bound="mfma", kernel="gqa_fwd_kernel<128, 2> (B=1 T=2048 16/4 heads D=128)",
                         achieved=gq["tflops"], peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s", frac=gq["frac"],
                         traffic=profiled_traffic(GQA_PROFILE), traffic_source=str(GQA_PROFILE.relative_to(ROOT)),
                         measured_ceiling=kernels["measured_ceilings"]["gemm"]["bf16"]["tflops"],
