@@ -4,10 +4,13 @@ Mirrors ref: src/decider/combined_gates.py: ``unpack_gate_op(combined, a_log,
 dt_bias) -> (decay, beta)`` over ``unpack_gate`` (ref: :6-16), and
 ``install_combined_gates(core)`` (ref: :19-43), which snapshots
 ``cat(in_proj_a.weight, in_proj_b.weight)`` into a non-persistent buffer so the
-packed Gated-DeltaNet forward computes both gate projections with one GEMM and
-the transform with one kernel (``fastdecisions_amd.packed_conv._forward``).
-Reinvoke after changing the projection weights.  Any head count works (the
-reference requires two bias-free [16, 2048] projections).
+packed Gated-DeltaNet forward (``fastdecisions_amd.packed_conv._forward``)
+computes both gate projections and both transforms in one kernel,
+``fastdecisions::gate_proj`` (8, 16, 24 or 32 heads, hidden a multiple of
+1024), whose rows do not depend on the token count; other head counts take
+one GEMM and the ``unpack_gate`` kernel, as the reference does.  Reinvoke
+after changing the projection weights.  Any head count works (the reference
+requires two bias-free [16, 2048] projections).
 
 ``install_combined_projections(core)`` goes further: all four input
 projections of a Gated-DeltaNet layer (q|k|v, z, a, b) become one GEMM whose

@@ -323,9 +323,6 @@ int launch_run(const char* who, const void* x, int64_t x_row, const void* w, con
   return fd_check_launch(who);
 }
 
-#ifndef FD_CONV_RUN
-#define FD_CONV_RUN 8
-#endif
 // Tokens per thread: 8 gives 6 wavefronts per SIMD at B=1, T=2048, C=6144 (89
 // VGPRs) and measured fastest: 4 was 3 % slower, 16 4 % slower, 2 28 % slower.
 // The fast path's arithmetic is about 17 VALU instructions per output: 4 fp64
@@ -333,7 +330,7 @@ int launch_run(const char* who, const void* x, int64_t x_row, const void* w, con
 // for the hardware SiLU and 4 for the tie-window test, one branch per output
 // for the exact fallback.  SQ_INSTS_VALU counts 21.8 per output over a whole
 // launch at B=1, T=2048, C=6144 (addresses, packing and the run setup included).
-constexpr int kRun = FD_CONV_RUN;
+constexpr int kRun = 8;
 
 int packed_conv_entry(const char* who, const void* x, int64_t x_row_stride, const void* weight, const void* bias,
                       void* q, void* k, void* v, int batch, int seq_len, int key_dim, int value_dim, int width,

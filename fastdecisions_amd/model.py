@@ -180,7 +180,8 @@ def build_decider(shape: DeciderShape = DECIDER_2B_SHAPED, seed: int = 0, device
 #                        RMSNorm (linear-attention decoder layers)
 #   residual_chain       add+RMSNorm in every decoder layer, each MLP residual add inside the next norm
 #   gated_delta          the chunked gated-delta rule on the HIP kernels
-#   combined_gates       a|b gate projections as one GEMM + the gate transform kernel
+#   combined_gates       both gate projections and the gate transform in one kernel (fd_gate_proj_fwd;
+#                        one GEMM + the transform kernel for head counts it does not take)
 #   gated_norm           the delta rule's gated RMSNorm in the delta-rule launch sequence
 #   attention_fusions    q/k RMSNorm + RoPE prologue, gated GQA store, q|gate|k|v as one GEMM
 #   combined_projections q|k|v|z as one GEMM, conv + a|b projection + gate transform in one launch
