@@ -14,7 +14,7 @@
 // fp64 once, into a ring of WIDTH rows, and serves the WIDTH outputs that use it.
 //
 // 16-byte accesses were measured slower here (B=1, T=2048, C=6144): 8 channels
-// per thread need 152 VGPRs (3 wavefronts per SIMD instead of 6) and took
+// per thread need 152 VGPRs (3 wavefronts per SIMD instead of 5) and took
 // 15.8 us against 14.7; lane pairs that load and store 16 bytes and swap halves
 // (DPP) took 15.9.  The whole grid is resident in one round at these sizes, so
 // occupancy, not the access width, sets how much of the arithmetic hides under
@@ -323,8 +323,10 @@ int launch_run(const char* who, const void* x, int64_t x_row, const void* w, con
   return fd_check_launch(who);
 }
 
-// Tokens per thread: 8 gives 6 wavefronts per SIMD at B=1, T=2048, C=6144 (89
-// VGPRs) and measured fastest: 4 was 3 % slower, 16 4 % slower, 2 28 % slower.
+// Tokens per thread: 8 measured fastest (89 VGPRs, 5 wavefronts per SIMD; B=1,
+// T=2048, C=6144 launches 6 per SIMD): 4 was 3 % slower, 16 4 % slower, 2 28 %
+// slower.  Held to 80 VGPRs for 6 per SIMD, the kernel spilled and took 21.0
+// against 15.0 us.
 // The fast path's arithmetic is about 17 VALU instructions per output: 4 fp64
 // fmas, 2 for the input widening (once per row), the fp64 -> fp32 rounding, 5
 // for the hardware SiLU and 4 for the tie-window test, one branch per output
