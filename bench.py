@@ -69,7 +69,7 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-kernels", action="store_true", help="skip the per-kernel micro-benchmarks")
     p.add_argument("--no-forward", action="store_true", help="skip the full-forward benchmark")
-    p.add_argument("--only-kernel", choices=["gqa", "conv", "rmsnorm", "gdr", "copy"], default=None,
+    p.add_argument("--only-kernel", choices=["gqa", "conv", "rmsnorm", "gdr", "copy", "fusions"], default=None,
                    help="profiling aid: run just this kernel's HIP timing loop ('copy' is the plain device "
                         "copy used to calibrate HBM byte counters)")
     p.add_argument("--gqa-shape", default="1,16,4,128",
@@ -312,6 +312,123 @@ def bench_gated_delta(samples: int, only: bool = False) -> dict:
         out.update(eager_torch_chunk_gated_delta_rule=res["eager_torch_chunk_gated_delta_rule"],
                    speedup_vs_eager=res["eager_torch_chunk_gated_delta_rule"]["median_us"] / us)
     return out
+
+
+def bench_fusions(samples: int, only: bool = False) -> dict:
+    """The kernels of the widened rows at the forward's shapes (B=1, T=2048, decider-2b-shaped), each
+    against the eager ops it replaces, inputs read in place from a combined projection output as in
+    the model and rotated past the 256 MB MALL: the a|b gate projection + transform, the attention
+    prologue (q/k RMSNorm + partial RoPE), the gated RMSNorm of the delta rule's output, the MLP's
+    SiLU*mul over the two gate|up GEMM outputs, and the slot-only readout (4 slots, 10 letters)."""
+    import torch
+    import torch.nn.functional as F
+    from transformers.models.qwen3_5.modeling_qwen3_5 import (Qwen3_5RMSNorm, Qwen3_5RMSNormGated,
+                                                             apply_rotary_pos_emb)
+    from fastdecisions_amd.attention_prologue_kernel import attention_prologue
+    from fastdecisions_amd.gated_norm_kernel import gated_rms_norm, silu_mul_split
+    from fastdecisions_amd.slot_projection import slot_readout
+    from fastdecisions_amd.unpack_gate_transform_kernel import gate_projection
+    T, hidden, H, D = 2048, 2048, 16, 128
+    g = torch.Generator().manual_seed(3)
+    rnd = lambda *shape, scale=1.0: (torch.randn(shape, generator=g) * scale).to(torch.bfloat16).cuda()
+    n_rep = max(10, samples // 3)
+    cases = {}
+
+    def run(name, config, bytes_, hip_fns, eager_fns, launches):
+        graphs = {"hip": graph_of(hip_fns)}
+        if not only:
+            graphs["eager"] = graph_of(eager_fns)
+        times = time_graphs(graphs, {k_: launches for k_ in graphs}, n_rep, 3)
+        res = {k_: summary(t) for k_, t in times.items()}
+        us = res["hip"]["median_us"]
+        out = dict(config=config, bytes=bytes_, hip=res["hip"], gbs=bytes_ / us / 1e3, frac=bytes_ / us / 1e3 / HBM_PEAK_GBS)
+        if not only:
+            out.update(eager=res["eager"], speedup_vs_eager=res["eager"]["median_us"] / us)
+        cases[name] = out
+
+    # a|b gate projection + gate transform (fd_gate_proj_fwd): x [T, 2048], W [32, 2048]
+    sets = 64
+    xs = [rnd(1, T, hidden) for _ in range(sets)]
+    w_ab = rnd(2 * H, hidden, scale=0.02)
+    a_log = torch.empty(H).uniform_(1, 16, generator=g).log().cuda()
+    dt_bias = torch.ones(H, device="cuda")
+
+    def gate_eager(x):
+        ab = F.linear(x, w_ab)
+        return -a_log.float().exp() * F.softplus(ab[..., :H].float() + dt_bias), ab[..., H:].sigmoid()
+    run("gate_proj", "T=2048 hidden 2048 -> a|b 2x16 heads, then g (fp32) and beta (bf16)",
+        T * hidden * 2 + 2 * H * hidden * 2 + T * H * (4 + 2),
+        [lambda x=x: gate_projection(x, w_ab, a_log, dt_bias) for x in xs], [lambda x=x: gate_eager(x) for x in xs],
+        sets)
+    del xs
+
+    # attention prologue: q|gate, k, v from the combined projection (5120 per token)
+    sets = 25
+    projs = [rnd(1, T, 5120) for _ in range(sets)]
+    qw, kw = rnd(D, scale=0.02), rnd(D, scale=0.02)
+    cos, sin = rnd(1, T, 32), rnd(1, T, 32)
+    qn, kn = Qwen3_5RMSNorm(D).cuda().to(torch.bfloat16), Qwen3_5RMSNorm(D).cuda().to(torch.bfloat16)
+    qn.weight.data.copy_(qw)
+    kn.weight.data.copy_(kw)
+    views = lambda p: (p[..., :4096].view(1, T, H, 2 * D)[..., :D], p[..., 4096:4608].view(1, T, 4, D))
+
+    def prologue_eager(p):
+        q, k = views(p)
+        return apply_rotary_pos_emb(qn(q).transpose(1, 2), kn(k).transpose(1, 2), cos, sin)
+    run("attn_prologue", "T=2048 16 q / 4 kv heads x 128, RoPE on 32 features, q and k read in place",
+        2 * T * (H + 4) * D * 2 + 2 * T * 32 * 2,
+        [lambda p=p: attention_prologue(*views(p), qw, kw, cos, sin, 1e-6) for p in projs],
+        [lambda p=p: prologue_eager(p) for p in projs], sets)
+    del projs
+
+    # gated RMSNorm: the delta rule's output rows [T*16, 128], z read in place from q|k|v|z (8192 per token)
+    sets = 21
+    xs = [rnd(T * H, D) for _ in range(sets)]
+    projs = [rnd(1, T, 8192) for _ in range(sets)]
+    nw = (1.0 + 0.02 * torch.randn(D, generator=g)).to(torch.bfloat16).cuda()
+    gnorm = Qwen3_5RMSNormGated(D).cuda().to(torch.bfloat16)
+    gnorm.weight.data.copy_(nw)
+    zview = lambda p: p[..., 6144:].view(1, T, H, D)
+    run("gated_rmsnorm", "2048 tokens x 16 heads of 128, z read in place",
+        3 * T * H * D * 2 + D * 2,
+        [lambda x=x, p=p: gated_rms_norm(x, zview(p), nw, 1e-6) for x, p in zip(xs, projs)],
+        [lambda x=x, p=p: gnorm(x.view(1, T, H, D), zview(p)) for x, p in zip(xs, projs)], sets)
+    del xs, projs
+
+    # SiLU*mul over the split gate|up GEMM outputs (8192 + 4096 columns -> 6144)
+    sets = 7
+    g1s = [rnd(1, T, 8192) for _ in range(sets)]
+    g2s = [rnd(1, T, 4096) for _ in range(sets)]
+
+    def silu_eager(a, b):
+        gate = torch.cat((a[..., :4096], b[..., :2048]), -1)
+        up = torch.cat((a[..., 4096:], b[..., 2048:]), -1)
+        return F.silu(gate) * up
+    run("silu_mul_split", "T=2048, intermediate 6144 from gate|up halves 8192 + 4096",
+        T * (8192 + 4096) * 2 + T * 6144 * 2,
+        [lambda a=a, b=b: silu_mul_split(a, b) for a, b in zip(g1s, g2s)],
+        [lambda a=a, b=b: silu_eager(a, b) for a, b in zip(g1s, g2s)], sets)
+    del g1s, g2s
+
+    # slot-only readout: final RMSNorm + 10-letter projection + masked softmax at 4 tail slots
+    hs = [rnd(1, T, hidden) for _ in range(8)]
+    fw = rnd(hidden, scale=0.02)
+    letters = rnd(10, hidden, scale=0.02)
+    rows = torch.zeros(4, dtype=torch.int32, device="cuda")
+    pos = torch.arange(T - 4, T, dtype=torch.int32, device="cuda")
+    nopts = torch.full((4,), 4, dtype=torch.int32, device="cuda")
+    fnorm = Qwen3_5RMSNorm(hidden).cuda().to(torch.bfloat16)
+    fnorm.weight.data.copy_(fw)
+
+    def readout_eager(h):
+        logits = F.linear(fnorm(h), letters).float()[0, T - 4:, :4]
+        return logits.softmax(-1)
+    run("slot_readout", "4 slots of a [1, 2048, 2048] hidden state, 10 letters (4 allowed)",
+        4 * hidden * 2 + 10 * hidden * 2 + hidden * 2 + 4 * 10 * 8,
+        [lambda h=h: slot_readout(h, fw, letters, rows, pos, nopts) for h in hs],
+        [lambda h=h: readout_eager(h) for h in hs], len(hs))
+    torch.cuda.empty_cache()
+    return cases
 
 
 def bench_copy(samples: int, only: bool = True) -> dict:
@@ -590,7 +707,7 @@ def main() -> int:
 
     if args.only_kernel:
         fn = dict(gqa=bench_gqa, conv=bench_conv, rmsnorm=bench_rmsnorm, gdr=bench_gated_delta,
-                  copy=bench_copy)[args.only_kernel]
+                  copy=bench_copy, fusions=bench_fusions)[args.only_kernel]
         kw = {"shape": tuple(int(x) for x in args.gqa_shape.split(","))} if args.only_kernel == "gqa" else {}
         print(json.dumps({args.only_kernel: fn(args.kernel_samples, only=True, **kw)}), flush=True)
         return 0
@@ -610,6 +727,8 @@ def main() -> int:
         kernels["gated_delta"] = bench_gated_delta(args.kernel_samples)
         log(f"gated delta: {kernels['gated_delta']['hip']['median_us']:.1f} us, "
             f"{kernels['gated_delta']['tflops']:.1f} TFLOP/s")
+        kernels["fusions"] = bench_fusions(args.kernel_samples)
+        log("widened rows: " + ", ".join(f"{k_} {v['hip']['median_us']:.1f} us" for k_, v in kernels["fusions"].items()))
         torch.cuda.empty_cache()
         # measured on-box ceilings beside the published peaks: this library's streaming copy at each
         # HBM-bound kernel's bytes per launch, hipBLASLt GEMMs for the MFMA-bound ones
