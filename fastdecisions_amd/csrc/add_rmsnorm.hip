@@ -7,31 +7,44 @@
 // residual emitted as a second output, as the eager decoder layer does
 // (transformers Qwen3_5DecoderLayer residual add, Qwen3_5RMSNorm).
 //
-// HBM-bound: each 16-byte chunk (8 bf16) of a row belongs to one lane, and
-// each wavefront load instruction reads 1 KiB contiguous; the row stays in
-// registers between the reduction and the store, so x and residual are read
-// from HBM exactly once.
+// HBM-bound: the row stays in registers between the reduction and the store,
+// so x and residual are read from HBM exactly once.
 //   - Widths that are a multiple of 1024: two wavefronts per row (a
-//     128-thread workgroup).  Wavefront q owns chunks (q * CPL + c) * 64 + lane,
-//     c = 0 .. CPL - 1 (CPL = width / 1024).  At the decider's [2048, 2048]
-//     call that is 4 wavefronts per SIMD instead of 2: the call went from
-//     8.7 to 7.8 us (6.8 to 5.6 us with the inputs in L2), config 3
-//     ([4, 2048, 2048]) from 23.5 to 22.4 us.
-//   - Other widths: one wavefront per row, lane l owns chunks l, l+64, l+128, ...
-//     (no LDS, no barrier).
+//     128-thread workgroup), summing the squares in the order PyTorch's GPU
+//     row reduction uses for such a width (x.float().pow(2).mean(-1)): lane l
+//     owns the 4-feature groups at 256 k + 4 l (k = 0 .. width/256 - 1), one
+//     accumulator per position in the group summed over k in order, then
+//     ((a0 + a1) + a2) + a3, then a pairwise tree over the 64 lanes (xor
+//     butterfly with offsets 1, 2, .., 32).  Wavefront 0 holds the first half
+//     of the k and hands its accumulators to wavefront 1 through LDS.  Each
+//     wavefront load reads 512 B contiguous.  With the inverse square root
+//     rounded as torch.rsqrt rounds it, the normed output equals eager
+//     Qwen3_5RMSNorm bit for bit at the decider's [2048, 2048] and config 3's
+//     [8192, 2048] (PyTorch picks this reduction for a few hundred rows and
+//     more; very short inputs may reduce otherwise).
+//   - Other widths: one wavefront per row, lane l owns the 8-feature chunks
+//     l, l+64, l+128, ...; the sum in chunk order per lane, then an xor
+//     butterfly with offsets 32, 16, .., 1 (no LDS, no barrier).
 //
 // fp32 sequence (the CPU restatement reproduces it bit for bit):
 //   h_i    = bf16(f32(x_i) + f32(r_i))
-//   lane   : s = 0; for each owned chunk in order, for e = 0..7: s = s + h*h (two roundings)
-//   wave   : for off = 32,16,8,4,2,1: s = s + shfl_xor(s, off)
-//   row    : the wavefront's s, or with two wavefronts s(q = 0) + s(q = 1)
-//   inv    = 1 / sqrt(s / width + eps)       (correctly rounded sqrt and division)
+//   s      = the sum of h_i * h_i in the order above (each product and sum rounded)
+//   inv    = 1 / sqrt(s * fl(1 / width) + eps), rounded once (fp64 root and quotient)
 //   out_i  = bf16((h_i * inv) * g_i),  g_i = 1 + w_i  or  w_i
 #include "fd_common.h"
 
 namespace {
 
 constexpr int kRowsPerBlock = 4;  // one row per wavefront, 256 threads
+
+// 1 / sqrt(v) rounded once to fp32, as torch.rsqrt rounds it on this platform
+// (measured equal on 4M fp32 inputs; the hardware v_rsq_f32 differs on 11 %,
+// 1 / sqrtf, which rounds twice, on 28 %): the fp64 quotient of the fp64 root
+// is within 2^-52 relative of the exact value, far inside half an fp32 ulp.
+// Once per row, so the fp64 work costs nothing.
+__device__ __forceinline__ float inv_rms(float v) {
+  return static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(v)));
+}
 
 template <typename WT>
 __device__ __forceinline__ void load_gain8(const WT* w, int chunk, int gain_offset, float g[8]);
@@ -141,10 +154,8 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void add_rmsnorm_kernel(
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_xor(s, off, 64);
 
-    // Plain '/' and __builtin_sqrtf are IEEE correctly rounded in HIP device code
-    // (correctly rounded fp32 divide/sqrt is the HIP default).
-    const float mean = s / static_cast<float>(width);
-    const float inv = 1.0f / __builtin_sqrtf(mean + eps);
+    const float mean = s * (1.0f / static_cast<float>(width));
+    const float inv = inv_rms(mean + eps);
 
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
@@ -166,68 +177,106 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void add_rmsnorm_kernel(
 }
 
 // Two wavefronts per row (width == 1024 * CPL), one row per 128-thread
-// workgroup; the order of the fp32 operations is the file header's.
+// workgroup, summing the squares in PyTorch's order for a row reduction of
+// this width: lane l owns the 4-feature groups 256 k + 4 l .. +3 (k = 0 .. K-1,
+// K = width / 256), with one accumulator per group position summed over k in
+// order, then ((a0 + a1) + a2) + a3, then a pairwise tree over the 64 lanes.
+// Wavefront 0 holds k < K/2 and hands its accumulators to wavefront 1, which
+// continues with the rest.
+template <typename WT>
+__device__ __forceinline__ void load_gain4(const WT* w, int f, int gain_offset, float g[4]);
+
+template <>
+__device__ __forceinline__ void load_gain4<uint16_t>(const uint16_t* w, int f, int gain_offset, float g[4]) {
+  const uint2 raw = *reinterpret_cast<const uint2*>(w + f);
+  g[0] = fd_lo(raw.x); g[1] = fd_hi(raw.x); g[2] = fd_lo(raw.y); g[3] = fd_hi(raw.y);
+  if (gain_offset) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) g[e] = 1.0f + g[e];
+  }
+}
+
+template <>
+__device__ __forceinline__ void load_gain4<float>(const float* w, int f, int gain_offset, float g[4]) {
+  const float4 a = *reinterpret_cast<const float4*>(w + f);
+  g[0] = a.x; g[1] = a.y; g[2] = a.z; g[3] = a.w;
+  if (gain_offset) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) g[e] = 1.0f + g[e];
+  }
+}
+
 template <int CPL, typename WT, bool HAS_RES>
 __global__ __launch_bounds__(128) void add_rmsnorm_pair_kernel(
     const uint16_t* x, const uint16_t* res, const WT* __restrict__ w,
     uint16_t* out, uint16_t* res_out, int width, float eps, int gain_offset) {
-  __shared__ float part[2];
+  constexpr int KH = 2 * CPL;  // 4-feature groups per lane of each wavefront
+  __shared__ float part[4 * 64];
+  __shared__ float inv_s;
   const int lane = threadIdx.x & 63;
   const int q = threadIdx.x >> 6;
   const int64_t base = static_cast<int64_t>(blockIdx.x) * width;
   // every load before any store (residual_out may alias residual)
-  uint4 xv[CPL], rv[CPL];
+  uint2 xv[KH], rv[KH];
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) {
-    const int chunk = (q * CPL + c) * 64 + lane;
-    xv[c] = *reinterpret_cast<const uint4*>(x + base + chunk * 8);
-    rv[c] = make_uint4(0u, 0u, 0u, 0u);
-    if (HAS_RES) rv[c] = *reinterpret_cast<const uint4*>(res + base + chunk * 8);
+  for (int j = 0; j < KH; ++j) {
+    const int f = 256 * (q * KH + j) + 4 * lane;
+    xv[j] = *reinterpret_cast<const uint2*>(x + base + f);
+    rv[j] = make_uint2(0u, 0u);
+    if (HAS_RES) rv[j] = *reinterpret_cast<const uint2*>(res + base + f);
   }
-  uint32_t hw[CPL][4];
-  float h[CPL][8];
-  float s = 0.0f;
+  uint32_t hw[KH][2];
+  float h[KH][4];
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) {
-    const uint32_t xw[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
-    const uint32_t rw[4] = {rv[c].x, rv[c].y, rv[c].z, rv[c].w};
+  for (int j = 0; j < KH; ++j) {
+    const uint32_t xw[2] = {xv[j].x, xv[j].y};
+    const uint32_t rw[2] = {rv[j].x, rv[j].y};
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      hw[c][p] = HAS_RES ? fd_pack2(fd_lo(xw[p]) + fd_lo(rw[p]), fd_hi(xw[p]) + fd_hi(rw[p])) : xw[p];
-      h[c][2 * p] = fd_lo(hw[c][p]);
-      h[c][2 * p + 1] = fd_hi(hw[c][p]);
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float sq = h[c][e] * h[c][e];
-      s = s + sq;
+    for (int p = 0; p < 2; ++p) {
+      hw[j][p] = HAS_RES ? fd_pack2(fd_lo(xw[p]) + fd_lo(rw[p]), fd_hi(xw[p]) + fd_hi(rw[p])) : xw[p];
+      h[j][2 * p] = fd_lo(hw[j][p]);
+      h[j][2 * p + 1] = fd_hi(hw[j][p]);
     }
   }
   if (HAS_RES && res_out != nullptr) {
 #pragma unroll
-    for (int c = 0; c < CPL; ++c)
-      *reinterpret_cast<uint4*>(res_out + base + ((q * CPL + c) * 64 + lane) * 8) =
-          make_uint4(hw[c][0], hw[c][1], hw[c][2], hw[c][3]);
+    for (int j = 0; j < KH; ++j)
+      *reinterpret_cast<uint2*>(res_out + base + 256 * (q * KH + j) + 4 * lane) = make_uint2(hw[j][0], hw[j][1]);
   }
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (q == 0) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_xor(s, off, 64);
-  if (lane == 0) part[q] = s;
+    for (int j = 0; j < KH; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = acc[i] + h[j][i] * h[j][i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part[i * 64 + lane] = acc[i];
+  }
   __syncthreads();
-  const float mean = (part[0] + part[1]) / static_cast<float>(width);
-  const float inv = 1.0f / __builtin_sqrtf(mean + eps);
+  if (q == 1) {
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) {
-    const int chunk = (q * CPL + c) * 64 + lane;
-    float g[8];
-    load_gain8<WT>(w, chunk, gain_offset, g);
-    uint32_t o[4];
+    for (int i = 0; i < 4; ++i) acc[i] = part[i * 64 + lane];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      float a = (h[c][2 * p] * inv) * g[2 * p];
-      float b = (h[c][2 * p + 1] * inv) * g[2 * p + 1];
-      o[p] = fd_pack2(a, b);
-    }
-    *reinterpret_cast<uint4*>(out + base + chunk * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+    for (int j = 0; j < KH; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = acc[i] + h[j][i] * h[j][i];
+    float s = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+#pragma unroll
+    for (int off = 1; off <= 32; off <<= 1) s = s + __shfl_xor(s, off, 64);
+    const float mean = s * (1.0f / static_cast<float>(width));  // PyTorch's mean: the sum times fl(1 / width)
+    const float inv = inv_rms(mean + eps);
+    if (lane == 0) inv_s = inv;
+  }
+  __syncthreads();
+  const float inv = inv_s;
+#pragma unroll
+  for (int j = 0; j < KH; ++j) {
+    const int f = 256 * (q * KH + j) + 4 * lane;
+    float g[4];
+    load_gain4<WT>(w, f, gain_offset, g);
+    const float a0 = (h[j][0] * inv) * g[0], a1 = (h[j][1] * inv) * g[1];
+    const float a2 = (h[j][2] * inv) * g[2], a3 = (h[j][3] * inv) * g[3];
+    *reinterpret_cast<uint2*>(out + base + f) = make_uint2(fd_pack2(a0, a1), fd_pack2(a2, a3));
   }
 }
 

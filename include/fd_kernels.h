@@ -304,8 +304,11 @@ FD_API int fd_hbm_copy(const void* src, void* dst, int64_t bytes, int chunks_per
  *                  g = 1 + weight (gain_offset = 1, Qwen3.5 form) or weight (0)
  *
  * x, residual, out, residual_out: [rows, width] bf16 contiguous; weight:
- * [width] of weight_dtype (FD_DTYPE_BF16 or FD_DTYPE_F32).  fp32 accumulation,
- * fixed reduction order, correctly rounded sqrt and division.  out may alias x.
+ * [width] of weight_dtype (FD_DTYPE_BF16 or FD_DTYPE_F32).  fp32 accumulation
+ * in a fixed order; mean = sum * fl(1 / width); the inverse root rounded once
+ * to fp32.  For widths that are a multiple of 1024 the order is the one
+ * PyTorch's GPU row mean uses at width 2048, so at that width `out` equals
+ * eager Qwen3_5RMSNorm on the GPU bit for bit.  out may alias x.
  *
  * Limits: width a multiple of 8 in [8, 8192]; pointers 16-byte aligned.
  */

@@ -17,11 +17,12 @@
  *     the (w + 1) gain; the residual is rounded to bf16 before it is normalised as in
  *     transformers' Qwen3_5DecoderLayer + Qwen3_5RMSNorm).
  * The summation order of the RMSNorm matches the GPU kernel's documented order
- * (per-lane chunk order, then a 6-step xor butterfly over 64 lanes; for widths
- * that are a multiple of 1024 two wavefronts per row, whose sums are added), so GPU
- * output is compared bit for bit; the mathematics pins this restatement
- * independently (tests/test_oracle.py: fp64 closed forms, torch's F.conv1d and
- * eager RMSNorm, special cases).
+ * (widths a multiple of 1024: PyTorch's GPU row-mean order, 4-feature groups per
+ * lane strided by 256, four accumulators, a pairwise tree over 64 lanes; other
+ * widths: per-lane chunk order, then a 6-step xor butterfly), so GPU output is
+ * compared bit for bit; the mathematics pins this restatement independently
+ * (tests/test_oracle.py: fp64 closed forms, torch's F.conv1d and eager RMSNorm,
+ * special cases), and on the GPU eager RMSNorm at width 2048 equals it bit for bit.
  */
 #include <math.h>
 #include <stddef.h>
@@ -147,25 +148,40 @@ int fd_oracle_add_rmsnorm(const uint16_t* x, const uint16_t* residual, const voi
         h[i] = bf16_to_f32(x[base + i]);
       }
     }
-    /* one wavefront per row: lane l owns chunks l, l+64, l+128, ... (8 features each);
-     * width a multiple of 1024: two wavefronts, wavefront q's lane l owns chunks
-     * (q * cpl + c) * 64 + l for c = 0 .. cpl - 1, and the row sum is s(0) + s(1) */
-    const int waves = width % 1024 == 0 ? 2 : 1;
-    const int cpl = width / 1024;
-    float row_sum = 0.0f;
-    for (int q = 0; q < waves; ++q) {
-      float lane_sum[64];
+    float row_sum;
+    float lane_sum[64];
+    if (width % 1024 == 0) {
+      /* width a multiple of 1024 (PyTorch's GPU row-mean order at this width):
+       * lane l owns the 4-feature groups at 256 k + 4 l, k = 0 .. width/256 - 1;
+       * one accumulator per group position, summed over k in order, then
+       * ((a0 + a1) + a2) + a3, then a pairwise tree over the lanes with
+       * partner offsets 1, 2, .., 32 */
+      for (int l = 0; l < 64; ++l) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int k = 0; k < width / 256; ++k)
+          for (int i = 0; i < 4; ++i) {
+            const float hv = h[256 * k + 4 * l + i];
+            const float sq = hv * hv;
+            acc[i] = acc[i] + sq;
+          }
+        lane_sum[l] = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+      }
+      for (int off = 1; off <= 32; off <<= 1) {
+        float next[64];
+        for (int l = 0; l < 64; ++l) next[l] = lane_sum[l] + lane_sum[l ^ off];
+        memcpy(lane_sum, next, sizeof(next));
+      }
+    } else {
+      /* other widths: lane l owns the 8-feature chunks l, l+64, l+128, ..., its sum in
+       * chunk order, then an xor butterfly with offsets 32, 16, .., 1 */
       for (int l = 0; l < 64; ++l) {
         float s = 0.0f;
-        const int n_own = waves == 2 ? cpl : (nchunks - l + 63) / 64;
-        for (int c = 0; c < n_own; ++c) {
-          const int chunk = waves == 2 ? (q * cpl + c) * 64 + l : l + 64 * c;
+        for (int c = l; c < nchunks; c += 64)
           for (int e = 0; e < 8; ++e) {
-            const float hv = h[chunk * 8 + e];
+            const float hv = h[c * 8 + e];
             const float sq = hv * hv;
             s = s + sq;
           }
-        }
         lane_sum[l] = s;
       }
       for (int off = 32; off >= 1; off >>= 1) {
@@ -173,10 +189,12 @@ int fd_oracle_add_rmsnorm(const uint16_t* x, const uint16_t* residual, const voi
         for (int l = 0; l < 64; ++l) next[l] = lane_sum[l] + lane_sum[l ^ off];
         memcpy(lane_sum, next, sizeof(next));
       }
-      row_sum = q == 0 ? lane_sum[0] : row_sum + lane_sum[0];
     }
-    const float mean = row_sum / (float)width;
-    const float inv = 1.0f / sqrtf(mean + eps);
+    row_sum = lane_sum[0];
+    /* the mean as PyTorch forms it (the sum times fl(1 / width)); the inverse root
+     * rounded once to fp32, from the fp64 root and quotient */
+    const float mean = row_sum * (1.0f / (float)width);
+    const float inv = (float)(1.0 / sqrt((double)(mean + eps)));
     for (int i = 0; i < width; ++i) {
       float g = weight_dtype == 1 ? ((const float*)weight)[i] : bf16_to_f32(((const uint16_t*)weight)[i]);
       if (gain_offset) g = 1.0f + g;

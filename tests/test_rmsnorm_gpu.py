@@ -1,8 +1,11 @@
 """GPU parity of the fused residual add + RMSNorm kernel (fd_add_rmsnorm_fwd).
 
 Bar: updated residual bit-exact vs eager ``residual + x``; normed bit-exact vs
-the oracle's fp32 sequence and <= 1 bf16 ulp vs eager ``Qwen3_5RMSNorm``
-(BASELINE config 3).
+the oracle's fp32 sequence everywhere, and bit-exact vs eager ``Qwen3_5RMSNorm``
+on the GPU at width 2048 with a few hundred rows or more (BASELINE config 3 and
+the decider's [2048, 2048]), where PyTorch's row mean sums in the order the
+kernel follows.  Against CPU eager (the committed golden vectors, whose
+reduction order differs) the bar is <= 1 bf16 ulp.
 """
 from __future__ import annotations
 
@@ -61,11 +64,28 @@ def test_config3_full_size():
     torch.cuda.synchronize()
     assert torch.equal(res.view(torch.int16), ref_res.view(torch.int16))
     d = ulp_diff(to_bits(out), to_bits(ref_out))
-    print(f"config3: normed vs eager: {int((d != 0).sum())} of {d.size} differ by 1 ulp, max {int(d.max())}")
-    assert d.max() <= 1
+    print(f"config3: normed vs eager: {int((d != 0).sum())} of {d.size} differ, max {int(d.max())} ulp")
+    assert d.max() == 0
     want, want_res = oracle.add_rmsnorm(to_bits(x), to_bits(r), to_bits(w))
     assert np.array_equal(to_bits(out), want)
     assert np.array_equal(to_bits(res), want_res)
+
+
+@pytest.mark.parametrize("rows,scale,seed", [(2048, 1.0, 5), (2048, 8.0, 6), (300, 1.0, 7), (8192, 0.01, 8)])
+def test_equals_eager_at_width_2048(rows, scale, seed):
+    """The decider's residual stream ([2048, 2048] for B=1, T=2048) through the fused kernel and through
+    eager Qwen3_5RMSNorm on the GPU: every output bit equal."""
+    from fastdecisions_amd.persistent_residual_rms_kernel import fused_add_rms_norm
+    announce(f"rmsnorm vs eager rows={rows} scale={scale}")
+    x = seeded((rows, 2048), seed, scale).cuda()
+    r = seeded((rows, 2048), seed + 100, scale).cuda()
+    w = seeded((2048,), seed + 200, 0.02).cuda()
+    out, res = fused_add_rms_norm(x, r, w, 1e-6)
+    ref_out, ref_res = eager(x, r, w)
+    torch.cuda.synchronize()
+    assert torch.equal(res.view(torch.int16), ref_res.view(torch.int16))
+    d = ulp_diff(to_bits(out), to_bits(ref_out))
+    assert d.max() == 0, (int((d != 0).sum()), int(d.max()))
 
 
 @pytest.mark.parametrize("rows,width", [(1, 8), (3, 64), (5, 520), (7, 1000), (1025, 2048), (9, 4096),
