@@ -29,7 +29,7 @@
 // fp32 sequence (the CPU restatement reproduces it bit for bit):
 //   h_i    = bf16(f32(x_i) + f32(r_i))
 //   s      = the sum of h_i * h_i in the order above (each product and sum rounded)
-//   inv    = 1 / sqrt(s * fl(1 / width) + eps), rounded once (fp64 root and quotient)
+//   inv    = fp32(1 / sqrt(s * fl(1 / width) + eps)), the root and quotient in fp64
 //   out_i  = bf16((h_i * inv) * g_i),  g_i = 1 + w_i  or  w_i
 #include "fd_common.h"
 
@@ -37,11 +37,11 @@ namespace {
 
 constexpr int kRowsPerBlock = 4;  // one row per wavefront, 256 threads
 
-// 1 / sqrt(v) rounded once to fp32, as torch.rsqrt rounds it on this platform
-// (measured equal on 4M fp32 inputs; the hardware v_rsq_f32 differs on 11 %,
-// 1 / sqrtf, which rounds twice, on 28 %): the fp64 quotient of the fp64 root
-// is within 2^-52 relative of the exact value, far inside half an fp32 ulp.
-// Once per row, so the fp64 work costs nothing.
+// 1 / sqrt(v) evaluated in fp64 (IEEE root and quotient, together within
+// 2^-52 relative of the exact value) and rounded to fp32.  It equals
+// torch.rsqrt on this platform on every input measured (4M fp32 values; the
+// hardware v_rsq_f32 differs on 11 % of them, 1 / sqrtf, which rounds twice in
+// fp32, on 28 %).  Once per row, so the fp64 work costs nothing.
 __device__ __forceinline__ float inv_rms(float v) {
   return static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(v)));
 }

@@ -14,9 +14,12 @@
 // HBM-bound: a 16-lane group owns one (token, head) row of 128 features, 8 per
 // lane (one 16-byte load and store); the sum of squares is reduced with an xor
 // butterfly inside the group and the rotation partner is one lane-xor away.
-// fp32 sequence of the norm (the CPU restatement reproduces it bit for bit):
-//   lane: s = 0; for e in 0..7: s = s + x_e*x_e;  group: s += shfl_xor(s, 8, 4, 2, 1)
-//   inv = 1 / sqrt(s / 128 + eps);  y = bf16((x * inv) * g),  g = 1 + w or w
+// fp32 sequence of the norm, the order PyTorch's GPU row mean uses at width 128
+// (so the normed rows equal eager Qwen3_5RMSNorm bit for bit; the CPU
+// restatement reproduces it):
+//   lane: a = ((x0^2 + x1^2) + x2^2) + x3^2, b = the same over x4..x7, s = a + b
+//   group: s += shfl_xor(s, 1, 2, 4, 8)
+//   inv = fp32(1 / sqrt(s / 128 + eps)) from the fp64 root and quotient;  y = bf16((x * inv) * g),  g = 1 + w or w
 #include "fd_common.h"
 
 namespace {
@@ -84,14 +87,23 @@ __global__ __launch_bounds__(kThreads) void attn_prologue_kernel(PrologueArgs a)
     x[2 * i] = fd_lo(wd[i]);
     x[2 * i + 1] = fd_hi(wd[i]);
   }
-  float s = 0.0f;
+  // PyTorch's order for a row mean of width 128: 32 slots of 4 features, each
+  // ((x0^2 + x1^2) + x2^2) + x3^2, then a pairwise tree over the slots; a lane
+  // holds slots 2 ln and 2 ln + 1, so the tree's first level is inside the lane
+  float sa = x[0] * x[0], sb = x[4] * x[4];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) s = s + x[e] * x[e];
-  s = s + __shfl_xor(s, 8);
-  s = s + __shfl_xor(s, 4);
-  s = s + __shfl_xor(s, 2);
+  for (int e = 1; e < 4; ++e) {
+    sa = sa + x[e] * x[e];
+    sb = sb + x[4 + e] * x[4 + e];
+  }
+  float s = sa + sb;
   s = s + __shfl_xor(s, 1);
-  const float inv = 1.0f / __builtin_sqrtf(s / static_cast<float>(kD) + a.eps);
+  s = s + __shfl_xor(s, 2);
+  s = s + __shfl_xor(s, 4);
+  s = s + __shfl_xor(s, 8);
+  // 1 / sqrt in fp64 (root and quotient), rounded to fp32: torch.rsqrt's value on every input measured
+  const float inv =
+      static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(s * (1.0f / static_cast<float>(kD)) + a.eps)));
   float gw[8];
   if (a.w_vec) {
     if (a.w_f32) {

@@ -11,7 +11,11 @@
 // (fd_gated_silu_bf16: the exact expression where the bf16 rounding could
 // differ; fd_gated_silu_check verifies every (y2, z) pair of bf16 values).
 // A 16-lane group owns one row of 128 (8 features per lane, 16-byte accesses);
-// rows of 64 or 256 use 8 or 32 lanes.
+// rows of 64 or 256 use 8 or 32 lanes.  The mean of squares sums in the order
+// PyTorch's GPU row mean uses for these widths (slots of 4 features, each
+// summed in feature order, then a pairwise tree over the slots) and the inverse
+// root is evaluated in fp64, so at widths 64, 128 and 256 the rows equal eager
+// Qwen3_5RMSNormGated bit for bit.
 //
 // fd_silu_mul_fwd replaces the MLP's ``act_fn(gate_proj(x)) * up_proj(x)``
 // (transformers Qwen3_5MLP) on a combined [rows, 2*width] gate|up projection:
@@ -79,12 +83,21 @@ __global__ __launch_bounds__(kThreads) void gated_rmsnorm_kernel(const uint16_t*
       wv[e] = W_F32 ? static_cast<const float*>(w)[ln * 8 + e]
                     : fd_bf16_to_f32(static_cast<const uint16_t*>(w)[ln * 8 + e]);
   }
-  float s = 0.0f;
+  // PyTorch's order for a row mean of this width: width/4 slots of 4 features,
+  // each ((x0^2 + x1^2) + x2^2) + x3^2, then a pairwise tree over the slots; a
+  // lane holds slots 2 ln and 2 ln + 1, so the tree's first level is inside it
+  float sa = xv[0] * xv[0], sb = xv[4] * xv[4];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) s = s + xv[e] * xv[e];
+  for (int e = 1; e < 4; ++e) {
+    sa = sa + xv[e] * xv[e];
+    sb = sb + xv[4 + e] * xv[4 + e];
+  }
+  float s = sa + sb;
 #pragma unroll
-  for (int off = LANES / 2; off >= 1; off >>= 1) s = s + __shfl_xor(s, off);
-  const float inv = 1.0f / __builtin_sqrtf(s / static_cast<float>(kWidth) + eps);
+  for (int off = 1; off < LANES; off <<= 1) s = s + __shfl_xor(s, off);
+  // 1 / sqrt in fp64 (root and quotient), rounded to fp32: torch.rsqrt's value on every input measured
+  const float inv = static_cast<float>(
+      1.0 / __builtin_sqrt(static_cast<double>(s * (1.0f / static_cast<float>(kWidth)) + eps)));
   float y[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {

@@ -11,9 +11,10 @@
 //   y        = bf16((x * (1 / sqrt(mean(x^2) + eps))) * g),   g = 1 + w or w
 //   logit[k] = bf16(sum_d y_d * W[k, d])                        (F.linear on bf16)
 //   prob     = softmax(logit[:nopts] / temperature), 0 past nopts
-// One workgroup (256 threads) per slot: the row is read once (16-byte loads),
-// reduced across the workgroup, normalised into LDS, then each wavefront takes
-// every 4th letter row of W with a wavefront reduction per letter.
+// One workgroup (256 threads) per slot: the row's sum of squares is formed in
+// the order PyTorch's GPU row mean uses (for H a multiple of 256; then y equals
+// eager's normed row bit for bit), the row normalised into LDS, then each
+// wavefront takes every 4th letter row of W with a wavefront reduction per letter.
 #include "fd_common.h"
 
 namespace {
@@ -58,32 +59,56 @@ __global__ __launch_bounds__(kThreads) void slot_readout_kernel(SlotArgs a) {
   const uint16_t* x = a.hidden + (static_cast<int64_t>(b) * a.T + t) * a.H;
   const int nch = a.H / 8;
 
-  float s = 0.0f;
+  // the row, widened to fp32 into LDS (16-byte loads); each thread later
+  // normalises the same features in place
   for (int c = tid; c < nch; c += kThreads) {
     const uint4 raw = *reinterpret_cast<const uint4*>(x + 8 * c);
-    const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float lo = fd_lo(wd[i]), hi = fd_hi(wd[i]);
-      s = s + lo * lo;
-      s = s + hi * hi;
-    }
+    *reinterpret_cast<float4*>(sy + 8 * c) = make_float4(fd_lo(raw.x), fd_hi(raw.x), fd_lo(raw.y), fd_hi(raw.y));
+    *reinterpret_cast<float4*>(sy + 8 * c + 4) = make_float4(fd_lo(raw.z), fd_hi(raw.z), fd_lo(raw.w), fd_hi(raw.w));
   }
-  s = wave_sum(s);
-  if (l == 0) red[wv] = s;
   __syncthreads();
-  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
-  const float inv = 1.0f / __builtin_sqrtf(tot / static_cast<float>(a.H) + a.eps);
+  const bool torch_order = a.H % 256 == 0;
+  if (torch_order) {
+    // PyTorch's order for a row mean of this width (the model's final norm runs
+    // over every row in eager): lane l owns the 4-feature groups at 256 k + 4 l,
+    // one accumulator per group position summed over k in order, then
+    // ((a0 + a1) + a2) + a3, then a pairwise tree over the 64 lanes.
+    if (wv == 0) {
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int k = 0; k < a.H / 256; ++k) {
+        const float4 v = *reinterpret_cast<const float4*>(sy + 256 * k + 4 * l);
+        acc[0] = acc[0] + v.x * v.x;
+        acc[1] = acc[1] + v.y * v.y;
+        acc[2] = acc[2] + v.z * v.z;
+        acc[3] = acc[3] + v.w * v.w;
+      }
+      float s = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+#pragma unroll
+      for (int off = 1; off <= 32; off <<= 1) s = s + __shfl_xor(s, off);
+      if (l == 0) red[0] = s;
+    }
+  } else {
+    float s = 0.0f;
+    for (int c = tid; c < nch; c += kThreads) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s = s + sy[8 * c + e] * sy[8 * c + e];
+    }
+    s = wave_sum(s);
+    if (l == 0) red[wv] = s;
+  }
+  __syncthreads();
+  const float tot = torch_order ? red[0] : (red[0] + red[1]) + (red[2] + red[3]);
+  // the mean as torch forms it (the sum times fl(1 / H)); 1 / sqrt evaluated in
+  // fp64 and rounded to fp32, which matched torch.rsqrt on every input measured
+  const float inv = static_cast<float>(
+      1.0 / __builtin_sqrt(static_cast<double>(tot * (1.0f / static_cast<float>(a.H)) + a.eps)));
   for (int c = tid; c < nch; c += kThreads) {
-    const uint4 raw = *reinterpret_cast<const uint4*>(x + 8 * c);
-    const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float xv = (e & 1) ? fd_hi(wd[e >> 1]) : fd_lo(wd[e >> 1]);
       float g = a.w_f32 ? static_cast<const float*>(a.norm_w)[8 * c + e]
                         : fd_bf16_to_f32(static_cast<const uint16_t*>(a.norm_w)[8 * c + e]);
       if (a.gain_offset) g = 1.0f + g;
-      sy[8 * c + e] = bf16r((xv * inv) * g);
+      sy[8 * c + e] = bf16r((sy[8 * c + e] * inv) * g);
     }
   }
   __syncthreads();

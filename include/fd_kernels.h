@@ -172,7 +172,9 @@ FD_API int fd_gqa_gated_fwd(const void* q, const void* k, const void* v, const v
  *   y   = bf16((x * (1 / sqrt(mean(x^2) + eps))) * g),  g = 1 + w (gain_offset) or w
  *   out = bf16(bf16(y_i * cos_i) + bf16(rot_i * sin_i)) for i < rotary_dim,
  *         rot = (-y[R/2:R], y[0:R/2]);  out_i = y_i for i >= rotary_dim
- * fp32 arithmetic, fixed reduction order, correctly rounded sqrt and division.
+ * fp32 arithmetic; the sum of squares in the order PyTorch's GPU row mean uses
+ * at width 128 and the inverse root evaluated in fp64 and rounded to fp32, so the
+ * rows equal the eager ops on the GPU bit for bit.
  *
  *   q_in  token t, head h at q_in + t*q_token_stride + h*q_head_stride (bf16, 128 contiguous)
  *         (e.g. the query half of the q_proj output [tokens, q_heads, 2*head_dim])
@@ -305,8 +307,8 @@ FD_API int fd_hbm_copy(const void* src, void* dst, int64_t bytes, int chunks_per
  *
  * x, residual, out, residual_out: [rows, width] bf16 contiguous; weight:
  * [width] of weight_dtype (FD_DTYPE_BF16 or FD_DTYPE_F32).  fp32 accumulation
- * in a fixed order; mean = sum * fl(1 / width); the inverse root rounded once
- * to fp32.  For widths that are a multiple of 1024 the order is the one
+ * in a fixed order; mean = sum * fl(1 / width); the inverse root evaluated in
+ * fp64 and rounded to fp32.  For widths that are a multiple of 1024 the order is the one
  * PyTorch's GPU row mean uses at width 2048, so at that width `out` equals
  * eager Qwen3_5RMSNorm on the GPU bit for bit.  out may alias x.
  *
@@ -458,7 +460,10 @@ FD_API int fd_gate_proj_fwd(const void* x, int64_t x_row_stride, const void* wei
  *   y         = bf16((x * (1 / sqrt(mean(x^2) + eps))) * g),  g = 1 + w (gain_offset) or w
  *   logits[n] = bf16(y . letters[k]) for every letter k           (F.linear on bf16)
  *   probs[n]  = softmax(logits[n, :nopts[n]] / temperature), 0 for k >= nopts[n]
- * fp32 arithmetic; slots outside [0, batch) x [0, seq_len) read row 0, position 0.
+ * fp32 arithmetic; for widths that are a multiple of 256 the sum of squares runs
+ * in the order PyTorch's GPU row mean uses (y then equals eager's normed row bit
+ * for bit), the inverse root evaluated in fp64 and rounded to fp32; slots outside
+ * [0, batch) x [0, seq_len) read row 0, position 0.
  *
  *   hidden   [batch, seq_len, width] bf16 contiguous (the residual stream before the final norm)
  *   norm_weight [width] of weight_dtype;  letters [n_letters, width] bf16 contiguous
@@ -481,7 +486,9 @@ FD_API int fd_slot_readout_fwd(const void* hidden, int batch, int seq_len, int w
  * x, out [rows, width] bf16 contiguous, rows = tokens * heads (row r = token r / heads,
  * head r % heads); gate z of row r at gate + token*gate_token_stride + head*gate_head_stride
  * (elements: a [tokens, heads, width] view, e.g. part of a combined projection output);
- * weight [width] of weight_dtype.
+ * weight [width] of weight_dtype.  The sum of squares runs in the order PyTorch's GPU
+ * row mean uses at these widths and the inverse root is evaluated in fp64 and rounded
+ * to fp32, so `out` equals eager Qwen3_5RMSNormGated on the GPU bit for bit.
  * Limits: width in {64, 128, 256}; 16-byte aligned pointers, strides multiples of 8.
  */
 FD_API int fd_gated_rmsnorm_fwd(const void* x, const void* gate, int64_t gate_token_stride,

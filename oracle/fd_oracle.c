@@ -192,7 +192,7 @@ int fd_oracle_add_rmsnorm(const uint16_t* x, const uint16_t* residual, const voi
     }
     row_sum = lane_sum[0];
     /* the mean as PyTorch forms it (the sum times fl(1 / width)); the inverse root
-     * rounded once to fp32, from the fp64 root and quotient */
+     * evaluated in fp64 (root and quotient) and rounded to fp32 */
     const float mean = row_sum * (1.0f / (float)width);
     const float inv = (float)(1.0 / sqrt((double)(mean + eps)));
     for (int i = 0; i < width; ++i) {
@@ -206,8 +206,8 @@ int fd_oracle_add_rmsnorm(const uint16_t* x, const uint16_t* residual, const voi
 }
 
 /* Attention prologue on rows of 128 bf16 features (row r belongs to token r / heads):
- * RMSNorm with the GPU kernel's summation order (16 lanes of 8 features: per-lane
- * sum in feature order, then an xor butterfly over the 16 lanes), gain (1 + w) or w,
+ * RMSNorm with PyTorch's GPU summation order at width 128 (32 slots of 4 features,
+ * then a pairwise tree) and the inverse root evaluated in fp64, gain (1 + w) or w,
  * one bf16 rounding; then the rotary embedding of the first `rot` features with
  * every bf16 product and sum rounded (transformers apply_rotary_pos_emb on bf16;
  * ref: experiments/native_gqa/bench_native_gqa_model.py:47-53).
@@ -222,22 +222,24 @@ int fd_oracle_attn_prologue(const uint16_t* x, int64_t rows, int heads, const vo
     const uint16_t* xr = x + (size_t)r * 128;
     float v[128], y[128];
     for (int i = 0; i < 128; ++i) v[i] = bf16_to_f32(xr[i]);
-    float lane[16];
-    for (int l = 0; l < 16; ++l) {
-      float s = 0.0f;
-      for (int e = 0; e < 8; ++e) {
-        const float sq = v[8 * l + e] * v[8 * l + e];
+    /* PyTorch's GPU row-mean order at width 128: 32 slots of 4 features, each
+     * ((x0^2 + x1^2) + x2^2) + x3^2, then a pairwise tree over the slots */
+    float slot[32];
+    for (int l = 0; l < 32; ++l) {
+      float s = v[4 * l] * v[4 * l];
+      for (int e = 1; e < 4; ++e) {
+        const float sq = v[4 * l + e] * v[4 * l + e];
         s = s + sq;
       }
-      lane[l] = s;
+      slot[l] = s;
     }
-    for (int off = 8; off >= 1; off >>= 1) {
-      float next[16];
-      for (int l = 0; l < 16; ++l) next[l] = lane[l] + lane[l ^ off];
-      memcpy(lane, next, sizeof(next));
+    for (int off = 1; off <= 16; off <<= 1) {
+      float next[32];
+      for (int l = 0; l < 32; ++l) next[l] = slot[l] + slot[l ^ off];
+      memcpy(slot, next, sizeof(next));
     }
-    const float mean = lane[0] / 128.0f;
-    const float inv = 1.0f / sqrtf(mean + eps);
+    const float mean = slot[0] * (1.0f / 128.0f);
+    const float inv = (float)(1.0 / sqrt((double)(mean + eps)));
     for (int i = 0; i < 128; ++i) {
       float g = weight_dtype == 1 ? ((const float*)weight)[i] : bf16_to_f32(((const uint16_t*)weight)[i]);
       if (gain_offset) g = 1.0f + g;

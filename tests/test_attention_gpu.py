@@ -2,10 +2,11 @@
 attention store (fd_gqa_gated_fwd).
 
 Bars: the prologue is bit-exact against the C restatement of its fp32 sequence
-(oracle/fd_oracle.c) and, against transformers' eager q_norm / k_norm /
-apply_rotary_pos_emb, within one bf16 ulp on the golden fixture and (on this
-GPU, where the eager norm sums in another order) within one ulp on the
-pass-through features and two on the rotated ones, with > 99.9 % identical;
+(oracle/fd_oracle.c), bit-exact against transformers' eager q_norm / k_norm /
+apply_rotary_pos_emb on this GPU (the kernel sums the squares in the order
+PyTorch's GPU row mean uses at width 128 and rounds the inverse root once, as
+torch.rsqrt does), and within one bf16 ulp of the CPU-eager golden fixture,
+whose reduction order differs;
 the gated store is bit-exact against the eager ``out * sigmoid(gate)`` on the
 kernel's own ungated output.
 """
@@ -36,7 +37,7 @@ def test_prologue_golden(oracle, golden):
 
 def test_prologue_decider_shape_from_qproj_view(oracle):
     """q is the query half of the q_proj output [B, T, 16, 256] (no copy), k [B, T, 4, 128];
-    bit-exact vs the oracle and within one ulp of the eager ops on this GPU."""
+    bit-exact vs the oracle and vs the eager ops on this GPU."""
     from transformers.models.qwen3_5 import modeling_qwen3_5 as mq
     from fastdecisions_amd.attention_prologue_kernel import attention_prologue
     from fastdecisions_amd.model import DECIDER_2B_SHAPED, make_config
@@ -64,11 +65,7 @@ def test_prologue_decider_shape_from_qproj_view(oracle):
     uq = ulp_diff(to_bits(qo), to_bits(qe.transpose(1, 2)))
     uk = ulp_diff(to_bits(ko), to_bits(ke.transpose(1, 2)))
     print(f"prologue vs eager on GPU: max ulp q {uq.max()} k {uk.max()}, identical {(uq == 0).mean():.5f}")
-    # a norm that rounds one ulp apart (another fp32 summation order) stays one ulp apart
-    # in the pass-through features and can reach two in a rotated one (a sum of two rounded products)
-    R = cos.shape[-1]
-    for u in (uq, uk):
-        assert u[..., R:].max() <= 1 and u[..., :R].max() <= 2 and (u == 0).mean() > 0.999
+    assert uq.max() == 0 and uk.max() == 0
 
 
 @pytest.mark.parametrize("varlen", [False, True])
