@@ -4,21 +4,20 @@
 // (ref: src/decider/packed_conv_kernel.py:115-191), which reads x [B*T, C]
 // token-major and stores straight into q/k/v [B, T, H, D].
 //
-// HBM-bound, no MFMA.  A thread owns 4 contiguous channels (one 8-byte
-// vector) and a run of RUN consecutive tokens.  The causal window of the last
+// HBM-bound, no MFMA.  A thread owns 2 contiguous channels (one 4-byte
+// access) and a run of RUN consecutive tokens.  The causal window of the last
 // WIDTH-1 inputs stays in registers, so each input vector is loaded from HBM
 // once; only the WIDTH-1 halo rows in front of a run are read a second time
 // (from L2: the neighbouring run is mapped to the same XCD, see below).  A
-// wavefront covers 256 channels = 512 B contiguous per token row, for both the
-// loads and the stores (4 full 128-byte lines).  Each input row is widened to
+// wavefront covers 128 channels = 256 B contiguous per token row, for both the
+// loads and the stores (2 full 128-byte lines).  Each input row is widened to
 // fp64 once, into a ring of WIDTH rows, and serves the WIDTH outputs that use it.
 //
-// 16-byte accesses were measured slower here (B=1, T=2048, C=6144): 8 channels
-// per thread need 152 VGPRs (3 wavefronts per SIMD instead of 5) and took
-// 15.8 us against 14.7; lane pairs that load and store 16 bytes and swap halves
-// (DPP) took 15.9.  The whole grid is resident in one round at these sizes, so
-// occupancy, not the access width, sets how much of the arithmetic hides under
-// the transfers (the same loads and stores without the arithmetic: 10.75 us).
+// Occupancy, not the access width, sets how much of the arithmetic hides under
+// the transfers (B=1, T=2048, C=6144; the loads and stores alone take about
+// 10.7 us): 2 channels per thread need 51 VGPRs, so 8 wavefronts share a SIMD,
+// and took 13.6 us; 4 channels (8-byte accesses, 89 VGPRs, 5 wavefronts per
+// SIMD) took 14.7 us, 8 channels (16-byte, 152 VGPRs, 3 per SIMD) 15.8 us.
 //
 // XCD-aware block order: the hardware deals workgroups round-robin over the 8
 // XCDs, so block b runs on XCD b % 8.  Token runs are renumbered so that each
@@ -46,20 +45,16 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kNumXcd = 8;
-constexpr int kCh = 4;  // channels per thread: one 8-byte vector of bf16
+constexpr int kCh = 2;  // channels per thread: one 4-byte pair of bf16
 
-__device__ __forceinline__ uint2 load8(const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); }
+__device__ __forceinline__ uint32_t load4(const uint16_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
 
-// The 4 bf16 of an 8-byte vector as doubles (exact), element e = channel c0 + e.
+// The 2 bf16 of a 4-byte pair as doubles (exact), element e = channel c0 + e.
 // The empty asm pins each widened value in registers: without it the compiler
 // re-derives the conversions at every one of the WIDTH outputs that use a value.
-__device__ __forceinline__ void widen4(const uint2 raw, double (&d)[kCh]) {
-  const uint32_t u[2] = {raw.x, raw.y};
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    d[2 * i] = static_cast<double>(fd_lo(u[i]));
-    d[2 * i + 1] = static_cast<double>(fd_hi(u[i]));
-  }
+__device__ __forceinline__ void widen2(const uint32_t raw, double (&d)[kCh]) {
+  d[0] = static_cast<double>(fd_lo(raw));
+  d[1] = static_cast<double>(fd_hi(raw));
 #pragma unroll
   for (int e = 0; e < kCh; ++e) asm volatile("" : "+v"(d[e]));
 }
@@ -106,18 +101,14 @@ __device__ __forceinline__ void conv_block(int lin, int nblocks, const ConvArgs&
   // WIDTH-1 multiplies the current token.
   double wd[WIDTH][kCh];
   if (WIDTH == 4) {
-    const uint4* wp = reinterpret_cast<const uint4*>(w + c0 * 4);  // 4 channels x 4 taps = 32 B
+    const uint4 t = *reinterpret_cast<const uint4*>(w + c0 * 4);  // 2 channels x 4 taps = 16 B
+    const uint32_t u[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint4 t = wp[i];  // channels 2i, 2i+1, taps 0..3 each
-      const uint32_t u[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        wd[2 * j][2 * i] = fd_lo(u[j]);
-        wd[2 * j + 1][2 * i] = fd_hi(u[j]);
-        wd[2 * j][2 * i + 1] = fd_lo(u[2 + j]);
-        wd[2 * j + 1][2 * i + 1] = fd_hi(u[2 + j]);
-      }
+    for (int e = 0; e < kCh; ++e) {
+      wd[0][e] = fd_lo(u[2 * e]);
+      wd[1][e] = fd_hi(u[2 * e]);
+      wd[2][e] = fd_lo(u[2 * e + 1]);
+      wd[3][e] = fd_hi(u[2 * e + 1]);
     }
   } else {
 #pragma unroll
@@ -128,13 +119,9 @@ __device__ __forceinline__ void conv_block(int lin, int nblocks, const ConvArgs&
   }
   float bs[kCh];
   if (HAS_BIAS) {
-    const uint2 b = load8(bias + c0);
-    const uint32_t u[2] = {b.x, b.y};
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      bs[2 * i] = fd_lo(u[i]);
-      bs[2 * i + 1] = fd_hi(u[i]);
-    }
+    const uint32_t b = load4(bias + c0);
+    bs[0] = fd_lo(b);
+    bs[1] = fd_hi(b);
   }
 
   // Sequence containing r0: [seg_start, seg_end).  For varlen, seg is the
@@ -167,9 +154,9 @@ __device__ __forceinline__ void conv_block(int lin, int nblocks, const ConvArgs&
   }
   const uint16_t* __restrict__ xc = x + c0;
 
-  // The 8 outputs of one row from the window rows win[0..WIDTH-1] (oldest
+  // The outputs of one row from the window rows win[0..WIDTH-1] (oldest
   // first): exact tap sums rounded once to fp32, bias, activation, one
-  // 16-byte store of the bf16 results.  The fast SiLU runs on every lane;
+  // 4-byte store of the bf16 results.  The fast SiLU runs on every lane;
   // the exact expression only where fd_silu_bf16's test sends it.
   auto row_out = [&](const double* const (&win)[WIDTH], int r) {
     float y[kCh];
@@ -182,8 +169,7 @@ __device__ __forceinline__ void conv_block(int lin, int nblocks, const ConvArgs&
       if (HAS_BIAS) t = t + bs[e];
       y[e] = SILU ? fd_silu_bf16(t) : t;
     }
-    *reinterpret_cast<uint2*>(dst + static_cast<int64_t>(r) * dst_stride + dst_c) =
-        make_uint2(fd_pack2(y[0], y[1]), fd_pack2(y[2], y[3]));
+    *reinterpret_cast<uint32_t*>(dst + static_cast<int64_t>(r) * dst_stride + dst_c) = fd_pack2(y[0], y[1]);
   };
 
   if (r0 + RUN <= seg_end && r0 + RUN <= total_rows) {
@@ -191,19 +177,18 @@ __device__ __forceinline__ void conv_block(int lin, int nblocks, const ConvArgs&
     // issued up front: WIDTH-1 halo rows (zero before the sequence start) +
     // RUN rows.  Each row is widened to fp64 once, into a ring of WIDTH rows
     // (row m in slot m % WIDTH); every index below is static after unrolling.
-    uint2 raw[WIDTH - 1 + RUN];
+    uint32_t raw[WIDTH - 1 + RUN];
 #pragma unroll
     for (int m = 0; m < WIDTH - 1 + RUN; ++m) {
       const int r = r0 - (WIDTH - 1) + m;
-      raw[m] = (m >= WIDTH - 1 || r >= seg_start) ? load8(xc + static_cast<int64_t>(r) * x_row)
-                                                   : make_uint2(0u, 0u);
+      raw[m] = (m >= WIDTH - 1 || r >= seg_start) ? load4(xc + static_cast<int64_t>(r) * x_row) : 0u;
     }
     double ring[WIDTH][kCh];
 #pragma unroll
-    for (int m = 0; m < WIDTH - 1; ++m) widen4(raw[m], ring[m % WIDTH]);
+    for (int m = 0; m < WIDTH - 1; ++m) widen2(raw[m], ring[m % WIDTH]);
 #pragma unroll
     for (int i = 0; i < RUN; ++i) {
-      widen4(raw[i + WIDTH - 1], ring[(i + WIDTH - 1) % WIDTH]);
+      widen2(raw[i + WIDTH - 1], ring[(i + WIDTH - 1) % WIDTH]);
       const double* win[WIDTH];
 #pragma unroll
       for (int j = 0; j < WIDTH; ++j) win[j] = ring[(i + j) % WIDTH];
@@ -229,7 +214,7 @@ __device__ __forceinline__ void conv_block(int lin, int nblocks, const ConvArgs&
 #pragma unroll
       for (int j = 0; j < WIDTH; ++j) {
         const int src = r - (WIDTH - 1) + j;
-        widen4(src >= start ? load8(xc + static_cast<int64_t>(src) * x_row) : make_uint2(0u, 0u), xw[j]);
+        widen2(src >= start ? load4(xc + static_cast<int64_t>(src) * x_row) : 0u, xw[j]);
       }
       const double* win[WIDTH];
 #pragma unroll
@@ -250,10 +235,11 @@ __global__ __launch_bounds__(kThreads) void packed_conv_kernel(ConvArgs args) {
 // so every conv block keeps its XCD) run the projection of 16 tokens each with
 // 4 wavefronts taking two hidden-dimension parts apiece, and the rest run
 // exactly the conv's blocks.  The projection's bits equal fd_gate_proj_fwd's.
-// The register budget is held to the conv kernel's own occupancy (5-6
-// wavefronts per SIMD), which the projection body would otherwise lower.
+// The register budget asks for the conv kernel's own occupancy (8 wavefronts
+// per SIMD), which the projection body would otherwise lower; with 24 or 32
+// gate heads the body needs more registers and the launch runs 6 or 4.
 template <int WIDTH, int RUN, typename LT, typename BT, int NB>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) void conv_gate_kernel(ConvArgs conv, fd_gate::GateProjArgs gate,
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8))) void conv_gate_kernel(ConvArgs conv, fd_gate::GateProjArgs gate,
                                                              int gate_blocks) {
   __shared__ fd_gate::PartSmem<NB> part;
   const int b = blockIdx.x;
@@ -323,14 +309,13 @@ int launch_run(const char* who, const void* x, int64_t x_row, const void* w, con
   return fd_check_launch(who);
 }
 
-// Tokens per thread: 8 measured fastest (89 VGPRs, 5 wavefronts per SIMD; B=1,
-// T=2048, C=6144 launches 6 per SIMD): 4 was 3 % slower, 16 4 % slower, 2 28 %
-// slower.  Held to 80 VGPRs for 6 per SIMD, the kernel spilled and took 21.0
-// against 15.0 us.
+// Tokens per thread: 8 measured fastest with 2 channels per thread (B=1,
+// T=2048, C=6144: 13.6 us, 12,288 wavefronts at 8 per SIMD); 16 took 14.2 us
+// (one round, 6 per SIMD), 4 and 32 15.8 us, 12 and 24 22 us.
 // The fast path's arithmetic is about 17 VALU instructions per output: 4 fp64
 // fmas, 2 for the input widening (once per row), the fp64 -> fp32 rounding, 5
 // for the hardware SiLU and 4 for the tie-window test, one branch per output
-// for the exact fallback.  SQ_INSTS_VALU counts 21.8 per output over a whole
+// for the exact fallback.  SQ_INSTS_VALU counts 23.7 per output over a whole
 // launch at B=1, T=2048, C=6144 (addresses, packing and the run setup included).
 constexpr int kRun = 8;
 
