@@ -545,17 +545,20 @@ __global__ __launch_bounds__(256 * KSPLIT, 1) void gqa_fwd_kernel(GqaArgs a) {
           asm volatile("" : "+v"(l_run));
         }
       };
+      // All of the next tile's K operands are read before the chain: the
+      // compiler then waits once per tile for them (read one MFMA ahead, it
+      // waited at every MFMA for the read just issued); 38.6 -> 38.1 us at B=1.
       sn[0] = f32x16_t{};
-      bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(ktn + k_off(0, 0));
+      bf16x8_t kfa[kSteps];
+#pragma unroll
+      for (int kk = 0; kk < kSteps; ++kk) kfa[kk] = *reinterpret_cast<const bf16x8_t*>(ktn + k_off(0, kk));
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int kk = 0; kk < kSteps; ++kk) {
-        bf16x8_t kn = kf;
-        if (kk + 1 < kSteps) kn = *reinterpret_cast<const bf16x8_t*>(ktn + k_off(0, kk + 1));
-        sn[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sn[0], 0, 0, 0);
+        sn[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfa[kk], qf[kk], sn[0], 0, 0, 0);
 #pragma unroll
         for (int j = 0; j < kPer; ++j) piece(kk * kPer + j);
         __builtin_amdgcn_sched_barrier(0);
-        kf = kn;
       }
       const bool grow_any = __builtin_amdgcn_ballot_w64(grow) != 0;
       accumulate(BUF, pb, alpha, grow_any);
