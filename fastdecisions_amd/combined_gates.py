@@ -7,7 +7,9 @@ dt_bias) -> (decay, beta)`` over ``unpack_gate`` (ref: :6-16), and
 packed Gated-DeltaNet forward (``fastdecisions_amd.packed_conv._forward``)
 computes both gate projections and both transforms in one kernel,
 ``fastdecisions::gate_proj`` (8, 16, 24 or 32 heads, hidden a multiple of
-1024), whose rows do not depend on the token count; other head counts take
+128), whose rows do not depend on the token count and, with 16 heads, equal
+the eager in_proj_a / in_proj_b GEMMs' bit for bit (the kernel sums in the
+order hipBLASLt uses for a 16-output projection); other head counts take
 one GEMM and the ``unpack_gate`` kernel, as the reference does.  Reinvoke
 after changing the projection weights.  Any head count works (the reference
 requires two bias-free [16, 2048] projections).

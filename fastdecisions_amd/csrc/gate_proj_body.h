@@ -2,15 +2,19 @@
 // fd_gate_proj_fwd (gate_transform.hip) and fd_packed_conv_gate_fwd
 // (packed_conv.hip) share.
 //
-// One workgroup owns 16 tokens.  The hidden dimension is cut into kProjParts = 8
-// parts of hidden/8; part p accumulates all 2*heads outputs of its slice on
-// v_mfma_f32_16x16x32_bf16 (exact bf16 products, fp32 sums).  Lane l supplies
+// One workgroup owns 16 tokens.  Each output sums its hidden dimension in the
+// order hipBLASLt's bf16 GEMM uses for the eager in_proj_a / in_proj_b
+// projections (16 outputs, measured equal bit for bit on the MI355X at 1,024
+// to 5,008 tokens): kProjParts = 4 parts, part p taking the 32-wide slice
+// [128 j + 32 p, 128 j + 32 p + 32) of every 128-deep block j in turn, each
+// slice one v_mfma_f32_16x16x32_bf16 into the part's accumulator (exact bf16
+// products, fp32 sums); then ((p0 + p1) + p2) + p3.  Lane l supplies
 // A = x[row0 + l%16][k + 8(l/16) .. +7] and B = W[n0 + l%16][same k] (16-byte
 // loads); D[4(l/16)+r][l%16] is (token, output).  A workgroup of WAVES
 // wavefronts gives wavefront wv the parts wv, wv + WAVES, ...; the arithmetic of
 // every part is the same whatever WAVES is, so both launches produce the same
-// bits.  The 8 partial sums are added in part order through LDS and rounded to
-// bf16, the value a bf16 GEMM (F.linear) stores, then transformed:
+// bits, and no order depends on the token count.  The sum is rounded to bf16,
+// the value a bf16 GEMM (F.linear) stores, then transformed:
 //   g    = -exp(A_log) * softplus(a + dt_bias),  softplus(x) = x > 20 ? x : log1p(exp(x))
 //   beta = bf16(sigmoid(b)),                     sigmoid(x) = 1 / (1 + exp(-x))
 // in fp32 with the same library exp / log1p as PyTorch's elementwise kernels
@@ -23,7 +27,7 @@
 namespace fd_gate {
 
 constexpr int kProjRows = 16;
-constexpr int kProjParts = 8;
+constexpr int kProjParts = 4;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -69,29 +73,34 @@ __device__ __forceinline__ void gate_proj_rows(int64_t block, const GateProjArgs
   const int wv = tid >> 6;
   const int l = tid & 63;
   const int64_t xrow = min(row0 + (l & 15), a.rows - 1);  // rows past the end re-read the last one
-  const int kq = a.hidden / kProjParts;
+  const int nblk = a.hidden / 128;
 #pragma unroll
   for (int pp = 0; pp < kProjParts / WAVES; ++pp) {
     const int p = wv + pp * WAVES;
-    const uint16_t* xp = a.x + xrow * a.xs + p * kq + 8 * (l >> 4);
-    const uint16_t* wp = a.w + static_cast<int64_t>(l & 15) * a.hidden + p * kq + 8 * (l >> 4);
+    const uint16_t* xp = a.x + xrow * a.xs + 32 * p + 8 * (l >> 4);
+    const uint16_t* wp = a.w + static_cast<int64_t>(l & 15) * a.hidden + 32 * p + 8 * (l >> 4);
     f32x4_t acc[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4_t{};
-    for (int k = 0; k < kq; k += 128) {
+    for (int j0 = 0; j0 < nblk; j0 += 4) {
+      // the operands of four blocks are loaded before their MFMAs
       bf16x8_t av[4], bv[4][NB];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        av[s] = *reinterpret_cast<const bf16x8_t*>(xp + k + 32 * s);
+        const int j = j0 + s < nblk ? j0 + s : nblk - 1;
+        av[s] = *reinterpret_cast<const bf16x8_t*>(xp + 128 * j);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
-          bv[s][nb] = *reinterpret_cast<const bf16x8_t*>(wp + static_cast<int64_t>(16 * nb) * a.hidden + k + 32 * s);
+          bv[s][nb] = *reinterpret_cast<const bf16x8_t*>(wp + static_cast<int64_t>(16 * nb) * a.hidden + 128 * j);
       }
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
+      for (int s = 0; s < 4; ++s) {
+        if (j0 + s < nblk) {
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[s], bv[s][nb], acc[nb], 0, 0, 0);
+          for (int nb = 0; nb < NB; ++nb)
+            acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[s], bv[s][nb], acc[nb], 0, 0, 0);
+        }
+      }
     }
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
@@ -135,8 +144,8 @@ inline int gate_proj_check(const char* who, const void* x, int64_t x_row_stride,
   FD_REQUIRE(rows >= 0, FD_ERR_INVALID_ARGUMENT, "%s: rows must be >= 0", who);
   FD_REQUIRE(heads == 8 || heads == 16 || heads == 24 || heads == 32, FD_ERR_UNSUPPORTED,
              "%s: heads must be 8, 16, 24 or 32 (got %d)", who, heads);
-  FD_REQUIRE(hidden > 0 && hidden % (kProjParts * 128) == 0, FD_ERR_UNSUPPORTED,
-             "%s: hidden must be a positive multiple of %d (got %d)", who, kProjParts * 128, hidden);
+  FD_REQUIRE(hidden > 0 && hidden % 128 == 0, FD_ERR_UNSUPPORTED,
+             "%s: hidden must be a positive multiple of 128 (got %d)", who, hidden);
   FD_REQUIRE(x_row_stride >= hidden && x_row_stride % 8 == 0 && fd_aligned16(x) && fd_aligned16(weight),
              FD_ERR_ALIGNMENT, "%s: x rows and weight must be 16-byte aligned, row stride >= hidden", who);
   FD_REQUIRE((a_log_dtype == FD_DTYPE_BF16 || a_log_dtype == FD_DTYPE_F32) &&

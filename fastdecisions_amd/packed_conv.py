@@ -98,7 +98,7 @@ def _segments(kwargs):
 
 def _gate_proj_fits(self, hidden_states) -> bool:
     """Sizes the fused a|b projection + gate transform kernel takes."""
-    return (self.num_v_heads in (8, 16, 24, 32) and hidden_states.shape[-1] % 1024 == 0
+    return (self.num_v_heads in (8, 16, 24, 32) and hidden_states.shape[-1] % 128 == 0
             and hidden_states.stride(-1) == 1 and hidden_states.is_contiguous())
 
 

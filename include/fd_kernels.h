@@ -443,10 +443,14 @@ FD_API int fd_gate_transform_fwd(const void* a, const void* b, int64_t a_row_str
  *   g        [rows, heads] fp32, beta [rows, heads] bf16 (contiguous)
  *   ab       NULL or [rows, 2*heads] bf16: the a|b values the transform used
  *
- * Limits: heads in {8, 16, 24, 32}; hidden a multiple of 1024; x rows and
- * weight 16-byte aligned.  The fp32 sums run in a fixed order (8 hidden-
- * dimension parts added in order), so a and b can differ from another GEMM's
- * bf16 output by one bf16 ulp where the sum lies near a rounding boundary.
+ * Limits: heads in {8, 16, 24, 32}; hidden a multiple of 128; x rows and
+ * weight 16-byte aligned.  The fp32 sums run in one fixed order whatever the
+ * number of tokens: 4 parts, part p taking the 32-wide slice 128 j + 32 p of
+ * every 128-deep block j on one MFMA accumulator, then ((p0 + p1) + p2) + p3,
+ * the order hipBLASLt's bf16 GEMM uses for a 16-output projection on the
+ * MI355X.  With 16 heads a and b therefore equal the eager in_proj_a /
+ * in_proj_b outputs bit for bit; other GEMMs can differ by one bf16 ulp where
+ * a sum lies near a rounding boundary.
  */
 FD_API int fd_gate_proj_fwd(const void* x, int64_t x_row_stride, const void* weight, int hidden,
                             const void* a_log, int a_log_dtype, const void* dt_bias, int dt_bias_dtype,

@@ -243,7 +243,7 @@ def test_joined_launch_argument_errors():
         kw.get("hs", f), 2048, f, kw.get("hidden", 2048), f, 1, f, 1, f, f, kw.get("heads", 16), None)
     assert conv_gate(heads=12) == _lib.FD_ERR_UNSUPPORTED
     assert "heads must be" in _err(lib) and "fd_packed_conv_gate_fwd" in _err(lib)
-    assert conv_gate(hidden=1536) == _lib.FD_ERR_UNSUPPORTED
+    assert conv_gate(hidden=1000) == _lib.FD_ERR_UNSUPPORTED
     assert conv_gate(W=5) == _lib.FD_ERR_UNSUPPORTED
     assert conv_gate(hs=f + 8) == _lib.FD_ERR_ALIGNMENT
     assert conv_gate(B=0) == _lib.FD_OK  # no tokens: nothing to launch
