@@ -102,6 +102,19 @@ def _gate_proj_fits(self, hidden_states) -> bool:
             and hidden_states.stride(-1) == 1 and hidden_states.is_contiguous())
 
 
+def _eager_layout(query, key, value):
+    """q, k, v [B, T, H, D] as the views the eager layer hands transformers' delta rule: slices of
+    the [B, C, T] conv output transposed back.  The values are the same; the rule's l2norm of q and
+    k reduces over D in an order PyTorch picks from the layout, and only in this layout is it eager's."""
+    b, t = query.shape[:2]
+    mixed = torch.cat([query.reshape(b, t, -1), key.reshape(b, t, -1), value.reshape(b, t, -1)], dim=-1)
+    mixed = mixed.transpose(1, 2).contiguous().transpose(1, 2)
+    dk, dv = key.shape[2] * key.shape[3], value.shape[2] * value.shape[3]
+    q, k, v = torch.split(mixed, [dk, dk, dv], dim=-1)
+    return (q.reshape(b, t, -1, query.shape[3]), k.reshape(b, t, -1, key.shape[3]),
+            v.reshape(b, t, -1, value.shape[3]))
+
+
 def _forward(self, hidden_states, cache_params=None, attention_mask=None, **kwargs):
     # The original method owns caches, training and other geometries (ref: src/decider/packed_conv.py:25-38).
     if (cache_params is not None or self.training or torch.is_grad_enabled()
@@ -168,6 +181,8 @@ def _forward(self, hidden_states, cache_params=None, attention_mask=None, **kwar
                                               float(self.norm.variance_epsilon), cu_seqlens)
         return self.out_proj(core_attn_out.reshape(batch, seq, -1))
     segments = None if getattr(self, "_fd_gated_delta", False) else _segments(kwargs)
+    if not getattr(self, "_fd_gated_delta", False):
+        query, key, value = _eager_layout(query, key, value)
     if getattr(self, "_fd_gated_delta", False):
         from .gated_delta import gated_delta_rule
         core_attn_out = gated_delta_rule(query, key, value, g, beta, cu_seqlens)

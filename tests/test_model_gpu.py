@@ -102,6 +102,42 @@ def test_config4_decisions_identical(full_model):
         _uninstall(full_model)
 
 
+def test_everything_but_attention_and_delta_rule_reproduces_eager(full_model):
+    """Every HIP kernel installed except the GQA attention (with its prologue and gated store) and
+    the chunked delta rule: the forward's logits equal the eager reference path's bit for bit on
+    config-4 requests.  The conv (torch's fp32 GPU conv + SiLU), every RMSNorm (PyTorch's row-mean
+    order), the a|b gate projection (hipBLASLt's order for the 16-output projections) and its
+    transform, the gated norm, SiLU*mul and the combined projections (whose concatenated GEMMs give
+    each part the separate GEMM's bits at these shapes) reproduce the eager ops exactly; only the
+    attention and the delta rule compute in another order."""
+    from fastdecisions_amd.combined_gates import install_combined_gates, install_combined_projections
+    from fastdecisions_amd.layer_fusions import install_gated_norm, install_mlp_fusion
+    from fastdecisions_amd.packed_conv import install_packed_conv
+    from fastdecisions_amd.persistent_residual_rms import install_persistent_residual_rms
+    from fastdecisions_amd.workloads import config4_request
+    reqs = [config4_request(full_model.shape.vocab_size, seed=s) for s in (1, 2, 3)]
+    announce("eager forward of 3 config-4 requests")
+    with torch.no_grad():
+        ref = [full_model(r.ids[None].cuda()) for r in reqs]
+    core = full_model.core
+    install_packed_conv(core)
+    install_persistent_residual_rms(core, all_layers=True)
+    install_combined_gates(core)
+    install_gated_norm(core)
+    install_combined_projections(core)
+    install_mlp_fusion(core)
+    try:
+        announce("HIP forward without the attention and delta-rule kernels")
+        with torch.no_grad():
+            got = [full_model(r.ids[None].cuda()) for r in reqs]
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(got, ref)):
+            print(f"request {i}: largest logit difference {(a.float() - b.float()).abs().max().item():.3g}")
+            assert torch.equal(a, b), i
+    finally:
+        _uninstall(full_model)
+
+
 def test_config5_packed_varlen_decisions_identical(full_model):
     from oracle import cpu as oracle
     from fastdecisions_amd.model import install_hip_kernels
