@@ -36,6 +36,7 @@ CASES = [
     (2, 37, 1024, 1024, 1024, 8, torch.float32, False, None),
     (1, 300, 1024, 2048, 3072, 32, torch.bfloat16, True, [0, 100, 170, 300]),
     (1, 129, 512, 512, 2048, 24, torch.float32, False, [0, 1, 64, 129]),
+    (1, 77, 512, 512, 896, 16, torch.bfloat16, False, None),  # hidden 7 x 128: a partial group of blocks
 ]
 
 

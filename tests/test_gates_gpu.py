@@ -106,6 +106,7 @@ def test_wrapper_rejects_bad_inputs():
     (1, 2048, 16, 2048, torch.bfloat16),   # the decider's layer
     (2, 37, 8, 1024, torch.float32),       # ragged token count (tail workgroup), fp32 parameters
     (1, 100, 32, 3072, torch.bfloat16),
+    (1, 50, 16, 640, torch.bfloat16),      # 5 blocks of 128: the last group of four is partial
 ])
 def test_fused_projection_vs_float64_and_hipblaslt(oracle, B, T, H, hidden, pdt):
     """fd_gate_proj_fwd: the a|b projection against the float64 dot product, under the bound any
