@@ -137,16 +137,36 @@ __device__ __forceinline__ uint4 pack8(const float* x) {
 // values each): x*x rounded to bf16, summed in fp32 (lane chunk order, then an
 // xor butterfly over the 16 lanes), the sum, sum + eps and 1/sqrt each rounded
 // to bf16, then x * inv rounded to bf16.  Every lane of the wavefront must call it.
+// The value of lane i ^ m (m = 1, 2, 4, 8) inside i's row of 16 lanes, by DPP (no
+// LDS round trip).  row_ror:n gives lane i the value of lane (i - n) mod 16, so
+// ror 8 is i ^ 8, and i ^ 4 is ror 4 where bit 2 of i is set and ror 12 elsewhere.
+template <int M>
+__device__ __forceinline__ float row16_xor(float v) {
+  const int b = __builtin_bit_cast(int, v);
+  if constexpr (M == 1) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+  } else if constexpr (M == 2) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+  } else if constexpr (M == 4) {
+    const int r4 = __builtin_amdgcn_mov_dpp(b, 0x124, 0xF, 0xF, false);   // row_ror:4
+    const int r12 = __builtin_amdgcn_mov_dpp(b, 0x12C, 0xF, 0xF, false);  // row_ror:12
+    return __builtin_bit_cast(float, (threadIdx.x & 4) ? r4 : r12);
+  } else {
+    static_assert(M == 8, "xor distance within a row of 16 lanes");
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false));  // row_ror:8
+  }
+}
+
 __device__ __forceinline__ uint4 l2norm_row8(uint4 raw) {
   float x[8];
   unpack8(raw, x);
   float s = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) s = s + bf16r(x[e] * x[e]);
-  s = s + __shfl_xor(s, 8);
-  s = s + __shfl_xor(s, 4);
-  s = s + __shfl_xor(s, 2);
-  s = s + __shfl_xor(s, 1);
+  s = s + row16_xor<8>(s);
+  s = s + row16_xor<4>(s);
+  s = s + row16_xor<2>(s);
+  s = s + row16_xor<1>(s);
   const float e = bf16r(bf16r(s) + 1e-6f);
   const float inv = bf16r(1.0f / __builtin_sqrtf(e));
   float y[8];
@@ -245,11 +265,32 @@ __device__ __forceinline__ int aq_index(int i, int j) {
   return (((i >> 4) * 2 + (j >> 5)) * 64 + 16 * ((j & 31) >> 3) + (i & 15)) * 8 + (j & 7);
 }
 
+// Inside a 16-row block the solve reads row m of the transposed L tile in 4-wide
+// pieces starting at (m + 1) & ~3, for m = 0..14: 36 reads, piece k at (tri_m(k), tri_i0(k)).
+constexpr int kTriReads = 36;
+template <int N>
+struct IntC {
+  static constexpr int value = N;
+};
+constexpr int kTriWin = 8;
+// rows 0-2 have 4 pieces, rows 3-6 three, rows 7-10 two, rows 11-14 one
+constexpr int tri_m(int k) {
+  return k < 12 ? k / 4 : k < 24 ? 3 + (k - 12) / 3 : k < 32 ? 7 + (k - 24) / 2 : 11 + (k - 32);
+}
+constexpr int tri_i0(int k) {
+  return k < 12 ? 4 * (k % 4) : k < 24 ? 4 + 4 * ((k - 12) % 3) : k < 32 ? 8 + 4 * ((k - 24) % 2) : 12;
+}
+static_assert(tri_m(kTriReads - 1) == 14 && tri_i0(kTriReads - 1) == 12 && tri_m(11) == 2 && tri_i0(11) == 12 &&
+                  tri_m(12) == 3 && tri_i0(12) == 4 && tri_m(24) == 7 && tri_i0(25) == 12 && tri_m(32) == 11,
+              "36 pieces in the inner solve of a 16-row block");
+
 // One workgroup per (chunk, value head).  u = T (beta v) and w = T (beta e^gc k)
 // are the solutions of (I + L) x = rhs; thread j < 128 solves for column j of
 // u, thread 128 + j for column j of w, by forward substitution with the rows of
 // L read from LDS (every lane reads the same address: broadcast).
-__global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
+// BETA_F32: beta is fp32 (else bf16).
+template <bool BETA_F32>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void gd_prep_kernel(GdArgs a) {
   const int h = blockIdx.x % a.hv;
   const int c = blockIdx.x / a.hv;
   int r0, L;
@@ -277,6 +318,17 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
   const size_t qk_row = static_cast<size_t>(a.hk) * kD;
   const size_t v_row = static_cast<size_t>(a.hv) * kD;
   uint16_t* gq = a.qn + hc * kC * kD;
+  // g and beta of row l (padded rows carry g = beta = 0; wave 0 uses them), loaded
+  // first and by every wave, with no branch to convert in: wave 0 runs the cumsum
+  // below while the q, k, v rows are in flight
+  const size_t gidx = static_cast<size_t>(r0 + (l < L ? l : 0)) * a.hv + h;
+  const float graw = a.g[gidx];
+  float braw;
+  if constexpr (BETA_F32)
+    braw = static_cast<const float*>(a.beta)[gidx];
+  else
+    braw = fd_bf16_to_f32(static_cast<const uint16_t*>(a.beta)[gidx]);
+  __builtin_amdgcn_sched_barrier(0);
   // every load of the block is issued before any is used (rows past the chunk's
   // end re-read its first row and are zeroed below)
   uint4 rq[4], rk[4], rv[4];
@@ -288,14 +340,24 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
     rk[it] = *reinterpret_cast<const uint4*>(a.k + grow * qk_row + hk * kD + c16 * 8);
     rv[it] = *reinterpret_cast<const uint4*>(a.v + grow * v_row + h * kD + c16 * 8);
   }
-  // g and beta of row l (wave 0; padded rows carry g = beta = 0)
-  float gv = 0.0f, bv = 0.0f;
+  // g (inclusive cumsum over the chunk) and beta
   if (wv == 0) {
-    const size_t idx = static_cast<size_t>(r0 + (l < L ? l : 0)) * a.hv + h;
-    gv = a.g[idx];
-    bv = a.beta_f32 ? static_cast<const float*>(a.beta)[idx]
-                    : fd_bf16_to_f32(static_cast<const uint16_t*>(a.beta)[idx]);
-    if (l >= L) gv = bv = 0.0f;
+    float gv = l < L ? graw : 0.0f;
+    const float bv = l < L ? braw : 0.0f;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float up = __shfl_up(gv, off);
+      if (l >= off) gv = gv + up;
+    }
+    sG[l] = gv;
+    sB[l] = bv;
+    const float eg = expf(gv);
+    sBG[l] = bv * eg;
+    const float gl = __shfl(gv, kC - 1);
+    float* gx = a.gc + hc * 3 * kC;
+    gx[l] = eg;
+    gx[kC + l] = expf(gl - gv);
+    if (l == 0) gx[2 * kC] = expf(gl);
   }
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
@@ -312,23 +374,6 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
     *reinterpret_cast<uint4*>(sK + row * kRowK + c16 * 8) = k4;
     *reinterpret_cast<uint4*>(sV + row * kRowK + c16 * 8) = v4;
     *reinterpret_cast<uint4*>(gq + (((row >> 4) * 4 + (c16 >> 2)) * 64 + 16 * (c16 & 3) + (row & 15)) * 8) = q4;
-  }
-  // g (inclusive cumsum over the chunk) and beta
-  if (wv == 0) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float up = __shfl_up(gv, off);
-      if (l >= off) gv = gv + up;
-    }
-    sG[l] = gv;
-    sB[l] = bv;
-    const float eg = expf(gv);
-    sBG[l] = bv * eg;
-    const float gl = __shfl(gv, kC - 1);
-    float* gx = a.gc + hc * 3 * kC;
-    gx[l] = eg;
-    gx[kC + l] = expf(gl - gv);
-    if (l == 0) gx[2 * kC] = expf(gl);
   }
   __syncthreads();
 
@@ -350,11 +395,21 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
     }
     const int j = 32 * J + (l & 31);
     const float gj = sG[j];
+    // gc and beta of the lane's 16 rows 32I + 8q + 4(l/32) + e, read before any is
+    // used, and the decays computed for every row and then selected: a branch per
+    // row would serialise the 16 LDS round trips
+    f32x4_t gi[4], bi[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      gi[q] = *reinterpret_cast<const f32x4_t*>(sG + 32 * I + 8 * q + 4 * (l >> 5));
+      bi[q] = *reinterpret_cast<const f32x4_t*>(sB + 32 * I + 8 * q + 4 * (l >> 5));
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int i = 32 * I + (r >> 2) * 8 + (l >> 5) * 4 + (r & 3);
-      const float dec = i >= j ? expf(sG[i] - gj) : 0.0f;
-      sL[j * kRowF + i] = i > j ? (sB[i] * accG[r]) * dec : 0.0f;  // transposed: sL[j][i] = L[i][j]
+      const float e = expf(gi[r >> 2][r & 3] - gj);
+      const float dec = i >= j ? e : 0.0f;
+      sL[j * kRowF + i] = i > j ? (bi[r >> 2][r & 3] * accG[r]) * dec : 0.0f;  // transposed: sL[j][i] = L[i][j]
       gaq[aq_index(i, j)] = i >= j ? (a.scale * accA[r]) * dec : 0.0f;
     }
   } else {
@@ -385,23 +440,49 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
       kbits[i >> 1] = bits;
     x[i] = (is_w ? sBG[i] : sB[i]) * fd_bf16_to_f32(bits);
   }
+  if (is_w) {
+    // normalised k^T in the state pass's operand order: row dk = j, the 8 tokens
+    // 32st + 8g4 .. +7 of lane 16g4 + (j % 16) (16 lanes write 256 B contiguous);
+    // stored before the substitution so that its registers are free there
+    uint16_t* kt = a.kn + hc * kC * kD;
+    const int kwv = j >> 5, km = (j >> 4) & 1, kc16 = j & 15;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int i = 4 * (4 * st + g);  // kbits index of token 32st + 8g
+        *reinterpret_cast<uint4*>(kt + ((((kwv * 2 + km) * 2 + st) * 64) + 16 * g + kc16) * 8) =
+            make_uint4(kbits[i], kbits[i + 1], kbits[i + 2], kbits[i + 3]);
+      }
+  }
   __syncthreads();  // every wave has read its right-hand sides: the q/k/v tiles are free
   float* wl = reinterpret_cast<float*>(smem) + wv * (48 * 64);  // 12 KiB per wave
   uint16_t* gw = a.w + hc * 3 * kC * kD;
   float* gu = a.u + hc * kC * kD;
+  // the four blocks, each with its block index a compile-time constant (a loop
+  // this size is beyond the unroller's limit)
+  auto block = [&](auto bc) __attribute__((always_inline)) {
+    constexpr int b = decltype(bc)::value;
+    constexpr int b0 = 16 * b;
+    // the block's 36 reads of L pieces pass through a window of kTriWin registers,
+    // each issued kTriWin steps before its FMAs, so the LDS latency is not paid per
+    // read (x[i] still takes its updates in increasing m)
+    f32x4_t lwin[kTriWin];
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const int b0 = 16 * b;
+    for (int k = 0; k < kTriWin; ++k)
+      lwin[k] = *reinterpret_cast<const f32x4_t*>(sL + (b0 + tri_m(k)) * kRowF + b0 + tri_i0(k));
 #pragma unroll
-    for (int m = b0; m < b0 + 15; ++m) {
+    for (int k = 0; k < kTriReads; ++k) {
+      const int m = b0 + tri_m(k), i0 = b0 + tri_i0(k);
+      const f32x4_t lv = lwin[k % kTriWin];
       const float xm = x[m];
 #pragma unroll
-      for (int i0 = (m + 1) & ~3; i0 < b0 + 16; i0 += 4) {
-        const f32x4_t lv = *reinterpret_cast<const f32x4_t*>(sL + m * kRowF + i0);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (i0 + e > m) x[i0 + e] = fmaf(-lv[e], xm, x[i0 + e]);
-      }
+      for (int e = 0; e < 4; ++e)
+        if (i0 + e > m) x[i0 + e] = fmaf(-lv[e], xm, x[i0 + e]);
+      if (k + kTriWin < kTriReads)
+        lwin[k % kTriWin] = *reinterpret_cast<const f32x4_t*>(sL + (b0 + tri_m(k + kTriWin)) * kRowF + b0 +
+                                                               tri_i0(k + kTriWin));
+      __builtin_amdgcn_sched_barrier(0);
     }
     // X_block (16 rows of the wave's 64 columns) -> LDS [16][64]
 #pragma unroll
@@ -437,7 +518,7 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
         *reinterpret_cast<f32x4_t*>(gu + q * 4) = v;
       }
     }
-    if (b == 3) break;
+    if constexpr (b == 3) return;
     // C[rest rows][64 columns] = L[rest, block] X_block: rest row tile rt (16 rows), column tile t
     constexpr int kMaxRt = 3;
     const int nrt = 3 - b;
@@ -471,21 +552,11 @@ __global__ __launch_bounds__(kThreads) void gd_prep_kernel(GdArgs a) {
     }
 #pragma unroll
     for (int i = b0 + 16; i < kC; ++i) x[i] = x[i] - wl[(i - b0 - 16) * 64 + l];
-  }
-  if (is_w) {
-    // normalised k^T in the state pass's operand order: row dk = j, the 8 tokens
-    // 32st + 8g4 .. +7 of lane 16g4 + (j % 16) (16 lanes write 256 B contiguous)
-    uint16_t* kt = a.kn + hc * kC * kD;
-    const int kwv = j >> 5, km = (j >> 4) & 1, kc16 = j & 15;
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int i = 4 * (4 * st + g);  // kbits index of token 32st + 8g
-        *reinterpret_cast<uint4*>(kt + ((((kwv * 2 + km) * 2 + st) * 64) + 16 * g + kc16) * 8) =
-            make_uint4(kbits[i], kbits[i + 1], kbits[i + 2], kbits[i + 3]);
-      }
-  }
+  };
+  block(IntC<0>{});
+  block(IntC<1>{});
+  block(IntC<2>{});
+  block(IntC<3>{});
 }
 
 // ---------------------------------------------------------------------------
@@ -933,7 +1004,10 @@ int gd_run(const void* q, const void* k, const void* v, const float* g, const vo
     hipLaunchKernelGGL(gd_chunk_table, dim3(1), dim3(kThreads), 0, s, cu_seqlens, a.nseq, seq_len,
                        static_cast<int>(total), a);
   if (nc > 0) {
-    hipLaunchKernelGGL(gd_prep_kernel, dim3(static_cast<unsigned>(nc * v_heads)), dim3(kThreads), 0, s, a);
+    if (a.beta_f32)
+      hipLaunchKernelGGL(gd_prep_kernel<true>, dim3(static_cast<unsigned>(nc * v_heads)), dim3(kThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL(gd_prep_kernel<false>, dim3(static_cast<unsigned>(nc * v_heads)), dim3(kThreads), 0, s, a);
   }
   hipLaunchKernelGGL(gd_state_kernel, dim3(static_cast<unsigned>(nseq * v_heads * kSlices)), dim3(kStateThreads), 0,
                      s, a);
