@@ -151,8 +151,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void add_rmsnorm_kernel(
               make_uint4(hw[i][0], hw[i][1], hw[i][2], hw[i][3]);
       }
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_xor(s, off, 64);
+    s = fd_xor_sum_down<64>(s);
 
     const float mean = s * (1.0f / static_cast<float>(width));
     const float inv = inv_rms(mean + eps);
@@ -261,8 +260,7 @@ __global__ __launch_bounds__(128) void add_rmsnorm_pair_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[i] = acc[i] + h[j][i] * h[j][i];
     float s = ((acc[0] + acc[1]) + acc[2]) + acc[3];
-#pragma unroll
-    for (int off = 1; off <= 32; off <<= 1) s = s + __shfl_xor(s, off, 64);
+    s = fd_xor_sum_up<64>(s);
     const float mean = s * (1.0f / static_cast<float>(width));  // PyTorch's mean: the sum times fl(1 / width)
     const float inv = inv_rms(mean + eps);
     if (lane == 0) inv_s = inv;

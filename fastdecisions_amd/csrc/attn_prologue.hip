@@ -97,10 +97,7 @@ __global__ __launch_bounds__(kThreads) void attn_prologue_kernel(PrologueArgs a)
     sb = sb + x[4 + e] * x[4 + e];
   }
   float s = sa + sb;
-  s = s + __shfl_xor(s, 1);
-  s = s + __shfl_xor(s, 2);
-  s = s + __shfl_xor(s, 4);
-  s = s + __shfl_xor(s, 8);
+  s = fd_xor_sum_up<16>(s);
   // 1 / sqrt in fp64 (root and quotient), rounded to fp32: torch.rsqrt's value on every input measured
   const float inv =
       static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(s * (1.0f / static_cast<float>(kD)) + a.eps)));

@@ -51,6 +51,77 @@ __device__ __forceinline__ uint32_t fd_pack2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
+// The value of lane i and of lane i ^ M (M = 1 .. 32, a power of two) as a pair,
+// with no LDS round trip: DPP inside each row of 16 lanes for M <= 8 (row_ror:n
+// gives lane i the value of lane (i - n) mod 16, so ror 8 is i ^ 8, and i ^ 4 is
+// ror 4 where bit 2 of i is set and ror 12 elsewhere), v_permlane16_swap /
+// v_permlane32_swap across rows (with the value in both operands each lane
+// receives its own value and its partner's, in an order that depends on the
+// lane).  The sum and max below are symmetric in the pair, so they equal
+// s + __shfl_xor(s, M) and fmaxf(s, __shfl_xor(s, M)) bit for bit.  Every lane of
+// the wavefront must take part.
+template <int M>
+__device__ __forceinline__ void fd_xor_pair(float s, float& a, float& b) {
+  const uint32_t u = __float_as_uint(s);
+  if constexpr (M == 32 || M == 16) {
+    auto r = M == 32 ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
+                     : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  } else {
+    int p;
+    if constexpr (M == 1) {
+      p = __builtin_amdgcn_mov_dpp(static_cast<int>(u), 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    } else if constexpr (M == 2) {
+      p = __builtin_amdgcn_mov_dpp(static_cast<int>(u), 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    } else if constexpr (M == 4) {
+      const int r4 = __builtin_amdgcn_mov_dpp(static_cast<int>(u), 0x124, 0xF, 0xF, false);   // row_ror:4
+      const int r12 = __builtin_amdgcn_mov_dpp(static_cast<int>(u), 0x12C, 0xF, 0xF, false);  // row_ror:12
+      p = (threadIdx.x & 4) ? r4 : r12;
+    } else {
+      static_assert(M == 8, "xor distance: a power of two below 64");
+      p = __builtin_amdgcn_mov_dpp(static_cast<int>(u), 0x128, 0xF, 0xF, false);  // row_ror:8
+    }
+    a = s;
+    b = __uint_as_float(static_cast<uint32_t>(p));
+  }
+}
+template <int M>
+__device__ __forceinline__ float fd_xor_sum(float s) {
+  float a, b;
+  fd_xor_pair<M>(s, a, b);
+  return a + b;
+}
+template <int M>
+__device__ __forceinline__ float fd_xor_max(float s) {
+  float a, b;
+  fd_xor_pair<M>(s, a, b);
+  return fmaxf(a, b);
+}
+
+// s summed over each aligned group of N lanes (N = 2 .. 64) by an xor butterfly
+// with distances 1, 2, .., N/2 (up) or N/2, .., 1 (down).
+template <int N>
+__device__ __forceinline__ float fd_xor_sum_up(float s) {
+  if constexpr (N >= 2) s = fd_xor_sum<1>(s);
+  if constexpr (N >= 4) s = fd_xor_sum<2>(s);
+  if constexpr (N >= 8) s = fd_xor_sum<4>(s);
+  if constexpr (N >= 16) s = fd_xor_sum<8>(s);
+  if constexpr (N >= 32) s = fd_xor_sum<16>(s);
+  if constexpr (N >= 64) s = fd_xor_sum<32>(s);
+  return s;
+}
+template <int N>
+__device__ __forceinline__ float fd_xor_sum_down(float s) {
+  if constexpr (N >= 64) s = fd_xor_sum<32>(s);
+  if constexpr (N >= 32) s = fd_xor_sum<16>(s);
+  if constexpr (N >= 16) s = fd_xor_sum<8>(s);
+  if constexpr (N >= 8) s = fd_xor_sum<4>(s);
+  if constexpr (N >= 4) s = fd_xor_sum<2>(s);
+  if constexpr (N >= 2) s = fd_xor_sum<1>(s);
+  return s;
+}
+
 // SiLU exactly as PyTorch's GPU kernel evaluates it in fp32: y / (1 + expf(-y))
 // with the device expf and the correctly rounded IEEE division (no fast-math).
 // Measured on the MI355X: torch.nn.functional.silu on fp32 equals this

@@ -137,36 +137,13 @@ __device__ __forceinline__ uint4 pack8(const float* x) {
 // values each): x*x rounded to bf16, summed in fp32 (lane chunk order, then an
 // xor butterfly over the 16 lanes), the sum, sum + eps and 1/sqrt each rounded
 // to bf16, then x * inv rounded to bf16.  Every lane of the wavefront must call it.
-// The value of lane i ^ m (m = 1, 2, 4, 8) inside i's row of 16 lanes, by DPP (no
-// LDS round trip).  row_ror:n gives lane i the value of lane (i - n) mod 16, so
-// ror 8 is i ^ 8, and i ^ 4 is ror 4 where bit 2 of i is set and ror 12 elsewhere.
-template <int M>
-__device__ __forceinline__ float row16_xor(float v) {
-  const int b = __builtin_bit_cast(int, v);
-  if constexpr (M == 1) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
-  } else if constexpr (M == 2) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
-  } else if constexpr (M == 4) {
-    const int r4 = __builtin_amdgcn_mov_dpp(b, 0x124, 0xF, 0xF, false);   // row_ror:4
-    const int r12 = __builtin_amdgcn_mov_dpp(b, 0x12C, 0xF, 0xF, false);  // row_ror:12
-    return __builtin_bit_cast(float, (threadIdx.x & 4) ? r4 : r12);
-  } else {
-    static_assert(M == 8, "xor distance within a row of 16 lanes");
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false));  // row_ror:8
-  }
-}
-
 __device__ __forceinline__ uint4 l2norm_row8(uint4 raw) {
   float x[8];
   unpack8(raw, x);
   float s = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) s = s + bf16r(x[e] * x[e]);
-  s = s + row16_xor<8>(s);
-  s = s + row16_xor<4>(s);
-  s = s + row16_xor<2>(s);
-  s = s + row16_xor<1>(s);
+  s = fd_xor_sum_down<16>(s);
   const float e = bf16r(bf16r(s) + 1e-6f);
   const float inv = bf16r(1.0f / __builtin_sqrtf(e));
   float y[8];

@@ -93,8 +93,7 @@ __global__ __launch_bounds__(kThreads) void gated_rmsnorm_kernel(const uint16_t*
     sb = sb + xv[4 + e] * xv[4 + e];
   }
   float s = sa + sb;
-#pragma unroll
-  for (int off = 1; off < LANES; off <<= 1) s = s + __shfl_xor(s, off);
+  s = fd_xor_sum_up<LANES>(s);
   // 1 / sqrt in fp64 (root and quotient), rounded to fp32: torch.rsqrt's value on every input measured
   const float inv = static_cast<float>(
       1.0 / __builtin_sqrt(static_cast<double>(s * (1.0f / static_cast<float>(kWidth)) + eps)));

@@ -40,8 +40,7 @@ struct SlotArgs {
 __device__ __forceinline__ float bf16r(float x) { return fd_lo(fd_pack2(x, 0.0f)); }
 
 __device__ __forceinline__ float wave_sum(float s) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_xor(s, off);
+  s = fd_xor_sum_down<64>(s);
   return s;
 }
 
@@ -83,8 +82,7 @@ __global__ __launch_bounds__(kThreads) void slot_readout_kernel(SlotArgs a) {
         acc[3] = acc[3] + v.w * v.w;
       }
       float s = ((acc[0] + acc[1]) + acc[2]) + acc[3];
-#pragma unroll
-      for (int off = 1; off <= 32; off <<= 1) s = s + __shfl_xor(s, off);
+      s = fd_xor_sum_up<64>(s);
       if (l == 0) red[0] = s;
     }
   } else {
@@ -142,8 +140,12 @@ __global__ __launch_bounds__(kThreads) void slot_readout_kernel(SlotArgs a) {
     const int nopt = a.nopts ? min(max(a.nopts[n], 0), a.K) : a.K;
     float m = -__builtin_inff();
     for (int k = l; k < nopt; k += 64) m = fmaxf(m, sl[k] / a.temp);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    m = fd_xor_max<32>(m);
+    m = fd_xor_max<16>(m);
+    m = fd_xor_max<8>(m);
+    m = fd_xor_max<4>(m);
+    m = fd_xor_max<2>(m);
+    m = fd_xor_max<1>(m);
     float sum = 0.0f;
     for (int k = l; k < nopt; k += 64) sum += expf(sl[k] / a.temp - m);
     sum = wave_sum(sum);
