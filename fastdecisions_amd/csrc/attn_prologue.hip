@@ -20,6 +20,8 @@
 //   lane: a = ((x0^2 + x1^2) + x2^2) + x3^2, b = the same over x4..x7, s = a + b
 //   group: s += shfl_xor(s, 1, 2, 4, 8)
 //   inv = fp32(1 / sqrt(s / 128 + eps)) from the fp64 root and quotient;  y = bf16((x * inv) * g),  g = 1 + w or w
+#include <type_traits>
+
 #include "fd_common.h"
 
 namespace {
@@ -131,10 +133,24 @@ __global__ __launch_bounds__(kThreads) void attn_prologue_kernel(PrologueArgs a)
   }
   if (a.rot > 0) {
     // partner lane holds the other half of the rotated features (rot/16 lanes apart)
-    const int half_lanes = a.rot >> 4;
+    const int half_lanes = a.rot >> 4;  // 1, 2, 4 or 8: inside the 16-lane row, on DPP
     float p[8];
+    auto partners = [&](auto mc) {
+      constexpr int kM = decltype(mc)::value;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(y[e], half_lanes);
+      for (int e = 0; e < 8; ++e) {
+        float own;
+        fd_xor_pair<kM>(y[e], own, p[e]);
+      }
+    };
+    if (half_lanes == 1)
+      partners(std::integral_constant<int, 1>{});
+    else if (half_lanes == 2)
+      partners(std::integral_constant<int, 2>{});
+    else if (half_lanes == 4)
+      partners(std::integral_constant<int, 4>{});
+    else
+      partners(std::integral_constant<int, 8>{});
     if (rot_lane) {
       const bool first_half = ln < half_lanes;
       const uint32_t cw[4] = {cr.x, cr.y, cr.z, cr.w};
