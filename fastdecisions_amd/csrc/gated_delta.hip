@@ -44,6 +44,7 @@
 // lane layout (v_mfma_f32_16x16x32_bf16): lane l supplies A[l%16][8(l/16)+j]
 // and B[8(l/16)+j][l%16] for j = 0..7 of each 32-step; D[4(l/16)+r][l%16].
 #include <mutex>
+#include <type_traits>
 
 #include "fd_common.h"
 
@@ -245,10 +246,6 @@ __device__ __forceinline__ int aq_index(int i, int j) {
 // Inside a 16-row block the solve reads row m of the transposed L tile in 4-wide
 // pieces starting at (m + 1) & ~3, for m = 0..14: 36 reads, piece k at (tri_m(k), tri_i0(k)).
 constexpr int kTriReads = 36;
-template <int N>
-struct IntC {
-  static constexpr int value = N;
-};
 constexpr int kTriWin = 8;
 // rows 0-2 have 4 pieces, rows 3-6 three, rows 7-10 two, rows 11-14 one
 constexpr int tri_m(int k) {
@@ -530,10 +527,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
     for (int i = b0 + 16; i < kC; ++i) x[i] = x[i] - wl[(i - b0 - 16) * 64 + l];
   };
-  block(IntC<0>{});
-  block(IntC<1>{});
-  block(IntC<2>{});
-  block(IntC<3>{});
+  block(std::integral_constant<int, 0>{});
+  block(std::integral_constant<int, 1>{});
+  block(std::integral_constant<int, 2>{});
+  block(std::integral_constant<int, 3>{});
 }
 
 // ---------------------------------------------------------------------------
