@@ -132,3 +132,28 @@ def test_split_mlp_matches_eager_mlp():
           f"eager max {e_eager.max().item():.3e} rms {e_eager.pow(2).mean().sqrt().item():.3e}")
     assert e_ours.max() <= 1.5 * e_eager.max()
     assert e_ours.pow(2).mean() <= 1.1 ** 2 * e_eager.pow(2).mean()
+
+
+@pytest.mark.parametrize("width", [64, 256])
+def test_gated_rmsnorm_other_widths_vs_eager_on_gpu(width):
+    """Widths 64 and 256 run 8 and 32 lanes per row (the 32-lane butterfly crosses
+    16-lane rows); both sum in PyTorch's order for the width, so the rows equal
+    eager Qwen3_5RMSNormGated bit for bit, as at 128."""
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as mq
+    from fastdecisions_amd.gated_norm_kernel import gated_rms_norm
+    gen = torch.Generator().manual_seed(40 + width)
+    rows, heads = 4096, 8
+    x = (torch.randn((rows, width), generator=gen) * 0.3).to(torch.bfloat16).cuda()
+    zfull = torch.randn((rows // heads, heads, 2 * width), generator=gen).to(torch.bfloat16).cuda()
+    z = zfull[..., :width]
+    norm = mq.Qwen3_5RMSNormGated(width, eps=1e-6).cuda()
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.02 * torch.randn(width, generator=gen).cuda())
+    norm = norm.to(torch.bfloat16)
+    announce(f"gated rmsnorm width {width} vs eager")
+    with torch.no_grad():
+        ours, eager = gated_rms_norm(x, z, norm.weight.data, 1e-6), norm(x, z.reshape(-1, width))
+    torch.cuda.synchronize()
+    u = ulp_diff(to_bits(ours), to_bits(eager))
+    print(f"gated norm width {width} vs eager: max ulp {u.max()}, identical {(u == 0).mean():.5f}")
+    assert u.max() == 0
