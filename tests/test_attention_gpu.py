@@ -87,3 +87,32 @@ def test_gated_store_equals_eager_gate(varlen):
     torch.cuda.synchronize()
     assert gated.stride() == plain.stride()
     assert torch.equal(gated, eager)
+
+
+@pytest.mark.parametrize("rot", [16, 64, 128])
+def test_prologue_other_rotary_dims(oracle, rot):
+    """Rotary dims 16, 64 and 128 put a row's rotation partner 1, 4 and 8 lanes
+    away (the decider's 32: 2); bit-exact vs the oracle and the eager ops."""
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as mq
+    from fastdecisions_amd.attention_prologue_kernel import attention_prologue
+    gen = torch.Generator().manual_seed(60 + rot)
+    T = 96
+    q = torch.randn((1, T, 16, 128), generator=gen).to(torch.bfloat16).cuda()
+    k = torch.randn((1, T, 4, 128), generator=gen).to(torch.bfloat16).cuda()
+    cos = (torch.rand((1, T, rot), generator=gen) * 2 - 1).to(torch.bfloat16).cuda()
+    sin = (torch.rand((1, T, rot), generator=gen) * 2 - 1).to(torch.bfloat16).cuda()
+    qn = mq.Qwen3_5RMSNorm(128).cuda()
+    kn = mq.Qwen3_5RMSNorm(128).cuda()
+    with torch.no_grad():
+        qn.weight.copy_(torch.randn(128, generator=gen).cuda() * 0.05)
+        kn.weight.copy_(torch.randn(128, generator=gen).cuda() * 0.05)
+    qn, kn = qn.to(torch.bfloat16), kn.to(torch.bfloat16)
+    announce(f"attention prologue rotary dim {rot}")
+    qo, ko = attention_prologue(q, k, qn.weight.data, kn.weight.data, cos, sin, 1e-6)
+    with torch.no_grad():
+        qe, ke = mq.apply_rotary_pos_emb(qn(q).transpose(1, 2), kn(k).transpose(1, 2), cos, sin)
+    torch.cuda.synchronize()
+    cb, sb = to_bits(cos), to_bits(sin)
+    assert np.array_equal(to_bits(qo), oracle.attn_prologue(to_bits(q), to_bits(qn.weight.data), cb, sb))
+    assert np.array_equal(to_bits(ko), oracle.attn_prologue(to_bits(k), to_bits(kn.weight.data), cb, sb))
+    assert torch.equal(qo, qe.transpose(1, 2)) and torch.equal(ko, ke.transpose(1, 2))
