@@ -59,7 +59,8 @@ __device__ __forceinline__ uint32_t fd_pack2(float lo, float hi) {
 // receives its own value and its partner's, in an order that depends on the
 // lane).  The sum and max below are symmetric in the pair, so they equal
 // s + __shfl_xor(s, M) and fmaxf(s, __shfl_xor(s, M)) bit for bit.  Every lane of
-// the wavefront must take part.
+// the wavefront must take part, in a 1-D workgroup whose size is a multiple of 64
+// (the lane index is threadIdx.x % 64).
 template <int M>
 __device__ __forceinline__ void fd_xor_pair(float s, float& a, float& b) {
   const uint32_t u = __float_as_uint(s);
